@@ -1,0 +1,263 @@
+/*
+ * CPU oracle for the flint attention hot path. TEST INFRASTRUCTURE ONLY: see
+ * flint_oracle.h for who may use it, which reference lines each function
+ * restates, and which checks pin each function.
+ *
+ * Built with plain gcc -O2 and no -march flags, so float expressions are not
+ * contracted into FMAs; the order of float and double operations below follows
+ * /root/reference/src/ref/ref_model.cpp line by line so that results with fp32
+ * storage are bit-identical to the reference's own CPU forward.
+ */
+#include "flint_oracle.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ---- storage rounding (IEEE binary16 / bfloat16, round to nearest even) ---- */
+
+static float round_f16(float x) {
+    uint32_t u;
+    memcpy(&u, &x, 4);
+    const uint32_t sign = u & 0x80000000u, a = u & 0x7fffffffu;
+    if (a >= 0x7f800000u) return x; /* inf, nan */
+    const int e = (int)(a >> 23) - 127;
+    uint32_t r;
+    if (e >= -14) {
+        /* normal binary16: keep 10 fraction bits, drop 13 with RNE */
+        r = a + 0x0fffu + ((a >> 13) & 1u);
+        r &= ~0x1fffu;
+        if (r >= 0x47800000u) r = 0x7f800000u; /* >= 65536 after rounding: overflow */
+    } else if (e >= -25) {
+        /* subnormal binary16: multiples of 2^-24 */
+        const int shift = 13 + (-14 - e); /* 14..24 */
+        const uint32_t m = (a & 0x7fffffu) | 0x800000u;
+        const uint32_t half = 1u << (shift - 1), mask = (1u << shift) - 1u;
+        uint32_t q = m >> shift;
+        const uint32_t rem = m & mask;
+        if (rem > half || (rem == half && (q & 1u))) q++;
+        float v = ldexpf((float)q, -24);
+        memcpy(&r, &v, 4);
+    } else {
+        r = 0;
+    }
+    r |= sign;
+    float out;
+    memcpy(&out, &r, 4);
+    return out;
+}
+
+static float round_bf16(float x) {
+    uint32_t u;
+    memcpy(&u, &x, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return x; /* nan */
+    u += 0x7fffu + ((u >> 16) & 1u);
+    u &= 0xffff0000u;
+    float out;
+    memcpy(&out, &u, 4);
+    return out;
+}
+
+float fo_round(float x, int store) {
+    if (store == FO_STORE_F16) return round_f16(x);
+    if (store == FO_STORE_BF16) return round_bf16(x);
+    return x;
+}
+
+void fo_round_array(float *x, long n, int store) {
+    for (long i = 0; i < n; i++) x[i] = fo_round(x[i], store);
+}
+
+/* ---- norm / rope: ref_model.cpp:45-61 ---- */
+
+void fo_rmsnorm(const float *x, const float *w, float *y, int n, float eps) {
+    double ss = 0;
+    for (int i = 0; i < n; i++) ss += (double)x[i] * x[i];
+    const float scale = 1.0f / sqrtf((float)(ss / n) + eps);
+    for (int i = 0; i < n; i++) y[i] = x[i] * scale * w[i];
+}
+
+void fo_rope_neox(float *x, int d, int pos, float theta) {
+    for (int i = 0; i < d / 2; i++) {
+        const float freq = powf(theta, -2.0f * i / d);
+        const float a = pos * freq, c = cosf(a), s = sinf(a);
+        const float x0 = x[i], x1 = x[i + d / 2];
+        x[i] = x0 * c - x1 * s;
+        x[i + d / 2] = x0 * s + x1 * c;
+    }
+}
+
+/* ---- ring / window: flint_config.h:25,29-31; fused.metal:265,269; prefill.metal:106 ---- */
+
+int fo_slot(int pos, int is_swa, int n_slots) { return is_swa ? (pos & (n_slots - 1)) : pos; }
+
+int fo_first_key(int pos, int is_swa, int window) {
+    if (!is_swa) return 0;
+    return pos - (window - 1) > 0 ? pos - (window - 1) : 0;
+}
+
+/* ---- q/k/v of one token: ref_model.cpp:110-124 ---- */
+
+void fo_qkv_prep(const fo_layer *L, const float *qkv, int pos, float *q, float *k, float *v) {
+    const int D = FO_HEAD_DIM;
+    memcpy(q, qkv, sizeof(float) * FO_Q_DIM);
+    memcpy(k, qkv + FO_Q_DIM, sizeof(float) * FO_KV_DIM);
+    memcpy(v, qkv + FO_Q_DIM + FO_KV_DIM, sizeof(float) * FO_KV_DIM);
+    for (int hh = 0; hh < FO_N_HEAD; hh++) {
+        fo_rmsnorm(&q[hh * D], L->q_norm, &q[hh * D], D, L->rms_eps);
+        if (L->has_rope) fo_rope_neox(&q[hh * D], D, pos, L->rope_theta);
+    }
+    for (int hh = 0; hh < FO_N_HEAD_KV; hh++) {
+        fo_rmsnorm(&k[hh * D], L->k_norm, &k[hh * D], D, L->rms_eps);
+        if (L->has_rope) fo_rope_neox(&k[hh * D], D, pos, L->rope_theta);
+    }
+    fo_round_array(k, FO_KV_DIM, L->store);
+    fo_round_array(v, FO_KV_DIM, L->store);
+}
+
+/* ---- sink softmax over the window: ref_model.cpp:126-148 ---- */
+
+static void attend_heads(const fo_layer *L, const float *q, const float *K, const float *V, int pos,
+                         float *att, int h0, int h1) {
+    const int D = FO_HEAD_DIM, kv_dim = FO_KV_DIM, group = FO_GQA;
+    const int first = fo_first_key(pos, L->is_swa, L->window);
+    const float scale = 1.0f / sqrtf((float)D);
+    float *s = (float *)malloc(sizeof(float) * (size_t)(pos + 1));
+    double acc[FO_HEAD_DIM];
+    for (int hh = h0; hh < h1; hh++) {
+        const int kvh = hh / group;
+        float m = L->sinks[hh];
+        for (int j = first; j <= pos; j++) {
+            const float *kj = &K[(size_t)j * kv_dim + kvh * D];
+            float d = 0;
+            for (int i = 0; i < D; i++) d += q[hh * D + i] * kj[i];
+            s[j] = d * scale;
+            m = m > s[j] ? m : s[j];
+        }
+        double denom = expf(L->sinks[hh] - m);
+        for (int i = 0; i < D; i++) acc[i] = 0.0;
+        for (int j = first; j <= pos; j++) {
+            const double p = expf(s[j] - m);
+            denom += p;
+            const float *vj = &V[(size_t)j * kv_dim + kvh * D];
+            for (int i = 0; i < D; i++) acc[i] += p * vj[i];
+        }
+        for (int i = 0; i < D; i++) att[hh * D + i] = (float)(acc[i] / denom);
+    }
+    free(s);
+}
+
+typedef struct {
+    const fo_layer *L;
+    const float *q, *K, *V;
+    int pos, h0, h1;
+    float *att;
+} attend_job;
+
+static void *attend_thread(void *p) {
+    attend_job *j = (attend_job *)p;
+    attend_heads(j->L, j->q, j->K, j->V, j->pos, j->att, j->h0, j->h1);
+    return NULL;
+}
+
+void fo_attend(const fo_layer *L, const float *q, const float *K, const float *V, int pos, float *att,
+               int n_threads) {
+    if (n_threads <= 1) {
+        attend_heads(L, q, K, V, pos, att, 0, FO_N_HEAD);
+        return;
+    }
+    if (n_threads > FO_N_HEAD) n_threads = FO_N_HEAD;
+    pthread_t th[FO_N_HEAD];
+    attend_job jobs[FO_N_HEAD];
+    const int per = (FO_N_HEAD + n_threads - 1) / n_threads;
+    int n = 0;
+    for (int t = 0; t < n_threads; t++) {
+        const int h0 = t * per, h1 = h0 + per < FO_N_HEAD ? h0 + per : FO_N_HEAD;
+        if (h0 >= h1) break;
+        jobs[n] = (attend_job){L, q, K, V, pos, h0, h1, att};
+        if (pthread_create(&th[n], NULL, attend_thread, &jobs[n]) != 0) {
+            attend_heads(L, q, K, V, pos, att, h0, h1);
+            continue;
+        }
+        n++;
+    }
+    for (int t = 0; t < n; t++) pthread_join(th[t], NULL);
+}
+
+/* ---- split-K formulation and LSE merge: fused.metal:266-283 (per split), 331-350 (merge) ---- */
+
+void fo_attend_split(const fo_layer *L, const float *q, const float *K, const float *V, int pos,
+                     int n_split, float *att) {
+    const int D = FO_HEAD_DIM, kv_dim = FO_KV_DIM;
+    const int first = fo_first_key(pos, L->is_swa, L->window);
+    const int n_keys = pos + 1 - first;
+    const float scale = 1.0f / sqrtf((float)D);
+    if (n_split < 1) n_split = 1;
+    const int kps = (n_keys + n_split - 1) / n_split;
+    float *ms = (float *)malloc(sizeof(float) * n_split);
+    double *ls = (double *)malloc(sizeof(double) * n_split);
+    double *accs = (double *)malloc(sizeof(double) * n_split * D);
+    for (int hh = 0; hh < FO_N_HEAD; hh++) {
+        const int kvh = hh / FO_GQA;
+        for (int sp = 0; sp < n_split; sp++) {
+            const int j0 = first + sp * kps;
+            int j1 = j0 + kps;
+            if (j1 > pos + 1) j1 = pos + 1;
+            float m = -INFINITY;
+            for (int j = j0; j < j1; j++) {
+                const float *kj = &K[(size_t)j * kv_dim + kvh * D];
+                float d = 0;
+                for (int i = 0; i < D; i++) d += q[hh * D + i] * kj[i];
+                const float sj = d * scale;
+                m = m > sj ? m : sj;
+            }
+            double l = 0;
+            double *acc = &accs[(size_t)sp * D];
+            for (int i = 0; i < D; i++) acc[i] = 0;
+            for (int j = j0; j < j1; j++) {
+                const float *kj = &K[(size_t)j * kv_dim + kvh * D];
+                float d = 0;
+                for (int i = 0; i < D; i++) d += q[hh * D + i] * kj[i];
+                const double p = exp((double)(d * scale) - m);
+                l += p;
+                const float *vj = &V[(size_t)j * kv_dim + kvh * D];
+                for (int i = 0; i < D; i++) acc[i] += p * vj[i];
+            }
+            ms[sp] = m;
+            ls[sp] = l;
+        }
+        const float sink = L->sinks[hh];
+        float M = sink;
+        for (int sp = 0; sp < n_split; sp++)
+            if (ls[sp] != 0 && ms[sp] > M) M = ms[sp];
+        double Ltot = exp((double)sink - M);
+        double out[FO_HEAD_DIM] = {0};
+        for (int sp = 0; sp < n_split; sp++) {
+            if (ls[sp] == 0) continue; /* empty split, fused.metal:343 */
+            const double c = exp((double)ms[sp] - M);
+            Ltot += ls[sp] * c;
+            for (int i = 0; i < D; i++) out[i] += accs[(size_t)sp * D + i] * c;
+        }
+        for (int i = 0; i < D; i++) att[hh * D + i] = (float)(out[i] / Ltot);
+    }
+    free(ms);
+    free(ls);
+    free(accs);
+}
+
+/* ---- decode step / prefill: ref_model.cpp:95-149 (attention block of forward) ---- */
+
+void fo_decode_step(const fo_layer *L, const float *qkv, int pos, float *K, float *V, float *att,
+                    int n_threads) {
+    float q[FO_Q_DIM];
+    fo_qkv_prep(L, qkv, pos, q, &K[(size_t)pos * FO_KV_DIM], &V[(size_t)pos * FO_KV_DIM]);
+    fo_attend(L, q, K, V, pos, att, n_threads);
+}
+
+void fo_prefill(const fo_layer *L, const float *qkv, int q_stride, int p0, int T, float *K, float *V,
+                float *att, int n_threads) {
+    for (int t = 0; t < T; t++)
+        fo_decode_step(L, qkv + (size_t)t * q_stride, p0 + t, K, V, att + (size_t)t * FO_Q_DIM, n_threads);
+}

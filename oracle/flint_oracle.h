@@ -1,0 +1,94 @@
+/*
+ * CPU oracle for the flint attention hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY. Only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py may load this library, and only as the checker
+ * (or as the timed CPU baseline). The product path (libflint_attn.so) never
+ * links, loads or calls it.
+ *
+ * It restates the reference's fp32 CPU attention, keeping its order of float
+ * and double operations so that, with fp32 KV storage, results are bit-identical
+ * to the reference's RefModel::forward (checked by tests/test_ref_parity.py
+ * against oracle/_ref, which is compiled from the reference sources):
+ *   rmsnorm            /root/reference/src/ref/ref_model.cpp:45-50
+ *   rope_neox          /root/reference/src/ref/ref_model.cpp:53-61
+ *   per-head q/k prep  /root/reference/src/ref/ref_model.cpp:110-121
+ *   sink softmax       /root/reference/src/ref/ref_model.cpp:126-148
+ * plus the GPU-path behaviour the reference's own attention test applies:
+ *   K/V rounded through the cache dtype    /root/reference/src/main.mm:268-277
+ *   current token's K/V rounded before use /root/reference/src/metal/fused.metal:285-289
+ *   split-K partials + LSE merge           /root/reference/src/metal/fused.metal:319-350
+ *   SWA window / ring slot                 /root/reference/src/metal/flint_config.h:25,29-31
+ *
+ * Parity pinning (what checks each function; all in tests/test_oracle.py and
+ * tests/test_ref_parity.py):
+ *   fo_round            numpy float16 / torch bfloat16 casts, bit-exact, all finite inputs of a sweep
+ *   fo_rmsnorm          closed form for constant vectors; reference RefModel (bit-exact)
+ *   fo_rope_neox        pos 0 identity, pair-norm preservation, relative-position invariance
+ *                       of <rope(q,m), rope(k,n)>; reference RefModel (bit-exact)
+ *   fo_attend           one key + sink closed form, n identical keys, sink -> -inf equals plain
+ *                       softmax (scipy), sink -> +inf gives 0, SWA window brute force;
+ *                       reference RefModel (bit-exact, fp32 storage)
+ *   fo_attend_split     equals fo_attend for n_split in {1, 2, 16, 32, 64}
+ *   fo_slot/fo_first_key brute force over pos in [0, 4096) against a linear history
+ */
+#ifndef FLINT_ORACLE_H
+#define FLINT_ORACLE_H
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { FO_N_HEAD = 32, FO_N_HEAD_KV = 4, FO_HEAD_DIM = 128, FO_GQA = 8 };
+enum { FO_Q_DIM = 4096, FO_KV_DIM = 512, FO_QKV_DIM = 5120 };
+enum { FO_STORE_F32 = 0, FO_STORE_F16 = 1, FO_STORE_BF16 = 2 };
+
+typedef struct {
+    int is_swa;       /* sliding-window layer: keys [max(0, pos-window+1), pos] */
+    int has_rope;     /* NEOX RoPE on q and k (independent of is_swa) */
+    int window;       /* 513 for Flint */
+    int store;        /* FO_STORE_*: dtype the KV cache holds */
+    float rope_theta;
+    float rms_eps;
+    const float *q_norm; /* [128] shared by all q heads */
+    const float *k_norm; /* [128] shared by all kv heads */
+    const float *sinks;  /* [32] one logit per q head */
+} fo_layer;
+
+float fo_round(float x, int store);
+void fo_round_array(float *x, long n, int store);
+
+void fo_rmsnorm(const float *x, const float *w, float *y, int n, float eps);
+void fo_rope_neox(float *x, int d, int pos, float theta);
+
+int fo_slot(int pos, int is_swa, int n_slots);
+int fo_first_key(int pos, int is_swa, int window);
+
+/* q [32][128], k [4][128], v [4][128] for one token from its raw qkv row [5120].
+ * k and v are rounded through the storage dtype (what the cache will hold). */
+void fo_qkv_prep(const fo_layer *L, const float *qkv, int pos, float *q, float *k, float *v);
+
+/* Attention output att [32][128] for the query q at position pos over the
+ * linear history K, V [pos+1][512] (row j = what the cache holds for position j). */
+void fo_attend(const fo_layer *L, const float *q, const float *K, const float *V, int pos, float *att,
+               int n_threads);
+
+/* Same result through n_split key splits (float max, double partial sums) and
+ * the log-sum-exp merge with the sink. */
+void fo_attend_split(const fo_layer *L, const float *q, const float *K, const float *V, int pos,
+                     int n_split, float *att);
+
+/* One decode step: prep the token at pos, write its K/V into history row pos,
+ * attend. K, V must hold rows 0..pos-1 already. */
+void fo_decode_step(const fo_layer *L, const float *qkv, int pos, float *K, float *V, float *att,
+                    int n_threads);
+
+/* Prefill of T tokens at positions p0..p0+T-1 (qkv rows q_stride floats apart);
+ * identical to T decode steps. att is [T][4096]. */
+void fo_prefill(const fo_layer *L, const float *qkv, int q_stride, int p0, int T, float *K, float *V,
+                float *att, int n_threads);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,179 @@
+"""ctypes binding of the CPU oracle (oracle/liboracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, always as the checker or the timed CPU baseline,
+never as the product path. See flint_oracle.h for the reference lines each C
+function restates and the checks that pin it.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+REF_DRIVER = os.path.join(HERE, "_ref", "ref_driver")
+
+N_HEAD, N_HEAD_KV, HEAD_DIM, GQA = 32, 4, 128, 8
+Q_DIM, KV_DIM, QKV_DIM = 4096, 512, 5120
+STORE = {"f32": 0, "f16": 1, "bf16": 2}
+
+_f32p = ctypes.POINTER(ctypes.c_float)
+
+
+class _Layer(ctypes.Structure):
+    _fields_ = [
+        ("is_swa", ctypes.c_int),
+        ("has_rope", ctypes.c_int),
+        ("window", ctypes.c_int),
+        ("store", ctypes.c_int),
+        ("rope_theta", ctypes.c_float),
+        ("rms_eps", ctypes.c_float),
+        ("q_norm", _f32p),
+        ("k_norm", _f32p),
+        ("sinks", _f32p),
+    ]
+
+
+_lib = None
+
+
+def build():
+    """Compile liboracle.so from oracle/flint_oracle.c (gcc)."""
+    subprocess.run(["make", "-s", "-C", HERE, "all"], check=True)
+
+
+def build_ref():
+    """Compile oracle/_ref/ref_driver from the reference sources, if present."""
+    if not os.path.isdir("/root/reference/src"):
+        return False
+    subprocess.run(["make", "-s", "-C", HERE, "ref"], check=True)
+    return os.path.exists(REF_DRIVER)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = ctypes.CDLL(LIB_PATH)
+        L.fo_round.restype = ctypes.c_float
+        L.fo_round.argtypes = [ctypes.c_float, ctypes.c_int]
+        L.fo_round_array.argtypes = [_f32p, ctypes.c_long, ctypes.c_int]
+        L.fo_rmsnorm.argtypes = [_f32p, _f32p, _f32p, ctypes.c_int, ctypes.c_float]
+        L.fo_rope_neox.argtypes = [_f32p, ctypes.c_int, ctypes.c_int, ctypes.c_float]
+        L.fo_slot.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int]
+        L.fo_first_key.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int]
+        lp = ctypes.POINTER(_Layer)
+        L.fo_qkv_prep.argtypes = [lp, _f32p, ctypes.c_int, _f32p, _f32p, _f32p]
+        L.fo_attend.argtypes = [lp, _f32p, _f32p, _f32p, ctypes.c_int, _f32p, ctypes.c_int]
+        L.fo_attend_split.argtypes = [lp, _f32p, _f32p, _f32p, ctypes.c_int, ctypes.c_int, _f32p]
+        L.fo_decode_step.argtypes = [lp, _f32p, ctypes.c_int, _f32p, _f32p, _f32p, ctypes.c_int]
+        L.fo_prefill.argtypes = [lp, _f32p, ctypes.c_int, ctypes.c_int, ctypes.c_int, _f32p, _f32p, _f32p,
+                                 ctypes.c_int]
+        _lib = L
+    return _lib
+
+
+def _p(a):
+    assert a.dtype == np.float32 and a.flags["C_CONTIGUOUS"], (a.dtype, a.flags)
+    return a.ctypes.data_as(_f32p)
+
+
+class Layer:
+    """Per-layer attention parameters, mirroring what the engine binds per layer
+    (q_norm/k_norm/sinks tensors, is_swa/has_rope flags, n_swa, rope theta, eps)."""
+
+    def __init__(self, q_norm, k_norm, sinks, is_swa, has_rope, store="f16", rope_theta=1e4, window=513,
+                 rms_eps=1e-6):
+        self.q_norm = np.ascontiguousarray(q_norm, np.float32)
+        self.k_norm = np.ascontiguousarray(k_norm, np.float32)
+        self.sinks = np.ascontiguousarray(sinks, np.float32)
+        assert self.q_norm.shape == (HEAD_DIM,) and self.k_norm.shape == (HEAD_DIM,)
+        assert self.sinks.shape == (N_HEAD,)
+        self.is_swa, self.has_rope, self.store = int(is_swa), int(has_rope), store
+        self.rope_theta, self.window, self.rms_eps = float(rope_theta), int(window), float(rms_eps)
+        self._s = _Layer(self.is_swa, self.has_rope, self.window, STORE[store], self.rope_theta, self.rms_eps,
+                         _p(self.q_norm), _p(self.k_norm), _p(self.sinks))
+
+    @property
+    def ref(self):
+        return ctypes.byref(self._s)
+
+
+def round_store(x, store):
+    x = np.array(x, np.float32, copy=True, order="C")
+    lib().fo_round_array(_p(x), x.size, STORE[store])
+    return x
+
+
+def rmsnorm(x, w, eps=1e-6):
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    y = np.empty_like(x)
+    lib().fo_rmsnorm(_p(x), _p(w), _p(y), x.size, eps)
+    return y
+
+
+def rope_neox(x, pos, theta):
+    x = np.array(x, np.float32, copy=True, order="C")
+    lib().fo_rope_neox(_p(x), x.size, int(pos), float(theta))
+    return x
+
+
+def slot(pos, is_swa, n_slots=1024):
+    return lib().fo_slot(int(pos), int(is_swa), int(n_slots))
+
+
+def first_key(pos, is_swa, window=513):
+    return lib().fo_first_key(int(pos), int(is_swa), int(window))
+
+
+def qkv_prep(layer, qkv_row, pos):
+    qkv_row = np.ascontiguousarray(qkv_row, np.float32)
+    q = np.empty(Q_DIM, np.float32)
+    k = np.empty(KV_DIM, np.float32)
+    v = np.empty(KV_DIM, np.float32)
+    lib().fo_qkv_prep(layer.ref, _p(qkv_row), int(pos), _p(q), _p(k), _p(v))
+    return q, k, v
+
+
+def attend(layer, q, K, V, pos, n_threads=1):
+    """att [4096] for query q (already normed/roped) at pos over history rows K,V [>=pos+1][512]."""
+    q = np.ascontiguousarray(q, np.float32)
+    K = np.ascontiguousarray(K, np.float32)
+    V = np.ascontiguousarray(V, np.float32)
+    assert K.shape[0] >= pos + 1 and V.shape[0] >= pos + 1
+    att = np.empty(Q_DIM, np.float32)
+    lib().fo_attend(layer.ref, _p(q), _p(K), _p(V), int(pos), _p(att), int(n_threads))
+    return att
+
+
+def attend_split(layer, q, K, V, pos, n_split):
+    q = np.ascontiguousarray(q, np.float32)
+    K = np.ascontiguousarray(K, np.float32)
+    V = np.ascontiguousarray(V, np.float32)
+    att = np.empty(Q_DIM, np.float32)
+    lib().fo_attend_split(layer.ref, _p(q), _p(K), _p(V), int(pos), int(n_split), _p(att))
+    return att
+
+
+def decode_step(layer, qkv_row, pos, K, V, n_threads=1):
+    """Writes history row pos of K, V (arrays [cap][512], modified in place) and returns att [4096]."""
+    assert K.dtype == np.float32 and K.flags["C_CONTIGUOUS"] and K.shape[0] > pos
+    qkv_row = np.ascontiguousarray(qkv_row, np.float32)
+    att = np.empty(Q_DIM, np.float32)
+    lib().fo_decode_step(layer.ref, _p(qkv_row), int(pos), _p(K), _p(V), _p(att), int(n_threads))
+    return att
+
+
+def prefill(layer, qkv, p0, K, V, n_threads=1):
+    """qkv [T][5120] rows for positions p0..p0+T-1; K,V history [cap][512] (rows < p0 filled).
+    Returns att [T][4096]."""
+    qkv = np.ascontiguousarray(qkv, np.float32)
+    T = qkv.shape[0]
+    assert K.shape[0] >= p0 + T
+    att = np.empty((T, Q_DIM), np.float32)
+    lib().fo_prefill(layer.ref, _p(qkv), QKV_DIM, int(p0), int(T), _p(K), _p(V), _p(att), int(n_threads))
+    return att
