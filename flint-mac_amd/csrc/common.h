@@ -1,0 +1,72 @@
+// Shared constants and CDNA4 (gfx950) building blocks for the flint attention
+// kernels. Shapes are Flint's fixed attention shapes
+// (/root/reference/src/metal/flint_config.h:13-19).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace flint {
+
+constexpr int N_HEAD = 32;
+constexpr int N_HEAD_KV = 4;
+constexpr int HEAD_DIM = 128;
+constexpr int GQA = N_HEAD / N_HEAD_KV;  // 8
+constexpr int Q_DIM = N_HEAD * HEAD_DIM;  // 4096
+constexpr int KV_DIM = N_HEAD_KV * HEAD_DIM;  // 512
+constexpr int QKV_DIM = Q_DIM + 2 * KV_DIM;  // 5120: one raw q|k|v row
+constexpr float LOG2E = 1.4426950408889634f;
+
+// KV storage dtypes (values of flint_attn_layer.kv_dtype).
+constexpr int DT_F16 = 1;
+constexpr int DT_BF16 = 2;
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
+
+// Per-dtype conversions and MFMA calls. The KV cache holds raw 16-bit words.
+template <int DT>
+struct KvType;
+
+template <>
+struct KvType<DT_F16> {
+    typedef f16x8 vec8;
+    __device__ static inline uint16_t from_float(float x) {
+        _Float16 h = (_Float16)x;  // round to nearest even
+        return __builtin_bit_cast(uint16_t, h);
+    }
+    __device__ static inline float to_float(uint16_t u) { return (float)__builtin_bit_cast(_Float16, u); }
+    __device__ static inline vec8 as_vec(u16x8 u) { return __builtin_bit_cast(vec8, u); }
+    // D(16x16) += A(16x32) * B(32x16)
+    __device__ static inline f32x4 mfma16(vec8 a, vec8 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+    }
+};
+
+template <>
+struct KvType<DT_BF16> {
+    typedef bf16x8 vec8;
+    __device__ static inline uint16_t from_float(float x) {
+        __bf16 h = (__bf16)x;  // round to nearest even
+        return __builtin_bit_cast(uint16_t, h);
+    }
+    __device__ static inline float to_float(uint16_t u) { return __uint_as_float(uint32_t(u) << 16); }
+    __device__ static inline vec8 as_vec(u16x8 u) { return __builtin_bit_cast(vec8, u); }
+    __device__ static inline f32x4 mfma16(vec8 a, vec8 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+    }
+};
+
+// f16 operands for the prefill MFMAs (both KV dtypes convert exactly into f16
+// within its range; see attn_prefill.hip).
+__device__ inline f32x16 mfma32_f16(f16x8 a, f16x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ inline float wave_sum_xor(float v, int mask) { return v + __shfl_xor(v, mask, 64); }
+__device__ inline float wave_max_xor(float v, int mask) { return fmaxf(v, __shfl_xor(v, mask, 64)); }
+
+}  // namespace flint

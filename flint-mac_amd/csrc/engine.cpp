@@ -1,0 +1,431 @@
+// Host side of the flint attention hot path: argument checks, launch plans,
+// device workspaces, the per-layer KV-cache engine and the C ABI
+// (include/flint_attn.h, include/capi.h). Compiled by hipcc as host C++.
+//
+// Stage scheduling mirrors the reference engine's attention stages
+// (/root/reference/src/engine.mm:735-766 decode, 1077-1104 prefill): one
+// stream-ordered launch sequence per layer on the caller's stream.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <memory>
+#include <mutex>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "../../include/capi.h"
+#include "../../include/flint_attn.h"
+#include "common.h"
+#include "flint_attn_internal.h"
+
+namespace flint {
+namespace {
+
+struct Error : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+
+void set_err(char *err, int32_t len, const char *msg) {
+    if (err && len > 0) {
+        std::strncpy(err, msg, len - 1);
+        err[len - 1] = 0;
+    }
+}
+
+void check(hipError_t e, const char *what) {
+    if (e != hipSuccess) throw Error(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+template <typename F>
+int32_t guarded(char *err, int32_t err_len, F &&f) {
+    try {
+        f();
+        return 0;
+    } catch (const std::exception &ex) {
+        set_err(err, err_len, ex.what());
+        return -1;
+    }
+}
+
+// theta^(-2i/128) with the CPU reference's float expression (ref_model.cpp:55)
+void rope_freqs(float theta, float *freq) {
+    for (int i = 0; i < HEAD_DIM / 2; i++) freq[i] = std::pow(theta, -2.0f * i / HEAD_DIM);
+}
+
+// Device scratch that grows on demand, one set per device.
+struct Workspace {
+    void *ptr = nullptr;
+    size_t bytes = 0;
+    void *get(size_t need) {
+        if (need <= bytes) return ptr;
+        if (ptr) check(hipFree(ptr), "hipFree");
+        ptr = nullptr;
+        bytes = 0;
+        check(hipMalloc(&ptr, need), "hipMalloc workspace");
+        bytes = need;
+        return ptr;
+    }
+};
+
+struct DeviceScratch {
+    Workspace partial, qh, kv;
+};
+
+std::mutex g_scratch_mu;
+std::vector<std::unique_ptr<DeviceScratch>> g_scratch;
+
+DeviceScratch &scratch() {
+    int dev = 0;
+    check(hipGetDevice(&dev), "hipGetDevice");
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if ((int)g_scratch.size() <= dev) g_scratch.resize(dev + 1);
+    if (!g_scratch[dev]) g_scratch[dev] = std::make_unique<DeviceScratch>();
+    return *g_scratch[dev];
+}
+
+void validate_layer(const flint_attn_layer *L) {
+    if (!L) throw Error("layer is NULL");
+    if (!L->k_cache || !L->v_cache) throw Error("layer KV cache pointer is NULL");
+    if (!L->q_norm || !L->k_norm || !L->sinks) throw Error("layer q_norm/k_norm/sinks pointer is NULL");
+    if (L->kv_dtype != FLINT_KV_F16 && L->kv_dtype != FLINT_KV_BF16) throw Error("kv_dtype must be F16 or BF16");
+    if (L->n_slots <= 0 || L->n_slots % 32 != 0) throw Error("n_slots must be a positive multiple of 32");
+    if (L->window < 1) throw Error("window must be >= 1");
+    if (L->is_swa) {
+        if (L->n_slots & (L->n_slots - 1)) throw Error("SWA ring size must be a power of two");
+        if (L->n_slots < L->window) throw Error("SWA ring must hold the window (n_slots >= window)");
+    }
+}
+
+// Split plan: 32-key tiles per split so that the 4 kv heads x splits fill the
+// 256 CUs about twice, and no split is shorter than two tiles per wave.
+int plan_tiles_per_split(int n_tiles, int keys_per_split, int n_seq_total_tiles_hint) {
+    if (keys_per_split > 0) return std::max(1, keys_per_split / 32);
+    (void)n_seq_total_tiles_hint;
+    const int target_splits = 128;
+    int tps = (n_tiles + target_splits - 1) / target_splits;
+    return std::max(tps, 8);
+}
+
+constexpr int PART_STRIDE = 132;
+
+void decode_impl(const flint_attn_layer *L, int n_seq, int64_t seq_stride, const float *qkv, float *att,
+                 const int32_t *pos, int32_t keys_per_split, hipStream_t stream) {
+    validate_layer(L);
+    if (n_seq < 1 || n_seq > MAX_SEQ) throw Error("n_seq must be in [1, " + std::to_string(MAX_SEQ) + "]");
+    if (!qkv || !att || !pos) throw Error("qkv/att/pos pointer is NULL");
+    if (keys_per_split < 0 || keys_per_split % 32 != 0) throw Error("keys_per_split must be a multiple of 32");
+    if (n_seq > 1 && seq_stride < (int64_t)N_HEAD_KV * L->n_slots * HEAD_DIM)
+        throw Error("seq_stride smaller than one sequence's cache");
+    DecodeParams P{};
+    P.qkv = qkv;
+    P.q_norm = L->q_norm;
+    P.k_norm = L->k_norm;
+    P.sinks = L->sinks;
+    P.k_cache = (uint16_t *)L->k_cache;
+    P.v_cache = (uint16_t *)L->v_cache;
+    P.seq_stride = seq_stride;
+    P.att = att;
+    P.n_slots = L->n_slots;
+    P.slot_mask = L->is_swa ? L->n_slots - 1 : 0x7fffffff;
+    P.is_swa = L->is_swa;
+    P.has_rope = L->has_rope;
+    P.window = L->window;
+    P.rms_eps = L->rms_eps;
+    rope_freqs(L->rope_theta, P.rope_freq);
+    P.n_seq = n_seq;
+    int total = 0, max_split = 1;
+    for (int s = 0; s < n_seq; s++) {
+        const int p = pos[s];
+        if (p < 0) throw Error("position must be >= 0");
+        if (!L->is_swa && p >= L->n_slots) throw Error("context full: position beyond the layer's KV capacity");
+        const int k_begin = L->is_swa ? std::max(p - (L->window - 1), 0) : 0;
+        const int tiles = p > 0 ? (p + 31) / 32 - k_begin / 32 : 0;
+        const int tps = plan_tiles_per_split(tiles, keys_per_split, 0);
+        const int ns = std::max(1, (tiles + tps - 1) / tps);
+        P.pos[s] = p;
+        P.tiles_per_split[s] = tps;
+        P.split_prefix[s] = total;
+        total += ns;
+        max_split = std::max(max_split, ns);
+    }
+    P.split_prefix[n_seq] = total;
+    P.max_split = max_split;
+    if (max_split > 1) {
+        const size_t need = (size_t)n_seq * N_HEAD * max_split * PART_STRIDE * sizeof(float);
+        P.partial = (float *)scratch().partial.get(need);
+    }
+    check(launch_decode(P, L->kv_dtype, total, stream), "decode launch");
+}
+
+void prefill_impl(const flint_attn_layer *L, const float *qkv, int q_stride, int p0, int T, float *att,
+                  hipStream_t stream) {
+    validate_layer(L);
+    if (!qkv || !att) throw Error("qkv/att pointer is NULL");
+    if (T <= 0) throw Error("prefill: empty");
+    if (p0 < 0) throw Error("prefill: negative start position");
+    if (q_stride < QKV_DIM || q_stride % 4 != 0) throw Error("q_stride must be >= 5120 and a multiple of 4");
+    if (!L->is_swa && p0 + T > L->n_slots) throw Error("prefill: context full");
+    PrefillParams P{};
+    P.qkv = qkv;
+    P.q_stride = q_stride;
+    P.p0 = p0;
+    P.T = T;
+    P.q_norm = L->q_norm;
+    P.k_norm = L->k_norm;
+    P.sinks = L->sinks;
+    P.rms_eps = L->rms_eps;
+    P.is_swa = L->is_swa;
+    P.has_rope = L->has_rope;
+    P.window = L->window;
+    rope_freqs(L->rope_theta, P.rope_freq);
+    P.att = att;
+    DeviceScratch &ws = scratch();
+    P.qh = (_Float16 *)ws.qh.get((size_t)N_HEAD * T * HEAD_DIM * sizeof(_Float16));
+    if (L->is_swa) {
+        P.kbase = std::max(0, p0 - (L->window - 1));
+        P.k_rows = ((p0 + T - P.kbase) + 31) / 32 * 32;
+        uint16_t *kv = (uint16_t *)ws.kv.get((size_t)2 * N_HEAD_KV * P.k_rows * HEAD_DIM * sizeof(uint16_t));
+        P.kd = kv;
+        P.vd = kv + (size_t)N_HEAD_KV * P.k_rows * HEAD_DIM;
+        P.ring_k = (uint16_t *)L->k_cache;
+        P.ring_v = (uint16_t *)L->v_cache;
+        P.ring_slots = L->n_slots;
+        P.ring_from = std::max(p0, p0 + T - L->n_slots);
+    } else {
+        P.kbase = 0;
+        P.k_rows = L->n_slots;
+        P.kd = (uint16_t *)L->k_cache;
+        P.vd = (uint16_t *)L->v_cache;
+        P.ring_k = P.ring_v = nullptr;
+        P.ring_slots = 0;
+        P.ring_from = 0;
+    }
+    check(launch_prefill(P, L->kv_dtype, stream), "prefill launch");
+}
+
+}  // namespace
+}  // namespace flint
+
+using namespace flint;
+
+// ---------------------------------------------------------------------------
+// engine object
+
+struct flint_attn_engine {
+    struct LayerMem {
+        flint_attn_layer desc{};
+        void *kv = nullptr;   // K then V
+        float *w = nullptr;   // q_norm[128] k_norm[128] sinks[32]
+    };
+    std::vector<LayerMem> layers;
+    ~flint_attn_engine() {
+        for (auto &l : layers) {
+            if (l.kv) (void)hipFree(l.kv);
+            if (l.w) (void)hipFree(l.w);
+        }
+    }
+};
+
+extern "C" {
+
+int32_t flint_attn_decode(const flint_attn_layer *layer, const float *qkv, float *att, int32_t pos,
+                          int32_t keys_per_split, void *stream, char *err, int32_t err_len) {
+    return guarded(err, err_len, [&] { decode_impl(layer, 1, 0, qkv, att, &pos, keys_per_split, (hipStream_t)stream); });
+}
+
+int32_t flint_attn_decode_batch(const flint_attn_layer *layer, int32_t n_seq, int64_t seq_stride, const float *qkv,
+                                float *att, const int32_t *pos, int32_t keys_per_split, void *stream, char *err,
+                                int32_t err_len) {
+    return guarded(err, err_len, [&] {
+        decode_impl(layer, n_seq, seq_stride, qkv, att, pos, keys_per_split, (hipStream_t)stream);
+    });
+}
+
+int32_t flint_attn_prefill(const flint_attn_layer *layer, const float *qkv, int32_t q_stride, int32_t p0, int32_t T,
+                           float *att, void *stream, char *err, int32_t err_len) {
+    return guarded(err, err_len, [&] { prefill_impl(layer, qkv, q_stride, p0, T, att, (hipStream_t)stream); });
+}
+
+int32_t flint_attn_sync(char *err, int32_t err_len) {
+    return guarded(err, err_len, [&] { check(hipDeviceSynchronize(), "hipDeviceSynchronize"); });
+}
+
+flint_attn_engine *flint_attn_engine_create(int32_t n_layer, const uint8_t *is_swa, const uint8_t *has_rope,
+                                            int32_t n_ctx, int32_t kv_dtype, float rope_theta, char *err,
+                                            int32_t err_len) {
+    try {
+        if (n_layer <= 0 || !is_swa || !has_rope) throw Error("engine: n_layer > 0 and the layer flags are required");
+        if (n_ctx <= 0) throw Error("engine: n_ctx must be > 0");
+        if (kv_dtype != FLINT_KV_F16 && kv_dtype != FLINT_KV_BF16) throw Error("engine: kv_dtype must be F16 or BF16");
+        auto e = std::make_unique<flint_attn_engine>();
+        e->layers.resize(n_layer);
+        // default weights until set_weights: unit norm gains, zero sinks
+        std::vector<float> init(HEAD_DIM * 2 + N_HEAD, 0.f);
+        std::fill(init.begin(), init.begin() + 2 * HEAD_DIM, 1.f);
+        for (int il = 0; il < n_layer; il++) {
+            auto &L = e->layers[il];
+            const int n_slots = is_swa[il] ? FLINT_SWA_RING : (n_ctx + 31) / 32 * 32;
+            const size_t kv_bytes = (size_t)N_HEAD_KV * n_slots * HEAD_DIM * 2;
+            check(hipMalloc(&L.kv, 2 * kv_bytes), "hipMalloc KV cache");
+            check(hipMemset(L.kv, 0, 2 * kv_bytes), "hipMemset KV cache");
+            check(hipMalloc((void **)&L.w, init.size() * sizeof(float)), "hipMalloc layer weights");
+            check(hipMemcpy(L.w, init.data(), init.size() * sizeof(float), hipMemcpyHostToDevice), "hipMemcpy");
+            L.desc.k_cache = L.kv;
+            L.desc.v_cache = (char *)L.kv + kv_bytes;
+            L.desc.n_slots = n_slots;
+            L.desc.kv_dtype = kv_dtype;
+            L.desc.is_swa = is_swa[il] != 0;
+            L.desc.has_rope = has_rope[il] != 0;
+            L.desc.window = FLINT_N_SWA;
+            L.desc.rope_theta = rope_theta;
+            L.desc.rms_eps = 1e-6f;
+            L.desc.q_norm = L.w;
+            L.desc.k_norm = L.w + HEAD_DIM;
+            L.desc.sinks = L.w + 2 * HEAD_DIM;
+        }
+        return e.release();
+    } catch (const std::exception &ex) {
+        set_err(err, err_len, ex.what());
+        return nullptr;
+    }
+}
+
+void flint_attn_engine_destroy(flint_attn_engine *e) { delete e; }
+
+int32_t flint_attn_engine_n_layer(const flint_attn_engine *e) { return e ? (int32_t)e->layers.size() : 0; }
+
+const flint_attn_layer *flint_attn_engine_layer(const flint_attn_engine *e, int32_t il) {
+    if (!e || il < 0 || il >= (int32_t)e->layers.size()) return nullptr;
+    return &e->layers[il].desc;
+}
+
+int32_t flint_attn_engine_set_weights(flint_attn_engine *e, int32_t il, const float *q_norm, const float *k_norm,
+                                      const float *sinks, char *err, int32_t err_len) {
+    return guarded(err, err_len, [&] {
+        if (!flint_attn_engine_layer(e, il)) throw Error("engine: bad layer index");
+        if (!q_norm || !k_norm || !sinks) throw Error("engine: weight pointer is NULL");
+        float *w = e->layers[il].w;
+        check(hipMemcpy(w, q_norm, HEAD_DIM * sizeof(float), hipMemcpyHostToDevice), "hipMemcpy q_norm");
+        check(hipMemcpy(w + HEAD_DIM, k_norm, HEAD_DIM * sizeof(float), hipMemcpyHostToDevice), "hipMemcpy k_norm");
+        check(hipMemcpy(w + 2 * HEAD_DIM, sinks, N_HEAD * sizeof(float), hipMemcpyHostToDevice), "hipMemcpy sinks");
+    });
+}
+
+int32_t flint_attn_engine_decode(flint_attn_engine *e, int32_t il, const float *qkv, float *att, int32_t pos,
+                                 void *stream, char *err, int32_t err_len) {
+    return guarded(err, err_len, [&] {
+        const flint_attn_layer *L = flint_attn_engine_layer(e, il);
+        if (!L) throw Error("engine: bad layer index");
+        decode_impl(L, 1, 0, qkv, att, &pos, 0, (hipStream_t)stream);
+    });
+}
+
+int32_t flint_attn_engine_prefill(flint_attn_engine *e, int32_t il, const float *qkv, int32_t p0, int32_t T,
+                                  float *att, void *stream, char *err, int32_t err_len) {
+    return guarded(err, err_len, [&] {
+        const flint_attn_layer *L = flint_attn_engine_layer(e, il);
+        if (!L) throw Error("engine: bad layer index");
+        prefill_impl(L, qkv, QKV_DIM, p0, T, att, (hipStream_t)stream);
+    });
+}
+
+int32_t flint_attn_engine_debug_attn(flint_attn_engine *e, int32_t il, const float *qkv, int32_t n_tok, int32_t chunk,
+                                     float *out, char *err, int32_t err_len) {
+    return guarded(err, err_len, [&] {
+        const flint_attn_layer *L = flint_attn_engine_layer(e, il);
+        if (!L) throw Error("engine: bad layer index");
+        if (!qkv || !out || n_tok <= 0 || chunk <= 0) throw Error("debug_attn: bad arguments");
+        float *dq = nullptr, *dout = nullptr;
+        struct Free {
+            float *&a, *&b;
+            ~Free() {
+                if (a) (void)hipFree(a);
+                if (b) (void)hipFree(b);
+            }
+        } fr{dq, dout};
+        check(hipMalloc((void **)&dq, (size_t)n_tok * QKV_DIM * sizeof(float)), "hipMalloc");
+        check(hipMalloc((void **)&dout, (size_t)n_tok * Q_DIM * sizeof(float)), "hipMalloc");
+        check(hipMemcpy(dq, qkv, (size_t)n_tok * QKV_DIM * sizeof(float), hipMemcpyHostToDevice), "hipMemcpy");
+        for (int p0 = 0; p0 < n_tok; p0 += chunk) {
+            const int T = std::min(chunk, n_tok - p0);
+            prefill_impl(L, dq + (size_t)p0 * QKV_DIM, QKV_DIM, p0, T, dout + (size_t)p0 * Q_DIM, nullptr);
+        }
+        check(hipMemcpy(out, dout, (size_t)n_tok * Q_DIM * sizeof(float), hipMemcpyDeviceToHost), "hipMemcpy");
+    });
+}
+
+// ---------------------------------------------------------------------------
+// The engine's C API (include/capi.h; /root/reference/src/capi.mm:1-78).
+
+}  // extern "C"
+
+struct flint_engine {
+    flint_attn_engine *attn = nullptr;
+    int32_t n_ctx = 0;
+    int32_t pos = 0;
+    std::vector<float> logits;
+    ~flint_engine() { flint_attn_engine_destroy(attn); }
+};
+
+extern "C" {
+
+flint_engine *flint_open(const flint_config *cfg, char *err, int32_t err_len) {
+    try {
+        if (!cfg || !cfg->model_path) throw Error("flint_open: no model path");
+        std::FILE *f = std::fopen(cfg->model_path, "rb");
+        if (!f) throw Error(std::string("cannot open ") + cfg->model_path);
+        uint32_t magic = 0;
+        const size_t got = std::fread(&magic, 1, 4, f);
+        std::fclose(f);
+        if (got != 4 || magic != 0x46554747u) throw Error(std::string("not a GGUF file: ") + cfg->model_path);
+        throw Error(
+            "flint_open: this library implements the attention hot path only; the GGUF weight loader, "
+            "projections and FFN are not part of this build");
+    } catch (const std::exception &ex) {
+        set_err(err, err_len, ex.what());
+        return nullptr;
+    }
+}
+
+void flint_close(flint_engine *e) { delete e; }
+
+int32_t flint_n_ctx(const flint_engine *e) { return e ? e->n_ctx : 0; }
+int32_t flint_n_vocab(void) { return 150144; }
+int32_t flint_pos(const flint_engine *e) { return e ? e->pos : 0; }
+
+int32_t flint_truncate(flint_engine *e, int32_t pos) {
+    if (!e || pos < 0 || pos > e->pos) return -1;
+    e->pos = pos;
+    return 0;
+}
+
+int32_t flint_prefill(flint_engine *e, const int32_t *tokens, int32_t n, char *err, int32_t err_len) {
+    if (!e) {
+        set_err(err, err_len, "flint_prefill: no engine");
+        return -1;
+    }
+    if (!tokens || n <= 0) {
+        set_err(err, err_len, "prefill: empty");
+        return -1;
+    }
+    set_err(err, err_len, "flint_prefill: weights are not part of this build");
+    return -1;
+}
+
+int32_t flint_decode(flint_engine *e, int32_t token, char *err, int32_t err_len) {
+    (void)token;
+    if (!e) {
+        set_err(err, err_len, "flint_decode: no engine");
+        return -1;
+    }
+    set_err(err, err_len, "flint_decode: weights are not part of this build");
+    return -1;
+}
+
+const float *flint_logits(const flint_engine *e) { return e && !e->logits.empty() ? e->logits.data() : nullptr; }
+
+}  // extern "C"

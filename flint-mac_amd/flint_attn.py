@@ -1,0 +1,229 @@
+"""Python binding of libflint_attn.so (the MI355X attention hot path) over its C ABI.
+
+Mirrors the reference engine's attention interface (/root/reference/src/engine.h:24-79:
+per-layer KV cache, decode step, chunked prefill, debug_attn) for tests and the
+benchmark. Device memory and streams come from PyTorch (plumbing only); every
+computation runs in the HIP kernels of libflint_attn.so. There is no fallback:
+if the library is missing, loading raises.
+"""
+import ctypes
+import os
+import re
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libflint_attn.so")
+INCLUDE = os.path.join(os.path.dirname(HERE), "include")
+
+N_HEAD, N_HEAD_KV, HEAD_DIM, GQA = 32, 4, 128, 8
+Q_DIM, KV_DIM, QKV_DIM = 4096, 512, 5120
+N_SWA, SWA_RING = 513, 1024
+KV_F16, KV_BF16 = 1, 2
+
+
+class FlintAttnError(RuntimeError):
+    pass
+
+
+class LayerDesc(ctypes.Structure):
+    """flint_attn_layer (include/flint_attn.h)."""
+    _fields_ = [
+        ("k_cache", ctypes.c_void_p),
+        ("v_cache", ctypes.c_void_p),
+        ("n_slots", ctypes.c_int32),
+        ("kv_dtype", ctypes.c_int32),
+        ("is_swa", ctypes.c_int32),
+        ("has_rope", ctypes.c_int32),
+        ("window", ctypes.c_int32),
+        ("rope_theta", ctypes.c_float),
+        ("rms_eps", ctypes.c_float),
+        ("q_norm", ctypes.c_void_p),
+        ("k_norm", ctypes.c_void_p),
+        ("sinks", ctypes.c_void_p),
+    ]
+
+
+_lib = None
+_vp, _i32, _i64, _f32 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_float
+_cp = ctypes.c_char_p
+_lp = ctypes.POINTER(LayerDesc)
+_i32p = ctypes.POINTER(ctypes.c_int32)
+_u8p = ctypes.POINTER(ctypes.c_uint8)
+_f32p = ctypes.POINTER(ctypes.c_float)
+
+_SIGS = {
+    "flint_attn_decode": (_i32, [_lp, _vp, _vp, _i32, _i32, _vp, _cp, _i32]),
+    "flint_attn_decode_batch": (_i32, [_lp, _i32, _i64, _vp, _vp, _i32p, _i32, _vp, _cp, _i32]),
+    "flint_attn_prefill": (_i32, [_lp, _vp, _i32, _i32, _i32, _vp, _vp, _cp, _i32]),
+    "flint_attn_sync": (_i32, [_cp, _i32]),
+    "flint_attn_engine_create": (_vp, [_i32, _u8p, _u8p, _i32, _i32, _f32, _cp, _i32]),
+    "flint_attn_engine_destroy": (None, [_vp]),
+    "flint_attn_engine_n_layer": (_i32, [_vp]),
+    "flint_attn_engine_set_weights": (_i32, [_vp, _i32, _f32p, _f32p, _f32p, _cp, _i32]),
+    "flint_attn_engine_layer": (_lp, [_vp, _i32]),
+    "flint_attn_engine_decode": (_i32, [_vp, _i32, _vp, _vp, _i32, _vp, _cp, _i32]),
+    "flint_attn_engine_prefill": (_i32, [_vp, _i32, _vp, _i32, _i32, _vp, _vp, _cp, _i32]),
+    "flint_attn_engine_debug_attn": (_i32, [_vp, _i32, _f32p, _i32, _i32, _f32p, _cp, _i32]),
+    "flint_open": (_vp, [_vp, _cp, _i32]),
+    "flint_close": (None, [_vp]),
+    "flint_n_ctx": (_i32, [_vp]),
+    "flint_n_vocab": (_i32, []),
+    "flint_pos": (_i32, [_vp]),
+    "flint_truncate": (_i32, [_vp, _i32]),
+    "flint_prefill": (_i32, [_vp, _i32p, _i32, _cp, _i32]),
+    "flint_decode": (_i32, [_vp, _i32, _cp, _i32]),
+    "flint_logits": (_f32p, [_vp]),
+}
+
+
+def lib():
+    """Load libflint_attn.so (raises FlintAttnError if it was not built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise FlintAttnError(f"{LIB_PATH} is missing: run __graft_entry__.build() (make -C flint-mac_amd)")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def header_functions():
+    """Names of every function declared in include/*.h."""
+    names = []
+    for fn in sorted(os.listdir(INCLUDE)):
+        if fn.endswith(".h"):
+            src = open(os.path.join(INCLUDE, fn)).read()
+            src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+            src = re.sub(r"//[^\n]*", "", src)
+            names += re.findall(r"\b(flint_\w+)\s*\(", src)
+    return sorted(set(names))
+
+
+def _call(fn, *args):
+    err = ctypes.create_string_buffer(512)
+    rc = fn(*args, err, len(err))
+    if rc != 0:
+        raise FlintAttnError(err.value.decode())
+
+
+def _stream(stream):
+    if stream is None:
+        import torch
+        return torch.cuda.current_stream().cuda_stream
+    return stream
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr())
+
+
+class KVLayer:
+    """One attention layer on the GPU: KV cache in HBM (K [4][n_slots][128],
+    V transposed [4][128][n_slots]) and its q_norm / k_norm / sinks.
+    `n_seq` > 1 allocates independent caches for that many sequences."""
+
+    def __init__(self, is_swa, has_rope, n_slots=None, kv_dtype="f16", rope_theta=1e4, window=N_SWA,
+                 q_norm=None, k_norm=None, sinks=None, n_seq=1, device="cuda", rms_eps=1e-6):
+        import torch
+        self.torch_dtype = {"f16": torch.float16, "bf16": torch.bfloat16}[kv_dtype]
+        self.kv_dtype = kv_dtype
+        if n_slots is None:
+            n_slots = SWA_RING if is_swa else 4096
+        self.n_slots, self.n_seq = int(n_slots), int(n_seq)
+        self.k = torch.zeros((n_seq, N_HEAD_KV, n_slots, HEAD_DIM), dtype=self.torch_dtype, device=device)
+        self.v = torch.zeros((n_seq, N_HEAD_KV, HEAD_DIM, n_slots), dtype=self.torch_dtype, device=device)
+        f = lambda a, n, d: torch.as_tensor(a if a is not None else [d] * n, dtype=torch.float32).to(device)
+        self.q_norm = f(q_norm, HEAD_DIM, 1.0).contiguous()
+        self.k_norm = f(k_norm, HEAD_DIM, 1.0).contiguous()
+        self.sinks = f(sinks, N_HEAD, 0.0).contiguous()
+        self.desc = LayerDesc(self.k.data_ptr(), self.v.data_ptr(), self.n_slots,
+                              KV_F16 if kv_dtype == "f16" else KV_BF16, int(bool(is_swa)), int(bool(has_rope)),
+                              int(window), float(rope_theta), float(rms_eps), self.q_norm.data_ptr(),
+                              self.k_norm.data_ptr(), self.sinks.data_ptr())
+        self.is_swa, self.has_rope, self.window, self.rope_theta = bool(is_swa), bool(has_rope), window, rope_theta
+
+    @property
+    def seq_stride(self):
+        return N_HEAD_KV * self.n_slots * HEAD_DIM
+
+    def slot(self, pos):
+        return pos & (self.n_slots - 1) if self.is_swa else pos
+
+    def decode(self, qkv, att, pos, keys_per_split=0, stream=None):
+        """qkv: cuda float32 [5120] (or [n_seq][5120]); att: cuda float32 [4096] (or [n_seq][4096]);
+        pos: int or list of ints (one per sequence)."""
+        if isinstance(pos, int):
+            assert self.n_seq == 1
+            _call(lib().flint_attn_decode, ctypes.byref(self.desc), _ptr(qkv), _ptr(att), pos, keys_per_split,
+                  _stream(stream))
+        else:
+            arr = (ctypes.c_int32 * len(pos))(*pos)
+            _call(lib().flint_attn_decode_batch, ctypes.byref(self.desc), len(pos), self.seq_stride, _ptr(qkv),
+                  _ptr(att), arr, keys_per_split, _stream(stream))
+
+    def prefill(self, qkv, att, p0, T=None, q_stride=QKV_DIM, stream=None):
+        """qkv: cuda float32 [T][q_stride] raw rows for positions p0..p0+T-1; att: cuda float32 [T][4096]."""
+        if T is None:
+            T = qkv.shape[0]
+        _call(lib().flint_attn_prefill, ctypes.byref(self.desc), _ptr(qkv), q_stride, p0, T, _ptr(att),
+              _stream(stream))
+
+
+def sync():
+    _call(lib().flint_attn_sync)
+
+
+class Engine:
+    """flint_attn_engine: the KV caches and weights of every layer."""
+
+    def __init__(self, is_swa, has_rope, n_ctx, kv_dtype="f16", rope_theta=1e4):
+        n = len(is_swa)
+        a = (ctypes.c_uint8 * n)(*[int(bool(x)) for x in is_swa])
+        b = (ctypes.c_uint8 * n)(*[int(bool(x)) for x in has_rope])
+        err = ctypes.create_string_buffer(512)
+        h = lib().flint_attn_engine_create(n, a, b, n_ctx, KV_F16 if kv_dtype == "f16" else KV_BF16,
+                                           rope_theta, err, len(err))
+        if not h:
+            raise FlintAttnError(err.value.decode())
+        self.h = ctypes.c_void_p(h)
+
+    def close(self):
+        if self.h:
+            lib().flint_attn_engine_destroy(self.h)
+            self.h = None
+
+    __del__ = close
+
+    @property
+    def n_layer(self):
+        return lib().flint_attn_engine_n_layer(self.h)
+
+    def layer(self, il):
+        p = lib().flint_attn_engine_layer(self.h, il)
+        if not p:
+            raise FlintAttnError(f"bad layer index {il}")
+        return p.contents
+
+    def set_weights(self, il, q_norm, k_norm, sinks):
+        import numpy as np
+        arrs = [np.ascontiguousarray(x, np.float32) for x in (q_norm, k_norm, sinks)]
+        _call(lib().flint_attn_engine_set_weights, self.h, il, *[x.ctypes.data_as(_f32p) for x in arrs])
+
+    def decode(self, il, qkv, att, pos, stream=None):
+        _call(lib().flint_attn_engine_decode, self.h, il, _ptr(qkv), _ptr(att), pos, _stream(stream))
+
+    def prefill(self, il, qkv, p0, att, stream=None):
+        _call(lib().flint_attn_engine_prefill, self.h, il, _ptr(qkv), p0, qkv.shape[0], _ptr(att), _stream(stream))
+
+    def debug_attn(self, il, qkv, chunk):
+        """host float32 qkv [n][5120] -> host float32 [n][4096] (Engine::debug_attn)."""
+        import numpy as np
+        qkv = np.ascontiguousarray(qkv, np.float32)
+        n = qkv.shape[0]
+        out = np.empty((n, Q_DIM), np.float32)
+        _call(lib().flint_attn_engine_debug_attn, self.h, il, qkv.ctypes.data_as(_f32p), n, chunk,
+              out.ctypes.data_as(_f32p))
+        return out

@@ -1,0 +1,51 @@
+"""Shared input generators and comparison helpers for the attention tests.
+
+Inputs follow BASELINE.json's configs: raw q|k|v ~ N(0,1), RMSNorm gains
+~ U(0.5, 1.5), per-head sink logits ~ N(0,1), seeded numpy generators.
+"""
+import numpy as np
+
+import oracle as fo
+
+N_HEAD, N_HEAD_KV, HEAD_DIM = 32, 4, 128
+Q_DIM, KV_DIM, QKV_DIM = 4096, 512, 5120
+
+# attention-output tolerance of the hot path vs the oracle (fp16/bf16 KV)
+MAX_ABS = 2e-3
+MEAN_ABS = 2e-4
+
+
+def layer_weights(rng):
+    q_norm = rng.uniform(0.5, 1.5, HEAD_DIM).astype(np.float32)
+    k_norm = rng.uniform(0.5, 1.5, HEAD_DIM).astype(np.float32)
+    sinks = rng.standard_normal(N_HEAD).astype(np.float32)
+    return q_norm, k_norm, sinks
+
+
+def oracle_layer(kv, q_norm, k_norm, sinks, store):
+    """fo.Layer with the same settings as a flint_attn.KVLayer."""
+    return fo.Layer(q_norm, k_norm, sinks, kv.is_swa, kv.has_rope, store, kv.rope_theta, kv.window)
+
+
+def assert_close(got, want, what="", max_abs=MAX_ABS, mean_abs=MEAN_ABS):
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    assert got.shape == want.shape, (got.shape, want.shape)
+    assert np.all(np.isfinite(got)), f"{what}: non-finite output"
+    d = np.abs(got - want)
+    mx, mn = float(d.max()), float(d.mean())
+    assert mx <= max_abs and mn <= mean_abs, f"{what}: max-abs {mx:.3e} (<= {max_abs}), mean-abs {mn:.3e} (<= {mean_abs})"
+    return mx, mn
+
+
+def to_cache_layout(K, V, n_slots, slots):
+    """Linear history rows K,V [n][512] placed at the given slots -> (K [4][n_slots][128], V^T [4][128][n_slots])."""
+    n = K.shape[0]
+    Kc = np.zeros((N_HEAD_KV, n_slots, HEAD_DIM), np.float32)
+    Vc = np.zeros((N_HEAD_KV, HEAD_DIM, n_slots), np.float32)
+    Kh = K.reshape(n, N_HEAD_KV, HEAD_DIM)
+    Vh = V.reshape(n, N_HEAD_KV, HEAD_DIM)
+    slots = np.asarray(slots)
+    Kc[:, slots, :] = Kh.transpose(1, 0, 2)
+    Vc[:, :, slots] = Vh.transpose(1, 2, 0)
+    return Kc, Vc

@@ -1,0 +1,140 @@
+"""The C-ABI library on the CPU: it loads, exports every function the headers
+declare, and its host-side checks and the engine C API's error paths behave
+like the reference's (/root/reference/src/capi.mm:17-73). No GPU work here:
+every call below fails its argument checks before touching the device."""
+import ctypes
+import os
+import subprocess
+
+import pytest
+
+import flint_attn as fa
+
+
+def test_library_exports_every_header_function():
+    names = fa.header_functions()
+    assert len(names) >= 21
+    L = fa.lib()
+    missing = [n for n in names if not hasattr(L, n)]
+    assert not missing, missing
+    nm = subprocess.run(["nm", "-D", "--defined-only", fa.LIB_PATH], capture_output=True, text=True).stdout
+    exported = {line.split()[-1] for line in nm.splitlines() if " T " in line}
+    assert set(names) <= exported
+
+
+def test_capi_header_matches_rust_ffi_signatures():
+    """The nine entry points the Rust server binds (/root/reference/server/src/ffi.rs:18-28)."""
+    want = {"flint_open", "flint_close", "flint_n_ctx", "flint_n_vocab", "flint_pos", "flint_truncate",
+            "flint_prefill", "flint_decode", "flint_logits"}
+    assert want <= set(fa.header_functions())
+
+
+def _err():
+    return ctypes.create_string_buffer(256)
+
+
+class _Cfg(ctypes.Structure):
+    _fields_ = [("model_path", ctypes.c_char_p), ("metallib_dir", ctypes.c_char_p), ("pool_gb", ctypes.c_double),
+                ("n_ctx", ctypes.c_int32)]
+
+
+def _open(path):
+    cfg = _Cfg(path.encode() if path else None, b".", 0.0, 4096)
+    err = _err()
+    h = fa.lib().flint_open(ctypes.cast(ctypes.pointer(cfg), ctypes.c_void_p), err, len(err))
+    return h, err.value.decode()
+
+
+def test_capi_open_errors(tmp_path):
+    L = fa.lib()
+    assert L.flint_n_vocab() == 150144
+    h, msg = _open(str(tmp_path / "missing.gguf"))
+    assert not h and msg.startswith("cannot open")
+    bad = tmp_path / "bad.gguf"
+    bad.write_bytes(b"NOPE" + b"\0" * 60)
+    h, msg = _open(str(bad))
+    assert not h and msg.startswith("not a GGUF file")
+    ok = tmp_path / "model.gguf"
+    ok.write_bytes(b"GGUF" + b"\0" * 60)
+    h, msg = _open(str(ok))
+    assert not h and "attention hot path only" in msg
+    # err may be NULL
+    cfg = _Cfg(str(tmp_path / "missing.gguf").encode(), b".", 0.0, 0)
+    assert not L.flint_open(ctypes.cast(ctypes.pointer(cfg), ctypes.c_void_p), None, 0)
+
+
+def test_capi_null_handle_paths():
+    L = fa.lib()
+    L.flint_close(None)
+    assert L.flint_truncate(None, 0) == -1
+    assert L.flint_pos(None) == 0 and L.flint_n_ctx(None) == 0
+    err = _err()
+    assert L.flint_decode(None, 1, err, len(err)) == -1 and err.value
+    assert L.flint_prefill(None, None, 0, err, len(err)) == -1
+    assert not L.flint_logits(None)
+
+
+def _layer(**kw):
+    d = dict(k_cache=0x1000, v_cache=0x2000, n_slots=1024, kv_dtype=fa.KV_F16, is_swa=1, has_rope=1, window=513,
+             rope_theta=1e4, rms_eps=1e-6, q_norm=0x3000, k_norm=0x4000, sinks=0x5000)
+    d.update(kw)
+    return fa.LayerDesc(**d)
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(n_slots=1000), "multiple of 32"),
+    (dict(n_slots=992), "power of two"),
+    (dict(n_slots=256), "must hold the window"),
+    (dict(kv_dtype=7), "kv_dtype"),
+    (dict(k_cache=0), "KV cache pointer"),
+    (dict(sinks=0), "sinks"),
+    (dict(window=0), "window"),
+])
+def test_decode_rejects_bad_layer(kw, msg):
+    with pytest.raises(fa.FlintAttnError, match=msg):
+        fa._call(fa.lib().flint_attn_decode, ctypes.byref(_layer(**kw)), ctypes.c_void_p(0x6000),
+                 ctypes.c_void_p(0x7000), 5, 0, None)
+
+
+def test_decode_rejects_bad_arguments():
+    L = fa.lib()
+    lay = _layer(is_swa=0, n_slots=2048)
+    with pytest.raises(fa.FlintAttnError, match="context full"):
+        fa._call(L.flint_attn_decode, ctypes.byref(lay), ctypes.c_void_p(1), ctypes.c_void_p(1), 2048, 0, None)
+    with pytest.raises(fa.FlintAttnError, match="multiple of 32"):
+        fa._call(L.flint_attn_decode, ctypes.byref(lay), ctypes.c_void_p(1), ctypes.c_void_p(1), 5, 33, None)
+    with pytest.raises(fa.FlintAttnError, match="position"):
+        fa._call(L.flint_attn_decode, ctypes.byref(lay), ctypes.c_void_p(1), ctypes.c_void_p(1), -1, 0, None)
+    with pytest.raises(fa.FlintAttnError, match="NULL"):
+        fa._call(L.flint_attn_decode, None, ctypes.c_void_p(1), ctypes.c_void_p(1), 5, 0, None)
+    pos = (ctypes.c_int32 * 2)(1, 2)
+    with pytest.raises(fa.FlintAttnError, match="n_seq"):
+        fa._call(L.flint_attn_decode_batch, ctypes.byref(lay), 0, 0, ctypes.c_void_p(1), ctypes.c_void_p(1), pos, 0,
+                 None)
+    with pytest.raises(fa.FlintAttnError, match="seq_stride"):
+        fa._call(L.flint_attn_decode_batch, ctypes.byref(lay), 2, 100, ctypes.c_void_p(1), ctypes.c_void_p(1), pos,
+                 0, None)
+
+
+def test_prefill_rejects_bad_arguments():
+    L = fa.lib()
+    full = _layer(is_swa=0, n_slots=4096)
+    with pytest.raises(fa.FlintAttnError, match="prefill: empty"):
+        fa._call(L.flint_attn_prefill, ctypes.byref(full), ctypes.c_void_p(1), 5120, 0, 0, ctypes.c_void_p(1), None)
+    with pytest.raises(fa.FlintAttnError, match="context full"):
+        fa._call(L.flint_attn_prefill, ctypes.byref(full), ctypes.c_void_p(1), 5120, 4000, 100, ctypes.c_void_p(1),
+                 None)
+    with pytest.raises(fa.FlintAttnError, match="q_stride"):
+        fa._call(L.flint_attn_prefill, ctypes.byref(full), ctypes.c_void_p(1), 100, 0, 10, ctypes.c_void_p(1), None)
+
+
+def test_engine_create_rejects_bad_arguments():
+    L = fa.lib()
+    err = _err()
+    flags = (ctypes.c_uint8 * 2)(1, 0)
+    assert not L.flint_attn_engine_create(0, flags, flags, 4096, 1, 1e4, err, len(err)) and err.value
+    assert not L.flint_attn_engine_create(2, flags, flags, 0, 1, 1e4, err, len(err))
+    assert not L.flint_attn_engine_create(2, flags, flags, 4096, 3, 1e4, err, len(err))
+    assert b"kv_dtype" in err.value
+    assert L.flint_attn_engine_n_layer(None) == 0
+    assert not L.flint_attn_engine_layer(None, 0)

@@ -1,0 +1,185 @@
+"""Fused decode attention on the GPU against the CPU oracle (BASELINE configs 1-3
+and the batched form of config 5), through the C ABI (flint_attn_decode,
+flint_attn_decode_batch). Tolerance: max-abs 2e-3 and mean-abs 2e-4 on the
+attention output; ring slot contents bit-exact for V (K within 1 ulp of the
+cache dtype: its norm/rope runs in fp32 on both sides)."""
+import numpy as np
+import pytest
+import torch
+
+import flint_attn as fa
+import oracle as fo
+from helpers import (HEAD_DIM, KV_DIM, N_HEAD_KV, QKV_DIM, Q_DIM, assert_close, layer_weights, oracle_layer,
+                     to_cache_layout)
+
+pytestmark = pytest.mark.gpu
+
+TORCH_DT = {"f16": torch.float16, "bf16": torch.bfloat16}
+
+
+def _say(msg):
+    print(f"\n[gpu-test] {msg}", flush=True)
+
+
+def _fill_cache(kv, K, V, slots, seq=0):
+    Kc, Vc = to_cache_layout(K, V, kv.n_slots, slots)
+    kv.k[seq].copy_(torch.from_numpy(Kc).to(kv.torch_dtype))
+    kv.v[seq].copy_(torch.from_numpy(Vc).to(kv.torch_dtype))
+
+
+def _history(rng, n, store, outlier_frac=0.0):
+    K = rng.standard_normal((n, KV_DIM)).astype(np.float32)
+    V = rng.standard_normal((n, KV_DIM)).astype(np.float32)
+    if outlier_frac:
+        K[rng.random(n) < outlier_frac] *= 8
+        V[rng.random(n) < outlier_frac] *= 8
+    return fo.round_store(K, store), fo.round_store(V, store)
+
+
+def _ulp_close(a, b, dtype):
+    """|a - b| <= 1 ulp of the 16-bit type at b's magnitude."""
+    a64, b64 = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    mant = 10 if dtype == "f16" else 7
+    ulp = np.maximum(np.abs(b64), 6.1e-5 if dtype == "f16" else 1e-38) * 2.0 ** -mant
+    return np.all(np.abs(a64 - b64) <= ulp * 1.0001)
+
+
+@pytest.mark.parametrize("store", ["f16", "bf16"])
+def test_decode_swa_ring_steps_config2(cuda, store):
+    """Config 2: SWA layer, RoPE, 1024-slot ring, window 513, positions 0..1300 one token at a time."""
+    n = 1301 if store == "f16" else 700
+    _say(f"decode swa ring steps store={store} n={n} seed=1")
+    rng = np.random.default_rng(1)
+    qn, kn, sk = layer_weights(rng)
+    kv = fa.KVLayer(is_swa=True, has_rope=True, kv_dtype=store, rope_theta=1e6, q_norm=qn, k_norm=kn, sinks=sk)
+    L = oracle_layer(kv, qn, kn, sk, store)
+    qkv = rng.standard_normal((n, QKV_DIM)).astype(np.float32)
+    dq = torch.from_numpy(qkv).to(cuda)
+    att = torch.zeros((n, Q_DIM), device=cuda)
+    for pos in range(n):
+        kv.decode(dq[pos], att[pos], pos)
+    torch.cuda.synchronize()
+    K = np.zeros((n, KV_DIM), np.float32)
+    V = np.zeros((n, KV_DIM), np.float32)
+    want = fo.prefill(L, qkv, 0, K, V, n_threads=8)
+    got = att.cpu().numpy()
+    for pos in range(n):
+        assert_close(got[pos], want[pos], f"pos {pos}")
+    assert_close(got, want, "all steps")
+    # ring: slot p & 1023 holds position p for the last 1024 positions
+    vc = kv.v[0].float().cpu().numpy()  # [4][128][1024]
+    kc = kv.k[0].float().cpu().numpy()  # [4][1024][128]
+    for p in range(max(0, n - 1024), n):
+        s = p & 1023
+        assert np.array_equal(vc[:, :, s], V[p].reshape(N_HEAD_KV, HEAD_DIM)), f"V slot {s} pos {p}"
+        assert _ulp_close(kc[:, s, :], K[p].reshape(N_HEAD_KV, HEAD_DIM), store), f"K slot {s} pos {p}"
+
+
+def test_decode_full_rope_config1(cuda):
+    """Config 1 shapes on the GPU: full layer with NEOX RoPE theta=1e6, 1024 cached positions, seed 0."""
+    _say("decode full rope 1024 cached seed=0")
+    rng = np.random.default_rng(0)
+    qn, kn, sk = layer_weights(rng)
+    n = 1024
+    kv = fa.KVLayer(is_swa=False, has_rope=True, n_slots=1056, kv_dtype="f16", rope_theta=1e6, q_norm=qn,
+                    k_norm=kn, sinks=sk)
+    L = oracle_layer(kv, qn, kn, sk, "f16")
+    K, V = _history(rng, n + 1, "f16")
+    _fill_cache(kv, K[:n], V[:n], np.arange(n))
+    qkv = rng.standard_normal(QKV_DIM).astype(np.float32)
+    att = torch.zeros(Q_DIM, device=cuda)
+    for kps in (0, 256, 1024):
+        kv.decode(torch.from_numpy(qkv).to(cuda), att, n, keys_per_split=kps)
+        torch.cuda.synchronize()
+        want = fo.decode_step(L, qkv, n, K, V, n_threads=8)
+        assert_close(att.cpu().numpy(), want, f"keys_per_split={kps}")
+
+
+@pytest.mark.parametrize("store", ["f16", "bf16"])
+def test_decode_split_k_32k_config3(cuda, store):
+    """Config 3: full layer (NoPE), 32768 cached positions, 1% outlier rows x8, seed 2;
+    16..128 splits with the LSE merge, all equal to the oracle and to each other."""
+    _say(f"decode split-k 32k store={store} seed=2")
+    rng = np.random.default_rng(2)
+    qn, kn, sk = layer_weights(rng)
+    n = 32768
+    kv = fa.KVLayer(is_swa=False, has_rope=False, n_slots=n + 32, kv_dtype=store, q_norm=qn, k_norm=kn, sinks=sk)
+    L = oracle_layer(kv, qn, kn, sk, store)
+    K, V = _history(rng, n + 1, store, outlier_frac=0.01)
+    _fill_cache(kv, K[:n], V[:n], np.arange(n))
+    qkv = rng.standard_normal(QKV_DIM).astype(np.float32)
+    dq = torch.from_numpy(qkv).to(cuda)
+    want = fo.decode_step(L, qkv, n, K.copy(), V.copy(), n_threads=8)
+    outs = {}
+    for kps in (0, 256, 512, 1024, 2048, 32768):  # auto, 128, 64, 32, 16, 1 splits
+        att = torch.zeros(Q_DIM, device=cuda)
+        kv.decode(dq, att, n, keys_per_split=kps)
+        torch.cuda.synchronize()
+        outs[kps] = att.cpu().numpy()
+        assert_close(outs[kps], want, f"keys_per_split={kps}")
+    for kps, o in outs.items():
+        np.testing.assert_allclose(o, outs[32768], rtol=0, atol=2e-5 * max(1.0, np.abs(want).max()))
+    # the current token's K/V landed in slot n
+    vc = kv.v[0, :, :, n].float().cpu().numpy()
+    assert np.array_equal(vc, fo.round_store(qkv[4608:], store).reshape(N_HEAD_KV, HEAD_DIM))
+
+
+def test_decode_edge_positions_and_sinks(cuda):
+    """pos 0 (current token only), 1, 31/32/33 around a tile edge, extreme sinks."""
+    _say("decode edge positions and sinks")
+    rng = np.random.default_rng(21)
+    for sink_val in (None, -30.0, 30.0):
+        qn, kn, sk = layer_weights(rng)
+        if sink_val is not None:
+            sk[:] = sink_val
+        kv = fa.KVLayer(is_swa=False, has_rope=True, n_slots=128, kv_dtype="f16", q_norm=qn, k_norm=kn, sinks=sk)
+        L = oracle_layer(kv, qn, kn, sk, "f16")
+        n = 70
+        qkv = rng.standard_normal((n, QKV_DIM)).astype(np.float32)
+        dq = torch.from_numpy(qkv).to(cuda)
+        att = torch.zeros((n, Q_DIM), device=cuda)
+        for pos in range(n):
+            kv.decode(dq[pos], att[pos], pos)
+        torch.cuda.synchronize()
+        K = np.zeros((n, KV_DIM), np.float32)
+        V = np.zeros((n, KV_DIM), np.float32)
+        want = fo.prefill(L, qkv, 0, K, V)
+        assert_close(att.cpu().numpy(), want, f"sink={sink_val}")
+
+
+@pytest.mark.parametrize("is_swa", [False, True])
+def test_decode_batch_matches_single(cuda, is_swa):
+    """Independent sequences at mixed positions in one launch == one launch per sequence == oracle."""
+    _say(f"decode batch is_swa={is_swa}")
+    rng = np.random.default_rng(4)
+    qn, kn, sk = layer_weights(rng)
+    positions = [0, 5, 700, 3000, 1025, 64]
+    n_slots = 1024 if is_swa else 3072
+    kv = fa.KVLayer(is_swa=is_swa, has_rope=is_swa, n_slots=n_slots, kv_dtype="f16", q_norm=qn, k_norm=kn,
+                    sinks=sk, n_seq=len(positions))
+    kv1 = fa.KVLayer(is_swa=is_swa, has_rope=is_swa, n_slots=n_slots, kv_dtype="f16", q_norm=qn, k_norm=kn,
+                     sinks=sk)
+    L = oracle_layer(kv, qn, kn, sk, "f16")
+    qkv = rng.standard_normal((len(positions), QKV_DIM)).astype(np.float32)
+    wants, hist = [], []
+    for s, p in enumerate(positions):
+        if not is_swa and p >= n_slots:
+            positions[s] = p = n_slots - 1
+        K, V = _history(rng, p + 1, "f16")
+        first = max(0, p - 1023) if is_swa else 0
+        _fill_cache(kv, K[first:p], V[first:p], np.arange(first, p) & (n_slots - 1) if is_swa else np.arange(p), s)
+        wants.append(fo.decode_step(L, qkv[s], p, K.copy(), V.copy(), n_threads=8))
+        hist.append((K, V, first))
+    dq = torch.from_numpy(qkv).to(cuda)
+    att = torch.zeros((len(positions), Q_DIM), device=cuda)
+    kv.decode(dq, att, positions)
+    torch.cuda.synchronize()
+    got = att.cpu().numpy()
+    for s, p in enumerate(positions):
+        assert_close(got[s], wants[s], f"seq {s} pos {p}")
+        K, V, first = hist[s]
+        _fill_cache(kv1, K[first:p], V[first:p], np.arange(first, p) & (n_slots - 1) if is_swa else np.arange(p))
+        one = torch.zeros(Q_DIM, device=cuda)
+        kv1.decode(dq[s], one, p)
+        torch.cuda.synchronize()
+        np.testing.assert_allclose(got[s], one.cpu().numpy(), rtol=0, atol=1e-5)

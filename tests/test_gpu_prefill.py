@@ -1,0 +1,180 @@
+"""Batched prefill attention on the GPU against the CPU oracle (
+the reference's own `flint test-attn` probes, chunk invariance, prefill ==
+decode), through the C ABI (flint_attn_prefill, flint_attn_engine_debug_attn).
+Tolerance: max-abs 2e-3, mean-abs 2e-4; KV cache / ring slot contents
+bit-exact for V and within 1 ulp for K."""
+import numpy as np
+import pytest
+import torch
+
+import flint_attn as fa
+import oracle as fo
+from helpers import HEAD_DIM, KV_DIM, N_HEAD_KV, QKV_DIM, Q_DIM, assert_close, layer_weights, oracle_layer
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(f"\n[gpu-test] {msg}", flush=True)
+
+
+def _oracle_history(L, qkv, p0=0, K=None, V=None):
+    """K,V history rows (normed/roped/rounded) for positions p0..p0+T-1 appended to K,V."""
+    T = qkv.shape[0]
+    if K is None:
+        K = np.zeros((p0 + T, KV_DIM), np.float32)
+        V = np.zeros((p0 + T, KV_DIM), np.float32)
+    for t in range(T):
+        _, K[p0 + t], V[p0 + t] = fo.qkv_prep(L, qkv[t], p0 + t)
+    return K, V
+
+
+def _oracle_at(L, qkv, K, V, positions, p0=0):
+    out = {}
+    for p in positions:
+        q, _, _ = fo.qkv_prep(L, qkv[p - p0], p)
+        out[p] = fo.attend(L, q, K, V, p, n_threads=8)
+    return out
+
+
+def _ulp_close(a, b, dtype):
+    a64, b64 = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    mant = 10 if dtype == "f16" else 7
+    ulp = np.maximum(np.abs(b64), 6.1e-5 if dtype == "f16" else 1e-38) * 2.0 ** -mant
+    return np.all(np.abs(a64 - b64) <= ulp * 1.0001)
+
+
+def _probes(T, extra=()):
+    base = [0, 1, 2, 31, 32, 33, 100, 511, 512, 513, 514, 1000, 1023, 1024, 1025, 2047, 2048, 3000, T - 2, T - 1]
+    rng = np.random.default_rng(99)
+    pts = set(p for p in base if 0 <= p < T) | set(int(x) for x in rng.integers(0, T, 24)) | set(extra)
+    return sorted(p for p in pts if 0 <= p < T)
+
+
+@pytest.mark.parametrize("store", ["bf16", "f16"])
+@pytest.mark.parametrize("is_swa", [False, True], ids=["full", "swa"])
+def test_prefill_4000_config4(cuda, store, is_swa):
+    """Config 4: 4000-token prompt, causal; full layer and SWA-513 layer with ring write of the last 1024."""
+    T = 4000
+    _say(f"prefill T={T} store={store} swa={is_swa} seed=3")
+    rng = np.random.default_rng(3)
+    qn, kn, sk = layer_weights(rng)
+    kv = fa.KVLayer(is_swa=is_swa, has_rope=is_swa, n_slots=1024 if is_swa else 4096, kv_dtype=store,
+                    rope_theta=1e4, q_norm=qn, k_norm=kn, sinks=sk)
+    L = oracle_layer(kv, qn, kn, sk, store)
+    qkv = rng.standard_normal((T, QKV_DIM)).astype(np.float32)
+    att = torch.zeros((T, Q_DIM), device=cuda)
+    kv.prefill(torch.from_numpy(qkv).to(cuda), att, 0)
+    torch.cuda.synchronize()
+    got = att.cpu().numpy()
+    assert np.all(np.isfinite(got))
+    K, V = _oracle_history(L, qkv)
+    want = _oracle_at(L, qkv, K, V, _probes(T))
+    for p, w in want.items():
+        assert_close(got[p], w, f"pos {p}")
+    assert_close(np.stack([got[p] for p in want]), np.stack(list(want.values())), "probes")
+    vc = kv.v[0].float().cpu().numpy()
+    kc = kv.k[0].float().cpu().numpy()
+    lo = T - 1024 if is_swa else 0
+    for p in range(lo, T):
+        s = kv.slot(p)
+        assert np.array_equal(vc[:, :, s], V[p].reshape(N_HEAD_KV, HEAD_DIM)), f"V slot {s} pos {p}"
+        assert _ulp_close(kc[:, s, :], K[p].reshape(N_HEAD_KV, HEAD_DIM), store), f"K slot {s} pos {p}"
+
+
+@pytest.mark.parametrize("il,is_swa", [(0, False), (2, True)], ids=["layer0_full_nope", "layer2_swa_rope"])
+def test_debug_attn_reference_test_attn_probes(cuda, il, is_swa):
+    """The reference's `flint test-attn` (/root/reference/src/main.mm:241-314): 1300 tokens in
+    512-token chunks, inputs uniform on [-2, 2] in steps of 0.002, probes at
+    {0,1,31,32,200,511,512,513,600,1023,1024,1100,1299} x heads {0,7,8,31}."""
+    _say(f"debug_attn test-attn probes layer {il}")
+    flags_swa = [False, False, True]
+    eng = fa.Engine(flags_swa, flags_swa, n_ctx=4096, kv_dtype="f16", rope_theta=1e4)
+    rng = np.random.default_rng(11 + il)
+    qn, kn, sk = layer_weights(rng)
+    eng.set_weights(il, qn, kn, sk)
+    n = 1300
+    qkv = (rng.integers(0, 2001, (n, QKV_DIM)) - 1000).astype(np.float32) / 500.0
+    got = eng.debug_attn(il, qkv, 512)
+    L = fo.Layer(qn, kn, sk, is_swa, is_swa, "f16", 1e4)
+    K, V = _oracle_history(L, qkv)
+    probes = [0, 1, 31, 32, 200, 511, 512, 513, 600, 1023, 1024, 1100, 1299]
+    want = _oracle_at(L, qkv, K, V, probes)
+    heads = [0, 7, 8, 31]
+    sel = lambda a: np.concatenate([a[h * HEAD_DIM:(h + 1) * HEAD_DIM] for h in heads])
+    g = np.stack([sel(got[p]) for p in probes])
+    w = np.stack([sel(want[p]) for p in probes])
+    assert_close(g, w, "test-attn probes")
+    rel = np.abs(g - w).max() / np.sqrt(np.mean(w.astype(np.float64) ** 2))
+    assert rel < 2e-2  # the reference's own pass criterion (main.mm:308)
+    eng.close()
+
+
+@pytest.mark.parametrize("is_swa", [False, True], ids=["full", "swa"])
+def test_prefill_chunk_invariance_and_continuation(cuda, is_swa):
+    """Chunked prefill (p0 > 0 continuations, including chunks larger than the ring
+    headroom) equals one-shot prefill and the oracle."""
+    n = 1300
+    _say(f"prefill chunk invariance swa={is_swa} n={n}")
+    rng = np.random.default_rng(31)
+    qn, kn, sk = layer_weights(rng)
+    qkv = rng.standard_normal((n, QKV_DIM)).astype(np.float32)
+    L = fo.Layer(qn, kn, sk, is_swa, True, "f16", 1e4)
+    K, V = _oracle_history(L, qkv)
+    want = _oracle_at(L, qkv, K, V, _probes(n, extra=range(590, 610)))
+    outs = {}
+    for chunk in (n, 512, 600, 97, 1):
+        eng = fa.Engine([is_swa], [True], n_ctx=2048, kv_dtype="f16", rope_theta=1e4)
+        eng.set_weights(0, qn, kn, sk)
+        outs[chunk] = eng.debug_attn(0, qkv, chunk)
+        eng.close()
+        for p, w in want.items():
+            assert_close(outs[chunk][p], w, f"chunk {chunk} pos {p}")
+    for chunk, o in outs.items():
+        assert_close(o, outs[n], f"chunk {chunk} vs one-shot", max_abs=1e-3, mean_abs=5e-5)
+
+
+@pytest.mark.parametrize("is_swa", [False, True], ids=["full", "swa"])
+def test_prefill_equals_decode(cuda, is_swa):
+    """Prefill of 700 tokens == 700 decode steps (outputs within tolerance, V caches bit-identical)."""
+    n = 700
+    _say(f"prefill == decode swa={is_swa} n={n}")
+    rng = np.random.default_rng(41)
+    qn, kn, sk = layer_weights(rng)
+    mk = lambda: fa.KVLayer(is_swa=is_swa, has_rope=True, n_slots=1024, kv_dtype="f16", q_norm=qn, k_norm=kn,
+                            sinks=sk)
+    a, b = mk(), mk()
+    qkv = rng.standard_normal((n, QKV_DIM)).astype(np.float32)
+    dq = torch.from_numpy(qkv).to(cuda)
+    att_p = torch.zeros((n, Q_DIM), device=cuda)
+    att_d = torch.zeros((n, Q_DIM), device=cuda)
+    a.prefill(dq, att_p, 0)
+    for pos in range(n):
+        b.decode(dq[pos], att_d[pos], pos)
+    torch.cuda.synchronize()
+    assert_close(att_p.cpu().numpy(), att_d.cpu().numpy(), "prefill vs decode")
+    assert torch.equal(a.v, b.v)
+    kd = (a.k.float() - b.k.float()).abs()
+    assert float(kd.max()) <= float(b.k.float().abs().max()) * 2 ** -10
+
+
+def test_prefill_short_and_odd_shapes(cuda):
+    """T = 1, 33, 65 at p0 = 0 and at p0 = 1000 across the ring wrap (SWA), bf16."""
+    _say("prefill short/odd shapes")
+    rng = np.random.default_rng(51)
+    qn, kn, sk = layer_weights(rng)
+    L = fo.Layer(qn, kn, sk, True, True, "bf16", 1e4)
+    total = 1000 + 65
+    qkv = rng.standard_normal((total, QKV_DIM)).astype(np.float32)
+    K, V = _oracle_history(L, qkv)
+    for T in (1, 33, 65):
+        for p0 in (0, 1000):
+            kv = fa.KVLayer(is_swa=True, has_rope=True, kv_dtype="bf16", q_norm=qn, k_norm=kn, sinks=sk)
+            if p0:
+                pre = torch.zeros((p0, Q_DIM), device=cuda)
+                kv.prefill(torch.from_numpy(qkv[:p0]).to(cuda), pre, 0)
+            att = torch.zeros((T, Q_DIM), device=cuda)
+            kv.prefill(torch.from_numpy(qkv[p0:p0 + T]).to(cuda), att, p0)
+            torch.cuda.synchronize()
+            want = _oracle_at(L, qkv, K, V, range(p0, p0 + T))
+            assert_close(att.cpu().numpy(), np.stack([want[p] for p in range(p0, p0 + T)]), f"T={T} p0={p0}")
