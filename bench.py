@@ -32,6 +32,31 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def graph_replay_ms(torch, step, reps, warmup=2):
+    """Capture `step` (a sequence of library launches on the current stream) into a HIP graph,
+    replay it `reps` times between two events, return ms per replay. Graph replay keeps the
+    host's per-launch cost (Python + ctypes + hipLaunchKernel) out of the GPU timeline."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(warmup):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
 def decode_bytes(n_keys):
     return n_keys * 4 * 128 * 2 * 2  # K and V, f16, 4 kv heads
 
@@ -55,31 +80,15 @@ def bench_decode_32k(torch, fa, steps, warmup, n_layers=8, ctx=32768):
         layers.append(kv)
     qkv = torch.randn((n_layers, 5120), device=dev)
     att = torch.empty((n_layers, 4096), device=dev)
-    stream = torch.cuda.current_stream()
 
     def step():
         for i, kv in enumerate(layers):
             kv.decode(qkv[i], att[i], ctx)
 
-    for _ in range(warmup):
-        step()
-    torch.cuda.synchronize()
-    # per-launch events over the timed region (same stream the kernels run on)
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps * n_layers + 1)]
     t0 = time.perf_counter()
-    ev[0].record(stream)
-    k = 1
-    for _ in range(steps):
-        for i, kv in enumerate(layers):
-            kv.decode(qkv[i], att[i], ctx)
-            ev[k].record(stream)
-            k += 1
-    torch.cuda.synchronize()
+    ms_per_step = graph_replay_ms(torch, step, steps, warmup)
     wall = time.perf_counter() - t0
-    per_launch_ms = [ev[j].elapsed_time(ev[j + 1]) for j in range(steps * n_layers)]
-    total_ms = ev[0].elapsed_time(ev[-1])
-    avg_launch_ms = sum(per_launch_ms) / len(per_launch_ms)
-    ms_per_step = total_ms / steps
+    avg_launch_ms = ms_per_step / n_layers
     nbytes = decode_bytes(ctx)
     del layers
     torch.cuda.empty_cache()
@@ -100,17 +109,12 @@ def bench_decode_swa(torch, fa, reps=200, pos=32768):
         kv.v.normal_()
     qkv = torch.randn((n, 5120), device=dev)
     att = torch.empty((n, 4096), device=dev)
-    for i, kv in enumerate(layers):
-        kv.decode(qkv[i], att[i], pos)
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for r in range(reps):
-        i = r % n
-        layers[i].decode(qkv[i], att[i], pos)
-    e1.record()
-    torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / reps
+
+    def step():
+        for i, kv in enumerate(layers):
+            kv.decode(qkv[i], att[i], pos)
+
+    return graph_replay_ms(torch, step, max(1, reps // n)) / n
 
 
 def bench_prefill(torch, fa, T=4000, reps=10):
@@ -164,15 +168,7 @@ def bench_config5(torch, fa, steps=3):
         for kv in layers:
             kv.decode(qkv, att, ctx)
 
-    step()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(steps):
-        step()
-    e1.record()
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / steps
+    ms = graph_replay_ms(torch, step, steps, warmup=1)
     nbytes = sum(12 * decode_bytes(c) + 36 * decode_bytes(min(c, 512)) for c in ctx)
     del layers
     torch.cuda.empty_cache()

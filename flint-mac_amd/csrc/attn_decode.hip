@@ -145,21 +145,18 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const DecodeParams P) 
             sc[r] = s0[r] + __shfl_xor(s0[r], 8, 64);
             sc[4 + r] = s1[r] + __shfl_xor(s1[r], 8, 64);
         }
-        const bool partial_tile = kb < k_begin || kb + 32 > pos;
+        const bool partial_tile = kb < k_begin || kb + 32 > pos;  // wave-uniform
         if (partial_tile) {
+            // keys outside [k_begin, pos) get score -inf and V = 0 (their slots may hold
+            // stale data, and 0 * inf is nan)
 #pragma unroll
             for (int j = 0; j < 8; j++) {
                 const int key = kb + 8 * g + j;
-                if (key < k_begin || key >= pos) sc[j] = -INFINITY;
+                const bool ok = (key >= k_begin) & (key < pos);
+                sc[j] = ok ? sc[j] : -INFINITY;
+#pragma unroll
+                for (int d = 0; d < 8; d++) vraw[d][j] = ok ? vraw[d][j] : (uint16_t)0;
             }
-            // masked keys also get V = 0: their slots may hold stale data, and 0 * inf is nan
-#pragma unroll
-            for (int d = 0; d < 8; d++)
-#pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    const int key = kb + 8 * g + j;
-                    if (key < k_begin || key >= pos) vraw[d][j] = 0;
-                }
         }
         float mt = sc[0];
 #pragma unroll
@@ -321,27 +318,47 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const DecodeParams P) 
 }
 
 // LSE merge of the split partials plus the sink (fused.metal:331-350).
-// grid = (N_HEAD, n_seq), 128 threads (one per dim).
-__global__ __launch_bounds__(128) void attn_combine_kernel(const DecodeParams P) {
-    const int hh = blockIdx.x, seq = blockIdx.y, dim = threadIdx.x;
+// grid = (N_HEAD, n_seq), 256 threads: the split weights are computed once per
+// split (threads over splits), then each thread sums one dim over half the splits.
+constexpr int MAX_SPLIT = 1024;
+__global__ __launch_bounds__(256) void attn_combine_kernel(const DecodeParams P) {
+    __shared__ float w_s[MAX_SPLIT];
+    __shared__ float red[2][8];
+    __shared__ float half_acc[HEAD_DIM];
+    const int hh = blockIdx.x, seq = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int ns = P.split_prefix[seq + 1] - P.split_prefix[seq];
     if (ns <= 1) return;  // written directly by the decode kernel
     const float *pp = P.partial + ((size_t)seq * N_HEAD + hh) * P.max_split * PART_STRIDE;
     const float sink = P.sinks[hh] * LOG2E;
     float M = sink;
-    for (int s = 0; s < ns; s++) {
+    for (int s = tid; s < ns; s += 256) {
         const float ls = pp[s * PART_STRIDE + HEAD_DIM + 1];
         if (ls != 0.f) M = fmaxf(M, pp[s * PART_STRIDE + HEAD_DIM]);
     }
-    float L = exp2f(sink - M), A = 0.f;
-    for (int s = 0; s < ns; s++) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) M = wave_max_xor(M, o);
+    if (lane == 0) red[0][wave] = M;
+    __syncthreads();
+    M = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
+    float L = 0.f;
+    for (int s = tid; s < ns; s += 256) {
         const float ls = pp[s * PART_STRIDE + HEAD_DIM + 1];
-        if (ls == 0.f) continue;
-        const float c = exp2f(pp[s * PART_STRIDE + HEAD_DIM] - M);
-        L += ls * c;
-        A += pp[s * PART_STRIDE + dim] * c;
+        const float w = ls != 0.f ? exp2f(pp[s * PART_STRIDE + HEAD_DIM] - M) : 0.f;
+        w_s[s] = w;
+        L += ls * w;
     }
-    P.att[(size_t)seq * Q_DIM + hh * HEAD_DIM + dim] = A / L;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) L = wave_sum_xor(L, o);
+    if (lane == 0) red[1][wave] = L;
+    __syncthreads();
+    L = red[1][0] + red[1][1] + red[1][2] + red[1][3] + exp2f(sink - M);
+    const int dim = tid & 127, part = tid >> 7;
+    float A = 0.f;
+#pragma unroll 8
+    for (int s = part; s < ns; s += 2) A += pp[s * PART_STRIDE + dim] * w_s[s];
+    if (part == 1) half_acc[dim] = A;
+    __syncthreads();
+    if (part == 0) P.att[(size_t)seq * Q_DIM + hh * HEAD_DIM + dim] = (A + half_acc[dim]) / L;
 }
 
 hipError_t launch_decode(const DecodeParams &P, int dtype, int total_splits, hipStream_t stream) {
@@ -355,7 +372,7 @@ hipError_t launch_decode(const DecodeParams &P, int dtype, int total_splits, hip
     bool need_combine = false;
     for (int s = 0; s < P.n_seq; s++) need_combine |= (P.split_prefix[s + 1] - P.split_prefix[s]) > 1;
     if (need_combine) {
-        hipLaunchKernelGGL(attn_combine_kernel, dim3(N_HEAD, P.n_seq), dim3(128), 0, stream, P);
+        hipLaunchKernelGGL(attn_combine_kernel, dim3(N_HEAD, P.n_seq), dim3(256), 0, stream, P);
         e = hipGetLastError();
     }
     return e;

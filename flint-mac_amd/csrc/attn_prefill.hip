@@ -180,6 +180,10 @@ __global__ __launch_bounds__(256) void flash_prefill_kernel(const PrefillParams 
     const int tile_lo = (k_lo - P.kbase) / PF_BK, tile_hi = (q_last - P.kbase) / PF_BK;
     const int n_valid = P.p0 + P.T - P.kbase;  // rows holding keys
     const int sig = pf_sigma(col);
+    // this lane's query row attends to key positions [key_lo, key_hi] (causal, SWA window);
+    // rows past T attend to nothing
+    const int key_hi = row_ok ? my_qp : -1;
+    const int key_lo = P.is_swa ? max(my_qp - (P.window - 1), 0) : 0;
 
     for (int kt = tile_lo; kt <= tile_hi; kt++) {
         const int r0 = kt * PF_BK;  // first row of the tile
@@ -213,8 +217,9 @@ __global__ __launch_bounds__(256) void flash_prefill_kernel(const PrefillParams 
         __syncthreads();
 
         const int kp0 = P.kbase + r0;  // key position of row 0
+        // wave-uniform: does any row of this block need masking in this tile?
         const bool need_mask = kp0 + PF_BK - 1 > q_first || (P.is_swa && q_last - kp0 >= P.window) ||
-                               r0 + PF_BK > n_valid || !row_ok || t0 + PF_BQ > P.T;
+                               t0 + PF_BQ > P.T;
 #pragma unroll
         for (int qt = 0; qt < 2; qt++) {
             f32x16 s = {};
@@ -226,9 +231,8 @@ __global__ __launch_bounds__(256) void flash_prefill_kernel(const PrefillParams 
                 for (int e = 0; e < 16; e++) {
                     const int j = e >> 2, r = e & 3;
                     const int kp = kp0 + 16 * (j >> 1) + 8 * hh + 4 * (j & 1) + r;
-                    const bool ok = row_ok && kp <= my_qp && (!P.is_swa || my_qp - kp < P.window) &&
-                                    kp - P.kbase < n_valid;
-                    if (!ok) s[e] = -INFINITY;
+                    const bool ok = (kp >= key_lo) & (kp <= key_hi);
+                    s[e] = ok ? s[e] : -INFINITY;
                 }
             }
             float mt = s[0];

@@ -154,6 +154,7 @@ void decode_impl(const flint_attn_layer *L, int n_seq, int64_t seq_stride, const
     }
     P.split_prefix[n_seq] = total;
     P.max_split = max_split;
+    if (max_split > 1024) throw Error("too many key splits (max 1024): raise keys_per_split");
     if (max_split > 1) {
         const size_t need = (size_t)n_seq * N_HEAD * max_split * PART_STRIDE * sizeof(float);
         P.partial = (float *)scratch().partial.get(need);

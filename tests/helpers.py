@@ -49,3 +49,13 @@ def to_cache_layout(K, V, n_slots, slots):
     Kc[:, slots, :] = Kh.transpose(1, 0, 2)
     Vc[:, :, slots] = Vh.transpose(1, 2, 0)
     return Kc, Vc
+
+
+def k_close(a, b, dtype):
+    """Cache K written by the GPU vs the oracle's: both normalise (and rotate) in fp32 before
+    rounding to the 16-bit type, so a value may land one unit in the last place away, and
+    values that RoPE brings near zero by cancellation may differ by the fp32 error (~1e-7)."""
+    a64, b64 = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    mant = 10 if dtype == "f16" else 7
+    ulp = np.abs(b64) * 2.0 ** -mant
+    return bool(np.all(np.abs(a64 - b64) <= ulp * 1.0001 + 1e-5))

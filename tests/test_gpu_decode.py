@@ -9,7 +9,7 @@ import torch
 
 import flint_attn as fa
 import oracle as fo
-from helpers import (HEAD_DIM, KV_DIM, N_HEAD_KV, QKV_DIM, Q_DIM, assert_close, layer_weights, oracle_layer,
+from helpers import (HEAD_DIM, k_close, KV_DIM, N_HEAD_KV, QKV_DIM, Q_DIM, assert_close, layer_weights, oracle_layer,
                      to_cache_layout)
 
 pytestmark = pytest.mark.gpu
@@ -35,13 +35,6 @@ def _history(rng, n, store, outlier_frac=0.0):
         V[rng.random(n) < outlier_frac] *= 8
     return fo.round_store(K, store), fo.round_store(V, store)
 
-
-def _ulp_close(a, b, dtype):
-    """|a - b| <= 1 ulp of the 16-bit type at b's magnitude."""
-    a64, b64 = np.asarray(a, np.float64), np.asarray(b, np.float64)
-    mant = 10 if dtype == "f16" else 7
-    ulp = np.maximum(np.abs(b64), 6.1e-5 if dtype == "f16" else 1e-38) * 2.0 ** -mant
-    return np.all(np.abs(a64 - b64) <= ulp * 1.0001)
 
 
 @pytest.mark.parametrize("store", ["f16", "bf16"])
@@ -72,7 +65,7 @@ def test_decode_swa_ring_steps_config2(cuda, store):
     for p in range(max(0, n - 1024), n):
         s = p & 1023
         assert np.array_equal(vc[:, :, s], V[p].reshape(N_HEAD_KV, HEAD_DIM)), f"V slot {s} pos {p}"
-        assert _ulp_close(kc[:, s, :], K[p].reshape(N_HEAD_KV, HEAD_DIM), store), f"K slot {s} pos {p}"
+        assert k_close(kc[:, s, :], K[p].reshape(N_HEAD_KV, HEAD_DIM), store), f"K slot {s} pos {p}"
 
 
 def test_decode_full_rope_config1(cuda):

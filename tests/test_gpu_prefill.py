@@ -9,7 +9,7 @@ import torch
 
 import flint_attn as fa
 import oracle as fo
-from helpers import HEAD_DIM, KV_DIM, N_HEAD_KV, QKV_DIM, Q_DIM, assert_close, layer_weights, oracle_layer
+from helpers import HEAD_DIM, KV_DIM, N_HEAD_KV, QKV_DIM, Q_DIM, assert_close, k_close, layer_weights, oracle_layer
 
 pytestmark = pytest.mark.gpu
 
@@ -36,12 +36,6 @@ def _oracle_at(L, qkv, K, V, positions, p0=0):
         out[p] = fo.attend(L, q, K, V, p, n_threads=8)
     return out
 
-
-def _ulp_close(a, b, dtype):
-    a64, b64 = np.asarray(a, np.float64), np.asarray(b, np.float64)
-    mant = 10 if dtype == "f16" else 7
-    ulp = np.maximum(np.abs(b64), 6.1e-5 if dtype == "f16" else 1e-38) * 2.0 ** -mant
-    return np.all(np.abs(a64 - b64) <= ulp * 1.0001)
 
 
 def _probes(T, extra=()):
@@ -79,7 +73,7 @@ def test_prefill_4000_config4(cuda, store, is_swa):
     for p in range(lo, T):
         s = kv.slot(p)
         assert np.array_equal(vc[:, :, s], V[p].reshape(N_HEAD_KV, HEAD_DIM)), f"V slot {s} pos {p}"
-        assert _ulp_close(kc[:, s, :], K[p].reshape(N_HEAD_KV, HEAD_DIM), store), f"K slot {s} pos {p}"
+        assert k_close(kc[:, s, :], K[p].reshape(N_HEAD_KV, HEAD_DIM), store), f"K slot {s} pos {p}"
 
 
 @pytest.mark.parametrize("il,is_swa", [(0, False), (2, True)], ids=["layer0_full_nope", "layer2_swa_rope"])
