@@ -10,15 +10,28 @@
 // the key range with a log-sum-exp merge.
 //
 // MI355X design:
-//  * One workgroup per (kv head, key split) serves all 8 q heads of the GQA
-//    group, so every K/V byte is read from HBM once (the reference re-reads
-//    K/V per q head).
-//  * KV layout is head-major: K [kvh][slot][128], V transposed [kvh][128][slot],
-//    so both MFMA operands are single 16-byte loads straight from HBM.
+//  * One 8-wave workgroup per (sequence, kv head, key split) serves all 8 q
+//    heads of the GQA group, so every K/V byte is read from HBM once (the
+//    reference re-reads K/V per q head).
+//  * KV layout is head-major: K [kvh][slot][128], V transposed in 32-slot tiles
+//    [kvh][slot/32][128][32], so a 32-key tile is two contiguous 8 KiB blocks and
+//    both MFMA operands are single 16-byte loads straight from HBM.
 //  * Scores are S^T = K * Q^T on v_mfma_f32_16x16x32: the 16 MFMA columns carry
 //    the 8 heads' q split into hi + lo halves of the 16-bit type, so the scores
 //    are fp32-accurate at no extra MFMA cost; P*V uses the same hi/lo trick on P.
-//  * A tile is 32 keys: 16 x 16-byte loads per lane (16 KiB per wave) in flight.
+//  * A tile is 32 keys (16 x 16-byte loads per lane, 16 KiB per wave). Each
+//    wave keeps two tiles in flight, and a tile's registers are refilled as
+//    soon as it is consumed; the first is requested before the prologue.
+//  * Compact code on the critical path: each wave runs the straight-line
+//    parts of the kernel once, from a cold instruction cache, so the q / k
+//    normalisation is cooperative (one q head per wave, a NEOX pair per lane)
+//    and hands the MFMA operands over through LDS, and the current token
+//    joins the block merge as one more partial.
+//  * Every split writes its partial (m, l, acc); a second, short kernel merges
+//    them (fused.metal:331-350), 8 split groups x 32 dim groups per head. (A
+//    last-block merge inside the streaming kernel needs an agent-scope
+//    release/acquire per block and funnels every partial through one CU, which
+//    measured slower than the kernel boundary.)
 //  * Batched entry: blockIdx.x walks a flattened (sequence, split) table so one
 //    launch serves many independent sequences (one token each).
 #include "common.h"
@@ -28,313 +41,360 @@ namespace flint {
 
 // partial record per (seq, head, split): acc[128], m (log2 units), l, 2 pad
 constexpr int PART_STRIDE = 132;
+constexpr int DEC_WAVES = 8;
+constexpr int DEC_THREADS = DEC_WAVES * 64;
+constexpr int MERGE_MAX_SPLIT = 1024;
+
+struct KvTile {
+    u32x4 k[2][4];  // K rows: sub-tile st, dim chunk c (8 packed 16-bit values each)
+    u32x4 v[8];     // V^T rows: dim tile d
+};
+
+// Issue the 16 loads of tile t (keys 32t .. 32t+31) for this lane. kc / vc are
+// wave-uniform bases; offsets stay 32-bit (a kv head's cache is < 2^31 elements)
+// so the loads take the scalar-base + vector-offset form.
+__device__ inline void load_tile(KvTile &T, const uint16_t *__restrict__ kc, const uint16_t *__restrict__ vc,
+                                 int t, int n, int g, int slot_mask, int n_slots) {
+    const uint32_t kb = (uint32_t)t * 32;
+#pragma unroll
+    for (int st = 0; st < 2; st++) {
+        // MFMA row i = n holds key kb + 8(i/4) + 4st + (i%4)
+        const uint32_t key = kb + 8 * (n >> 2) + 4 * st + (n & 3);
+        const uint32_t ko = (key & (uint32_t)slot_mask) * HEAD_DIM + 8 * g;
+#pragma unroll
+        for (int c = 0; c < 4; c++) T.k[st][c] = __builtin_nontemporal_load((const u32x4 *)(kc + ko + 32 * c));
+    }
+    // V^T tile of slots kb..kb+31 (8 KiB contiguous): row = dim 16d + n, keys kb + 8g .. +7
+    const uint32_t vo = ((kb & (uint32_t)slot_mask) * HEAD_DIM) + n * 32 + 8 * g;
+#pragma unroll
+    for (int d = 0; d < 8; d++) T.v[d] = __builtin_nontemporal_load((const u32x4 *)(vc + vo + 16 * d * 32));
+}
 
 template <int DT>
-__global__ __launch_bounds__(256) void attn_decode_kernel(const DecodeParams P) {
+struct DecodeState {
+    typedef typename KvType<DT>::vec8 vec8;
+    float m, l;      // running max (log2 units) of this lane's head, this lane's partial sum
+    f32x4 acc[8];    // O^T tile d: rows = dims 16d + 4g + r, column = this lane's (head, hi/lo)
+};
+
+// Online-softmax update with one 32-key tile.
+template <int DT>
+__device__ inline void consume_tile(DecodeState<DT> &S, KvTile &T, const typename KvType<DT>::vec8 (&qb)[4], int t,
+                                    int k_begin, int pos, int g, int hl) {
+    typedef KvType<DT> KT;
+    f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        s0 = KT::mfma16(__builtin_bit_cast(typename KT::vec8, T.k[0][c]), qb[c], s0);
+        s1 = KT::mfma16(__builtin_bit_cast(typename KT::vec8, T.k[1][c]), qb[c], s1);
+    }
+    float sc[8];  // keys kb + 8g + j: j < 4 from s0, j >= 4 from s1; hi + lo columns summed
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        sc[r] = s0[r] + __shfl_xor(s0[r], 8, 64);
+        sc[4 + r] = s1[r] + __shfl_xor(s1[r], 8, 64);
+    }
+    const int kb = t * 32;
+    if (kb < k_begin || kb + 32 > pos) {  // wave-uniform: a tile at either end of the key range
+        // keys outside [k_begin, pos) get score -inf and V = 0 (their slots may hold
+        // stale data, and 0 * inf is nan); V words hold keys (2w, 2w+1)
+        uint32_t vmask[4];
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            const int key = kb + 8 * g + 2 * w;
+            const bool ok0 = (key >= k_begin) & (key < pos), ok1 = (key + 1 >= k_begin) & (key + 1 < pos);
+            sc[2 * w] = ok0 ? sc[2 * w] : -INFINITY;
+            sc[2 * w + 1] = ok1 ? sc[2 * w + 1] : -INFINITY;
+            vmask[w] = (ok0 ? 0x0000ffffu : 0u) | (ok1 ? 0xffff0000u : 0u);
+        }
+#pragma unroll
+        for (int d = 0; d < 8; d++)
+#pragma unroll
+            for (int w = 0; w < 4; w++) T.v[d][w] &= vmask[w];
+    }
+    float mt = sc[0];
+#pragma unroll
+    for (int j = 1; j < 8; j++) mt = fmaxf(mt, sc[j]);
+    mt = wave_max_xor(mt, 16);
+    mt = wave_max_xor(mt, 32);
+    const float m_new = fmaxf(S.m, mt);
+    const float corr = exp2f(S.m - m_new);
+    float psum = 0.f;
+    uint16_t ph[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const float p = exp2f(sc[j] - m_new);
+        psum += p;
+        const uint16_t hi = KT::from_float(p);
+        const uint16_t lo = KT::from_float(p - KT::to_float(hi));
+        ph[j] = hl ? lo : hi;
+    }
+    const u32x4 pu = {pack2(ph[0], ph[1]), pack2(ph[2], ph[3]), pack2(ph[4], ph[5]), pack2(ph[6], ph[7])};
+    S.l = S.l * corr + psum;
+    S.m = m_new;
+    const typename KT::vec8 pb = __builtin_bit_cast(typename KT::vec8, pu);
+#pragma unroll
+    for (int d = 0; d < 8; d++) {
+        S.acc[d] *= corr;
+        S.acc[d] = KT::mfma16(__builtin_bit_cast(typename KT::vec8, T.v[d]), pb, S.acc[d]);
+    }
+}
+
+// sin/cos of a RoPE angle (a float, as the reference computes it): the angle
+// reaches ~6.5e4 rad at long context, so it is first reduced modulo 2*pi in
+// double precision (error ~1e-11 rad) to keep sincosf on its short path.
+__device__ inline void rope_sincos(float a, float *sn, float *cs) {
+    const double twopi = 6.283185307179586476925286766559;
+    const double r = (double)a - twopi * rint((double)a * (1.0 / twopi));
+    sincosf((float)r, sn, cs);
+}
+
+// RMSNorm (+ NEOX RoPE) of one 128-dim head row by one wave: lane holds dims
+// lane and lane + 64 (a NEOX pair, x) with their gains (w), cs/sn the rotation
+// of frequency `lane`.
+__device__ inline float2 norm_rope_pair(float2 x, float2 w, float eps, bool rope, float cs, float sn) {
+    float ss = x.x * x.x + x.y * x.y;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    const float scale = 1.0f / sqrtf(ss / HEAD_DIM + eps);
+    float x0 = x.x * scale * w.x, x1 = x.y * scale * w.y;
+    if (rope) {
+        const float y0 = x0 * cs - x1 * sn, y1 = x0 * sn + x1 * cs;
+        x0 = y0;
+        x1 = y1;
+    }
+    return make_float2(x0, x1);
+}
+
+// Accumulators of splits s0 + sg + 4i (i < 16), dims 8c..8c+7, for the final merge.
+// Indices past the last split are clamped to it (their weight is zero).
+__device__ inline void fetch_partials(float4 (&xa)[16], float4 (&xb)[16], const float *__restrict__ hp, int s0,
+                                      int n_split, int sg, int c) {
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const int sp = min(s0 + sg + 4 * i, n_split - 1);
+        xa[i] = *(const float4 *)(hp + sp * PART_STRIDE + 8 * c);
+        xb[i] = *(const float4 *)(hp + sp * PART_STRIDE + 8 * c + 4);
+    }
+}
+
+template <int DT>
+__global__ __launch_bounds__(DEC_THREADS) void attn_decode_kernel(const DecodeParams P) {
     typedef KvType<DT> KT;
     typedef typename KT::vec8 vec8;
 
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n = lane & 15, g = lane >> 4;   // MFMA column (q head x hi/lo) and k-group
     const int hloc = n & 7, hl = n >> 3;      // head within the GQA group, 0 = hi half, 1 = lo half
     const int kvh = blockIdx.y;
-    const int h = kvh * GQA + hloc;
 
     // ---- which sequence / split this block serves ----
     int seq = 0;
     while (seq + 1 < P.n_seq && (int)blockIdx.x >= P.split_prefix[seq + 1]) seq++;
     const int split = blockIdx.x - P.split_prefix[seq];
     const int n_split = P.split_prefix[seq + 1] - P.split_prefix[seq];
+    const bool last_split = split == n_split - 1;
     const int pos = P.pos[seq];
     const int k_begin = P.is_swa ? max(pos - (P.window - 1), 0) : 0;
     const int tile_lo = k_begin >> 5, tile_hi = (pos + 31) >> 5;  // tiles holding keys [k_begin, pos)
     const int tps = P.tiles_per_split[seq];
     const int t_begin = tile_lo + split * tps;
     const int t_end = min(t_begin + tps, tile_hi);
+    const int slot_mask = P.slot_mask;
 
     const uint16_t *__restrict__ kc = P.k_cache + (size_t)seq * P.seq_stride + (size_t)kvh * P.n_slots * HEAD_DIM;
     const uint16_t *__restrict__ vc = P.v_cache + (size_t)seq * P.seq_stride + (size_t)kvh * HEAD_DIM * P.n_slots;
     const float *__restrict__ row = P.qkv + (size_t)seq * QKV_DIM;
 
-    // ---- q: RMSNorm (+ RoPE), scaled by log2(e)/sqrt(D); lane holds dims 32c + 8g + e ----
-    float q[4][8];
+    // LDS: q halves in MFMA-operand order, q in fp32, the current token, the wave merge
+    __shared__ uint16_t sm_qh[2][GQA][HEAD_DIM];   // [hi/lo][head][dim]
+    __shared__ float sm_q[GQA][HEAD_DIM];          // log2(e)/sqrt(D)-scaled q (for the current token)
+    __shared__ float sm_kv[2][HEAD_DIM];           // current token: k and v as the cache holds them
+    __shared__ float sm_acc[DEC_WAVES][GQA][HEAD_DIM];  // reused as split weights by the final merge
+    __shared__ float sm_m[DEC_WAVES + 1][GQA], sm_l[DEC_WAVES + 1][GQA];
+
+    // ---- the prologue's inputs first, then this wave's first two tiles: vmcnt counts
+    //      completions in issue order, so the prologue can wait for its own small loads
+    //      while the tiles stay in flight ----
+    const bool cur_wave = last_split && wave == DEC_WAVES - 1;  // also handles the current token
+    const float *qr = row + (kvh * GQA + wave) * HEAD_DIM;
+    const float2 qx = make_float2(qr[lane], qr[lane + 64]);
+    const float2 qw = make_float2(P.q_norm[lane], P.q_norm[lane + 64]);
+    const float rfreq = P.rope_freq[lane];
+    float2 kx = {0.f, 0.f}, kw = {0.f, 0.f}, vx = {0.f, 0.f};
+    if (cur_wave) {
+        const float *kr = row + Q_DIM + kvh * HEAD_DIM, *vr = row + Q_DIM + KV_DIM + kvh * HEAD_DIM;
+        kx = make_float2(kr[lane], kr[lane + 64]);
+        kw = make_float2(P.k_norm[lane], P.k_norm[lane + 64]);
+        vx = make_float2(vr[lane], vr[lane + 64]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // Issued unconditionally (a wave without such a tile re-reads tile t_begin, which
+    // is in range and never consumed): loads under a branch make the compiler's wait
+    // counting at the join conservative, and the prologue would then wait for the tiles.
+    KvTile ta, tb;
+    int t_a = t_begin + wave, t_b = t_a + DEC_WAVES;
+    load_tile(ta, kc, vc, t_a < t_end ? t_a : t_begin, n, g, slot_mask, P.n_slots);
+    load_tile(tb, kc, vc, t_b < t_end ? t_b : t_begin, n, g, slot_mask, P.n_slots);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- prologue: wave w normalises q head w (+ RoPE), the last split's last wave also
+    //      the current token's k and v (rounded to the cache dtype, written to slot(pos)) ----
     {
-        const float *qr = row + h * HEAD_DIM;
-        double ss = 0;
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const float4 a = *(const float4 *)(qr + 32 * c + 8 * g);
-            const float4 b = *(const float4 *)(qr + 32 * c + 8 * g + 4);
-            q[c][0] = a.x; q[c][1] = a.y; q[c][2] = a.z; q[c][3] = a.w;
-            q[c][4] = b.x; q[c][5] = b.y; q[c][6] = b.z; q[c][7] = b.w;
-#pragma unroll
-            for (int e = 0; e < 8; e++) ss += (double)q[c][e] * q[c][e];
-        }
-        ss += __shfl_xor(ss, 16, 64);
-        ss += __shfl_xor(ss, 32, 64);
-        const float scale = 1.0f / sqrtf((float)(ss / HEAD_DIM) + P.rms_eps);
-#pragma unroll
-        for (int c = 0; c < 4; c++)
-#pragma unroll
-            for (int e = 0; e < 8; e++) q[c][e] = q[c][e] * scale * P.q_norm[32 * c + 8 * g + e];
-        if (P.has_rope) {
-#pragma unroll
-            for (int c = 0; c < 2; c++)
-#pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    const int i = 32 * c + 8 * g + e;  // pairs with i + 64 = 32(c+2) + 8g + e
-                    const float a = (float)pos * P.rope_freq[i];
-                    const float cs = cosf(a), sn = sinf(a);
-                    const float x0 = q[c][e], x1 = q[c + 2][e];
-                    q[c][e] = x0 * cs - x1 * sn;
-                    q[c + 2][e] = x0 * sn + x1 * cs;
-                }
-        }
+        float cs = 1.f, sn = 0.f;  // rotation of frequency `lane`
+        if (P.has_rope) rope_sincos((float)pos * rfreq, &sn, &cs);
         const float qs = LOG2E / sqrtf((float)HEAD_DIM);
-#pragma unroll
-        for (int c = 0; c < 4; c++)
-#pragma unroll
-            for (int e = 0; e < 8; e++) q[c][e] *= qs;
-    }
-    vec8 qb[4];  // MFMA B operand: column n = this lane's head, hi or lo half
-#pragma unroll
-    for (int c = 0; c < 4; c++) {
-        u16x8 u;
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-            const uint16_t hi = KT::from_float(q[c][e]);
-            const uint16_t lo = KT::from_float(q[c][e] - KT::to_float(hi));
-            u[e] = hl ? lo : hi;
-        }
-        qb[c] = KT::as_vec(u);
-    }
-
-    // ---- stream the key tiles of this split: wave w takes tiles t_begin + w, + 4, ... ----
-    float m = -1e30f, l = 0.f;  // running max (log2 units, per head) and this lane's partial sum
-    f32x4 acc[8];
-#pragma unroll
-    for (int d = 0; d < 8; d++) acc[d] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const int slot_mask = P.slot_mask;
-
-    for (int t = t_begin + wave; t < t_end; t += 4) {
-        const int kb = t * 32;
-        // K rows: sub-tile st, MFMA row i = n holds key kb + 8(i/4) + 4st + (i%4)
-        u16x8 kraw[2][4];
-#pragma unroll
-        for (int st = 0; st < 2; st++) {
-            const int key = kb + 8 * (n >> 2) + 4 * st + (n & 3);
-            const uint16_t *kp = kc + (size_t)(key & slot_mask) * HEAD_DIM + 8 * g;
-#pragma unroll
-            for (int c = 0; c < 4; c++) kraw[st][c] = *(const u16x8 *)(kp + 32 * c);
-        }
-        // V^T: dim row 16d + n, keys kb + 8g .. kb + 8g + 7
-        u16x8 vraw[8];
-        const int vslot = (kb + 8 * g) & slot_mask;
-#pragma unroll
-        for (int d = 0; d < 8; d++) vraw[d] = *(const u16x8 *)(vc + (size_t)(16 * d + n) * P.n_slots + vslot);
-
-        f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-            s0 = KT::mfma16(KT::as_vec(kraw[0][c]), qb[c], s0);
-            s1 = KT::mfma16(KT::as_vec(kraw[1][c]), qb[c], s1);
-        }
-        float sc[8];  // keys kb + 8g + j for j = 0..7 (j < 4 from s0, j >= 4 from s1)
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            sc[r] = s0[r] + __shfl_xor(s0[r], 8, 64);
-            sc[4 + r] = s1[r] + __shfl_xor(s1[r], 8, 64);
-        }
-        const bool partial_tile = kb < k_begin || kb + 32 > pos;  // wave-uniform
-        if (partial_tile) {
-            // keys outside [k_begin, pos) get score -inf and V = 0 (their slots may hold
-            // stale data, and 0 * inf is nan)
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const int key = kb + 8 * g + j;
-                const bool ok = (key >= k_begin) & (key < pos);
-                sc[j] = ok ? sc[j] : -INFINITY;
-#pragma unroll
-                for (int d = 0; d < 8; d++) vraw[d][j] = ok ? vraw[d][j] : (uint16_t)0;
-            }
-        }
-        float mt = sc[0];
-#pragma unroll
-        for (int j = 1; j < 8; j++) mt = fmaxf(mt, sc[j]);
-        mt = wave_max_xor(mt, 16);
-        mt = wave_max_xor(mt, 32);
-        const float m_new = fmaxf(m, mt);
-        const float corr = exp2f(m - m_new);
-        float p[8], psum = 0.f;
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            p[j] = exp2f(sc[j] - m_new);
-            psum += p[j];
-        }
-        l = l * corr + psum;
-        m = m_new;
-        u16x8 pu;
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const uint16_t hi = KT::from_float(p[j]);
-            const uint16_t lo = KT::from_float(p[j] - KT::to_float(hi));
-            pu[j] = hl ? lo : hi;
-        }
-        const vec8 pb = KT::as_vec(pu);
-#pragma unroll
-        for (int d = 0; d < 8; d++) {
-            acc[d] *= corr;
-            acc[d] = KT::mfma16(KT::as_vec(vraw[d]), pb, acc[d]);
-        }
-    }
-
-    // ---- current token (last split, wave 3): k/v from registers, written to slot(pos) ----
-    if (split == n_split - 1 && wave == 3) {
-        const float *kr = row + Q_DIM + kvh * HEAD_DIM;
-        float k[4][8];
-        double ss = 0;
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const float4 a = *(const float4 *)(kr + 32 * c + 8 * g);
-            const float4 b = *(const float4 *)(kr + 32 * c + 8 * g + 4);
-            k[c][0] = a.x; k[c][1] = a.y; k[c][2] = a.z; k[c][3] = a.w;
-            k[c][4] = b.x; k[c][5] = b.y; k[c][6] = b.z; k[c][7] = b.w;
-#pragma unroll
-            for (int e = 0; e < 8; e++) ss += (double)k[c][e] * k[c][e];
-        }
-        ss += __shfl_xor(ss, 16, 64);
-        ss += __shfl_xor(ss, 32, 64);
-        const float scale = 1.0f / sqrtf((float)(ss / HEAD_DIM) + P.rms_eps);
-#pragma unroll
-        for (int c = 0; c < 4; c++)
-#pragma unroll
-            for (int e = 0; e < 8; e++) k[c][e] = k[c][e] * scale * P.k_norm[32 * c + 8 * g + e];
-        if (P.has_rope) {
-#pragma unroll
-            for (int c = 0; c < 2; c++)
-#pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    const int i = 32 * c + 8 * g + e;
-                    const float a = (float)pos * P.rope_freq[i];
-                    const float cs = cosf(a), sn = sinf(a);
-                    const float x0 = k[c][e], x1 = k[c + 2][e];
-                    k[c][e] = x0 * cs - x1 * sn;
-                    k[c + 2][e] = x0 * sn + x1 * cs;
-                }
-        }
-        u16x8 kst[4];
-        float dot = 0.f;
-#pragma unroll
-        for (int c = 0; c < 4; c++)
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                kst[c][e] = KT::from_float(k[c][e]);
-                dot += q[c][e] * KT::to_float(kst[c][e]);
-            }
-        dot = wave_sum_xor(dot, 16);
-        dot = wave_sum_xor(dot, 32);
-        const float m_new = fmaxf(m, dot);
-        const float corr = exp2f(m - m_new), pc = exp2f(dot - m_new);
-        l = l * corr + (g == 0 ? pc : 0.f);
-        m = m_new;
-        const float *vr = row + Q_DIM + KV_DIM + kvh * HEAD_DIM;
-        uint16_t vst[8][4];
-#pragma unroll
-        for (int d = 0; d < 8; d++) {
-            const float4 v4 = *(const float4 *)(vr + 16 * d + 4 * g);
-            vst[d][0] = KT::from_float(v4.x);
-            vst[d][1] = KT::from_float(v4.y);
-            vst[d][2] = KT::from_float(v4.z);
-            vst[d][3] = KT::from_float(v4.w);
-            acc[d] *= corr;
-            if (hl == 0) {
-#pragma unroll
-                for (int r = 0; r < 4; r++) acc[d][r] += pc * KT::to_float(vst[d][r]);
-            }
-        }
-        if (n == 0) {  // one lane per k-group writes this kv head's row (dims owned by the lane)
+        const float2 qv = norm_rope_pair(qx, qw, P.rms_eps, P.has_rope, cs, sn);
+        const float q0 = qv.x * qs, q1 = qv.y * qs;
+        sm_q[wave][lane] = q0;
+        sm_q[wave][lane + 64] = q1;
+        const uint16_t h0 = KT::from_float(q0), h1 = KT::from_float(q1);
+        sm_qh[0][wave][lane] = h0;
+        sm_qh[0][wave][lane + 64] = h1;
+        sm_qh[1][wave][lane] = KT::from_float(q0 - KT::to_float(h0));
+        sm_qh[1][wave][lane + 64] = KT::from_float(q1 - KT::to_float(h1));
+        if (cur_wave) {
+            // the current token: no key read by this launch lives in slot(pos) (in the ring it
+            // held pos - n_slots, outside the window)
+            const float2 kv2 = norm_rope_pair(kx, kw, P.rms_eps, P.has_rope, cs, sn);
+            const uint16_t k0 = KT::from_float(kv2.x), k1 = KT::from_float(kv2.y);
+            const uint16_t v0 = KT::from_float(vx.x), v1 = KT::from_float(vx.y);
+            sm_kv[0][lane] = KT::to_float(k0);
+            sm_kv[0][lane + 64] = KT::to_float(k1);
+            sm_kv[1][lane] = KT::to_float(v0);
+            sm_kv[1][lane + 64] = KT::to_float(v1);
             const int slot = pos & slot_mask;
-            uint16_t *kw = P.k_cache + (size_t)seq * P.seq_stride + ((size_t)kvh * P.n_slots + slot) * HEAD_DIM;
+            uint16_t *kw_ = P.k_cache + (size_t)seq * P.seq_stride + ((size_t)kvh * P.n_slots + slot) * HEAD_DIM;
+            kw_[lane] = k0;
+            kw_[lane + 64] = k1;
+            uint16_t *vw = P.v_cache + (size_t)seq * P.seq_stride;
+            vw[vt_index(kvh, slot, lane, P.n_slots)] = v0;
+            vw[vt_index(kvh, slot, lane + 64, P.n_slots)] = v1;
+        }
+    }
+    lds_barrier();  // the q operands are in LDS; the tile loads stay in flight
+    vec8 qb[4];  // MFMA B operand: column n = head hloc, hi or lo half; k = dims 32c + 8g + e
 #pragma unroll
-            for (int c = 0; c < 4; c++) *(u16x8 *)(kw + 32 * c + 8 * g) = kst[c];
-            uint16_t *vw = P.v_cache + (size_t)seq * P.seq_stride + (size_t)kvh * HEAD_DIM * P.n_slots + slot;
+    for (int c = 0; c < 4; c++) qb[c] = *(const vec8 *)&sm_qh[hl][hloc][32 * c + 8 * g];
+
+    // ---- stream this wave's tiles t_begin + wave + 8i, two in flight ----
+    DecodeState<DT> S;
+    S.m = -1e30f;
+    S.l = 0.f;
 #pragma unroll
-            for (int d = 0; d < 8; d++)
-#pragma unroll
-                for (int r = 0; r < 4; r++) vw[(size_t)(16 * d + 4 * g + r) * P.n_slots] = vst[d][r];
+    for (int d = 0; d < 8; d++) S.acc[d] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // The first pair runs straight-line (exact wait counts: consuming tile a leaves
+    // tile b in flight). Later tiles go through a loop in which b streams in while a
+    // is consumed, then moves into a's registers while the next tile is requested.
+    // The scheduling barriers keep each refill after the consumption of the tile it
+    // replaces (a third tile of registers would spill).
+    if (t_a < t_end) consume_tile<DT>(S, ta, qb, t_a, k_begin, pos, g, hl);
+    __builtin_amdgcn_sched_barrier(0);
+    if (t_b < t_end) {
+        const int t_c = t_b + DEC_WAVES;
+        if (t_c < t_end) load_tile(ta, kc, vc, t_c, n, g, slot_mask, P.n_slots);
+        __builtin_amdgcn_sched_barrier(0);
+        consume_tile<DT>(S, tb, qb, t_b, k_begin, pos, g, hl);
+        __builtin_amdgcn_sched_barrier(0);
+        t_a = t_c;
+        t_b = t_c + DEC_WAVES;
+        if (t_b < t_end) load_tile(tb, kc, vc, t_b, n, g, slot_mask, P.n_slots);
+        __builtin_amdgcn_sched_barrier(0);
+        while (t_a < t_end) {
+            consume_tile<DT>(S, ta, qb, t_a, k_begin, pos, g, hl);
+            __builtin_amdgcn_sched_barrier(0);
+            ta = tb;
+            t_a = t_b;
+            t_b += DEC_WAVES;
+            if (t_b < t_end) load_tile(tb, kc, vc, t_b, n, g, slot_mask, P.n_slots);
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
 
-    // ---- merge hi/lo columns and the 4 waves through LDS ----
-    __shared__ float sm_acc[4][GQA][HEAD_DIM];
-    __shared__ float sm_m[4][GQA], sm_l[4][GQA];
-    l = wave_sum_xor(l, 16);
-    l = wave_sum_xor(l, 32);
+    // ---- merge hi/lo columns and the waves (and the current token) through LDS ----
+    S.l = wave_sum_xor(S.l, 16);
+    S.l = wave_sum_xor(S.l, 32);
 #pragma unroll
     for (int d = 0; d < 8; d++) {
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-            const float v = acc[d][r] + __shfl_xor(acc[d][r], 8, 64);
+            const float v = S.acc[d][r] + __shfl_xor(S.acc[d][r], 8, 64);
             if (hl == 0) sm_acc[wave][hloc][16 * d + 4 * g + r] = v;
         }
     }
     if (hl == 0 && g == 0) {
-        sm_m[wave][hloc] = m;
-        sm_l[wave][hloc] = l;
+        sm_m[wave][hloc] = S.m;
+        sm_l[wave][hloc] = S.l;
+    }
+    if (last_split) {
+        // score of the current token for head `wave` (q in fp32, k as the cache holds it)
+        float dot = sm_q[wave][lane] * sm_kv[0][lane] + sm_q[wave][lane + 64] * sm_kv[0][lane + 64];
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) dot += __shfl_xor(dot, o, 64);
+        if (lane == 0) {
+            sm_m[DEC_WAVES][wave] = dot;
+            sm_l[DEC_WAVES][wave] = 1.f;
+        }
     }
     __syncthreads();
 
-    const int th = threadIdx.x >> 5, d4 = (threadIdx.x & 31) * 4;  // head th, dims d4..d4+3
+    const int th = tid >> 6, d2 = (tid & 63) * 2;  // head th, dims d2, d2+1
     float M = sm_m[0][th];
-#pragma unroll
-    for (int w = 1; w < 4; w++) M = fmaxf(M, sm_m[w][th]);
-    float L = 0.f;
-    float4 A = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int w = 0; w < 4; w++) {
+    for (int w = 1; w < DEC_WAVES; w++) M = fmaxf(M, sm_m[w][th]);
+    if (last_split) M = fmaxf(M, sm_m[DEC_WAVES][th]);
+    float L = 0.f, A0 = 0.f, A1 = 0.f;
+    for (int w = 0; w < DEC_WAVES; w++) {
         if (sm_l[w][th] == 0.f) continue;
         const float c = exp2f(sm_m[w][th] - M);
         L += sm_l[w][th] * c;
-        A.x += sm_acc[w][th][d4 + 0] * c;
-        A.y += sm_acc[w][th][d4 + 1] * c;
-        A.z += sm_acc[w][th][d4 + 2] * c;
-        A.w += sm_acc[w][th][d4 + 3] * c;
+        A0 += sm_acc[w][th][d2] * c;
+        A1 += sm_acc[w][th][d2 + 1] * c;
+    }
+    if (last_split) {
+        const float c = exp2f(sm_m[DEC_WAVES][th] - M);
+        L += c;
+        A0 += sm_kv[1][d2] * c;
+        A1 += sm_kv[1][d2 + 1] * c;
     }
     const int hout = kvh * GQA + th;
+    float *out = P.att + (size_t)seq * Q_DIM + hout * HEAD_DIM + d2;
+    const float sink = P.sinks[hout] * LOG2E;
     if (n_split == 1) {
-        const float sink = P.sinks[hout] * LOG2E;
         const float Mf = fmaxf(M, sink), cs = exp2f(M - Mf);
         const float inv = 1.0f / (L * cs + exp2f(sink - Mf));
-        float4 o = {A.x * cs * inv, A.y * cs * inv, A.z * cs * inv, A.w * cs * inv};
-        *(float4 *)(P.att + (size_t)seq * Q_DIM + hout * HEAD_DIM + d4) = o;
-    } else {
-        float *pp = P.partial + (((size_t)seq * N_HEAD + hout) * P.max_split + split) * PART_STRIDE;
-        *(float4 *)(pp + d4) = A;
-        if (d4 == 0) {
-            pp[HEAD_DIM] = M;
-            pp[HEAD_DIM + 1] = L;
-        }
+        *(float2 *)out = make_float2(A0 * cs * inv, A1 * cs * inv);
+        return;
+    }
+    const size_t head_base = ((size_t)seq * N_HEAD + hout) * P.max_split;
+    float *pp = P.partial + (head_base + split) * PART_STRIDE;
+    *(float2 *)(pp + d2) = make_float2(A0, A1);
+    if (d2 == 0) {
+        pp[HEAD_DIM] = M;
+        pp[HEAD_DIM + 1] = L;
     }
 }
 
 // LSE merge of the split partials plus the sink (fused.metal:331-350).
-// grid = (N_HEAD, n_seq), 256 threads: the split weights are computed once per
-// split (threads over splits), then each thread sums one dim over half the splits.
-constexpr int MAX_SPLIT = 1024;
+// grid = (N_HEAD, n_seq), 256 threads: thread (dim group dg, split group sg) sums
+// dims 4dg..4dg+3 over splits sg, sg+8, ...; the first 64 splits' accumulators are
+// requested before the split weights are known, so the merge waits on about one
+// memory round trip.
 __global__ __launch_bounds__(256) void attn_combine_kernel(const DecodeParams P) {
-    __shared__ float w_s[MAX_SPLIT];
-    __shared__ float red[2][8];
-    __shared__ float half_acc[HEAD_DIM];
+    __shared__ float w_s[MERGE_MAX_SPLIT];
+    __shared__ float red[2][4];
+    __shared__ float4 part[8][32];
     const int hh = blockIdx.x, seq = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int ns = P.split_prefix[seq + 1] - P.split_prefix[seq];
     if (ns <= 1) return;  // written directly by the decode kernel
     const float *pp = P.partial + ((size_t)seq * N_HEAD + hh) * P.max_split * PART_STRIDE;
+    const int dg = tid & 31, sg = tid >> 5;
+    float4 x[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) x[i] = *(const float4 *)(pp + min(sg + 8 * i, ns - 1) * PART_STRIDE + 4 * dg);
     const float sink = P.sinks[hh] * LOG2E;
     float M = sink;
-    for (int s = tid; s < ns; s += 256) {
-        const float ls = pp[s * PART_STRIDE + HEAD_DIM + 1];
-        if (ls != 0.f) M = fmaxf(M, pp[s * PART_STRIDE + HEAD_DIM]);
-    }
+    for (int s = tid; s < ns; s += 256)
+        if (pp[s * PART_STRIDE + HEAD_DIM + 1] != 0.f) M = fmaxf(M, pp[s * PART_STRIDE + HEAD_DIM]);
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) M = wave_max_xor(M, o);
     if (lane == 0) red[0][wave] = M;
@@ -352,26 +412,44 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const DecodeParams P)
     if (lane == 0) red[1][wave] = L;
     __syncthreads();
     L = red[1][0] + red[1][1] + red[1][2] + red[1][3] + exp2f(sink - M);
-    const int dim = tid & 127, part = tid >> 7;
-    float A = 0.f;
-#pragma unroll 8
-    for (int s = part; s < ns; s += 2) A += pp[s * PART_STRIDE + dim] * w_s[s];
-    if (part == 1) half_acc[dim] = A;
+    float4 a = {0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0; s0 < ns; s0 += 64) {
+        if (s0 > 0) {
+#pragma unroll
+            for (int i = 0; i < 8; i++)
+                x[i] = *(const float4 *)(pp + min(s0 + sg + 8 * i, ns - 1) * PART_STRIDE + 4 * dg);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int sp = s0 + sg + 8 * i;
+            const float w = sp < ns ? w_s[sp] : 0.f;
+            a.x += x[i].x * w; a.y += x[i].y * w; a.z += x[i].z * w; a.w += x[i].w * w;
+        }
+    }
+    part[sg][dg] = a;
     __syncthreads();
-    if (part == 0) P.att[(size_t)seq * Q_DIM + hh * HEAD_DIM + dim] = (A + half_acc[dim]) / L;
+    if (sg == 0) {
+        float4 t = part[0][dg];
+#pragma unroll
+        for (int i = 1; i < 8; i++) {
+            const float4 u = part[i][dg];
+            t.x += u.x; t.y += u.y; t.z += u.z; t.w += u.w;
+        }
+        const float inv = 1.0f / L;
+        *(float4 *)(P.att + (size_t)seq * Q_DIM + hh * HEAD_DIM + 4 * dg) =
+            make_float4(t.x * inv, t.y * inv, t.z * inv, t.w * inv);
+    }
 }
 
 hipError_t launch_decode(const DecodeParams &P, int dtype, int total_splits, hipStream_t stream) {
-    dim3 grid(total_splits, N_HEAD_KV), block(256);
+    dim3 grid(total_splits, N_HEAD_KV), block(DEC_THREADS);
     if (dtype == DT_F16)
         hipLaunchKernelGGL(attn_decode_kernel<DT_F16>, grid, block, 0, stream, P);
     else
         hipLaunchKernelGGL(attn_decode_kernel<DT_BF16>, grid, block, 0, stream, P);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    bool need_combine = false;
-    for (int s = 0; s < P.n_seq; s++) need_combine |= (P.split_prefix[s + 1] - P.split_prefix[s]) > 1;
-    if (need_combine) {
+    if (P.max_split > 1) {
         hipLaunchKernelGGL(attn_combine_kernel, dim3(N_HEAD, P.n_seq), dim3(256), 0, stream, P);
         e = hipGetLastError();
     }

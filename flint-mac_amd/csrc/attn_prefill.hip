@@ -6,7 +6,8 @@
 //
 //  qk_prep: per token, RMSNorm (+ NEOX RoPE) of the 32 q heads and 4 k heads;
 //    q goes out as f16 [32][T][128] pre-scaled by log2(e)/sqrt(128); K goes
-//    into the key buffer [4][row][128] and V, transposed, into [4][128][row].
+//    into the key buffer [4][row][128] and V, transposed in 32-row tiles,
+//    into [4][row/32][128][32].
 //    Full-attention layers use the layer's cache directly (row = position).
 //    SWA layers attend from a scratch buffer covering [max(0, p0-512), p0+T)
 //    (the ring prefix [kbase, p0) is copied in first), and the positions
@@ -98,9 +99,9 @@ __global__ __launch_bounds__(256) void qk_prep_kernel(const PrefillParams P, int
             if (tt >= nt) continue;
             const int pos = P.p0 + t0 + tt;
             const uint16_t v = tile[tt][d];
-            P.vd[((size_t)kvh * HEAD_DIM + d) * P.k_rows + (pos - P.kbase)] = v;
+            P.vd[vt_index(kvh, pos - P.kbase, d, P.k_rows)] = v;
             if (P.ring_v && pos >= P.ring_from)
-                P.ring_v[((size_t)kvh * HEAD_DIM + d) * P.ring_slots + (pos & (P.ring_slots - 1))] = v;
+                P.ring_v[vt_index(kvh, pos & (P.ring_slots - 1), d, P.ring_slots)] = v;
         }
         return;
     }
@@ -124,8 +125,7 @@ __global__ __launch_bounds__(256) void ring_prefix_kernel(const PrefillParams P)
         const int d = i >> 6, r = i & 63;
         if (r >= nc) continue;
         const int pos = P.kbase + c0 + r;
-        P.vd[((size_t)kvh * HEAD_DIM + d) * P.k_rows + (pos - P.kbase)] =
-            P.ring_v[((size_t)kvh * HEAD_DIM + d) * P.ring_slots + (pos & mask)];
+        P.vd[vt_index(kvh, pos - P.kbase, d, P.k_rows)] = P.ring_v[vt_index(kvh, pos & mask, d, P.ring_slots)];
     }
 }
 
@@ -207,7 +207,7 @@ __global__ __launch_bounds__(256) void flash_prefill_kernel(const PrefillParams 
                 f16x8 v = {};
                 const int rr = r0 + 8 * kg;
                 if (rr < n_valid) {
-                    const u16x8 raw = *(const u16x8 *)(P.vd + ((size_t)kvh * HEAD_DIM + d) * P.k_rows + rr);
+                    const u16x8 raw = *(const u16x8 *)(P.vd + vt_index(kvh, rr, d, P.k_rows));
 #pragma unroll
                     for (int e = 0; e < 8; e++) v[e] = rr + e < n_valid ? to_f16<DT>(raw[e]) : (_Float16)0;
                 }

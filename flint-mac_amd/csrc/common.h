@@ -26,6 +26,9 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // 8 packed 16-bit values
+
+__device__ inline uint32_t pack2(uint16_t lo, uint16_t hi) { return (uint32_t)lo | ((uint32_t)hi << 16); }
 
 // Per-dtype conversions and MFMA calls. The KV cache holds raw 16-bit words.
 template <int DT>
@@ -64,6 +67,21 @@ struct KvType<DT_BF16> {
 // within its range; see attn_prefill.hip).
 __device__ inline f32x16 mfma32_f16(f16x8 a, f16x8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// V cache layout: per kv head, V transposed in tiles of 32 slots,
+// [kvh][rows/32][HEAD_DIM][32], so one 32-key tile of V^T is 8 KiB contiguous.
+__host__ __device__ inline size_t vt_index(int kvh, int row, int dim, int rows) {
+    return (((size_t)kvh * (rows >> 5) + (row >> 5)) * HEAD_DIM + dim) * 32 + (row & 31);
+}
+
+// Workgroup barrier that orders LDS only. __syncthreads() also orders global
+// memory, which the compiler implements by waiting for every outstanding global
+// load (s_waitcnt vmcnt(0)); this one leaves in-flight loads in flight.
+__device__ inline void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
 __device__ inline float wave_sum_xor(float v, int mask) { return v + __shfl_xor(v, mask, 64); }

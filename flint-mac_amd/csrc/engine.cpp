@@ -94,20 +94,35 @@ void validate_layer(const flint_attn_layer *L) {
     if (L->kv_dtype != FLINT_KV_F16 && L->kv_dtype != FLINT_KV_BF16) throw Error("kv_dtype must be F16 or BF16");
     if (L->n_slots <= 0 || L->n_slots % 32 != 0) throw Error("n_slots must be a positive multiple of 32");
     if (L->window < 1) throw Error("window must be >= 1");
+    if (((uintptr_t)L->q_norm | (uintptr_t)L->k_norm) & 15) throw Error("q_norm/k_norm must be 16-byte aligned");
     if (L->is_swa) {
         if (L->n_slots & (L->n_slots - 1)) throw Error("SWA ring size must be a power of two");
         if (L->n_slots < L->window) throw Error("SWA ring must hold the window (n_slots >= window)");
     }
 }
 
-// Split plan: 32-key tiles per split so that the 4 kv heads x splits fill the
-// 256 CUs about twice, and no split is shorter than two tiles per wave.
-int plan_tiles_per_split(int n_tiles, int keys_per_split, int n_seq_total_tiles_hint) {
+// Split plan: 32-key tiles per split, the same for every sequence of a launch.
+// An 8-wave block is one CU's share; the plan keeps the 4 x (total splits)
+// blocks within one round of the 256 CUs, with at least two tiles per wave.
+// Small launches (a few blocks, latency-bound) take one split per sequence
+// when that stays within 8 tiles per wave: the split merge costs more than
+// the extra tiles.
+int plan_tiles_per_split(int total_tiles, int max_tiles, int keys_per_split) {
     if (keys_per_split > 0) return std::max(1, keys_per_split / 32);
-    (void)n_seq_total_tiles_hint;
-    const int target_splits = 128;
-    int tps = (n_tiles + target_splits - 1) / target_splits;
-    return std::max(tps, 8);
+    const int cus = 256;
+    if (total_tiles * N_HEAD_KV <= 16 * cus / 8 && max_tiles <= 64) return std::max(max_tiles, 1);
+    int tps = (total_tiles * N_HEAD_KV + cus - 1) / cus;
+    return std::max(16, (tps + 7) / 8 * 8);
+}
+
+// theta^(-2i/128) table, cached for the last theta
+void rope_freqs_cached(float theta, float *freq) {
+    static thread_local float last_theta = -1.f, table[HEAD_DIM / 2];
+    if (theta != last_theta) {
+        rope_freqs(theta, table);
+        last_theta = theta;
+    }
+    std::memcpy(freq, table, sizeof(table));
 }
 
 constexpr int PART_STRIDE = 132;
@@ -135,18 +150,23 @@ void decode_impl(const flint_attn_layer *L, int n_seq, int64_t seq_stride, const
     P.has_rope = L->has_rope;
     P.window = L->window;
     P.rms_eps = L->rms_eps;
-    rope_freqs(L->rope_theta, P.rope_freq);
+    rope_freqs_cached(L->rope_theta, P.rope_freq);
     P.n_seq = n_seq;
-    int total = 0, max_split = 1;
+    int tiles[MAX_SEQ], total_tiles = 0, max_tiles = 0;
     for (int s = 0; s < n_seq; s++) {
         const int p = pos[s];
         if (p < 0) throw Error("position must be >= 0");
         if (!L->is_swa && p >= L->n_slots) throw Error("context full: position beyond the layer's KV capacity");
         const int k_begin = L->is_swa ? std::max(p - (L->window - 1), 0) : 0;
-        const int tiles = p > 0 ? (p + 31) / 32 - k_begin / 32 : 0;
-        const int tps = plan_tiles_per_split(tiles, keys_per_split, 0);
-        const int ns = std::max(1, (tiles + tps - 1) / tps);
-        P.pos[s] = p;
+        tiles[s] = p > 0 ? (p + 31) / 32 - k_begin / 32 : 0;
+        total_tiles += tiles[s];
+        max_tiles = std::max(max_tiles, tiles[s]);
+    }
+    const int tps = plan_tiles_per_split(total_tiles, max_tiles, keys_per_split);
+    int total = 0, max_split = 1;
+    for (int s = 0; s < n_seq; s++) {
+        const int ns = std::max(1, (tiles[s] + tps - 1) / tps);
+        P.pos[s] = pos[s];
         P.tiles_per_split[s] = tps;
         P.split_prefix[s] = total;
         total += ns;
@@ -155,9 +175,10 @@ void decode_impl(const flint_attn_layer *L, int n_seq, int64_t seq_stride, const
     P.split_prefix[n_seq] = total;
     P.max_split = max_split;
     if (max_split > 1024) throw Error("too many key splits (max 1024): raise keys_per_split");
+    DeviceScratch &ws = scratch();
     if (max_split > 1) {
         const size_t need = (size_t)n_seq * N_HEAD * max_split * PART_STRIDE * sizeof(float);
-        P.partial = (float *)scratch().partial.get(need);
+        P.partial = (float *)ws.partial.get(need);
     }
     check(launch_decode(P, L->kv_dtype, total, stream), "decode launch");
 }
@@ -182,7 +203,7 @@ void prefill_impl(const flint_attn_layer *L, const float *qkv, int q_stride, int
     P.is_swa = L->is_swa;
     P.has_rope = L->has_rope;
     P.window = L->window;
-    rope_freqs(L->rope_theta, P.rope_freq);
+    rope_freqs_cached(L->rope_theta, P.rope_freq);
     P.att = att;
     DeviceScratch &ws = scratch();
     P.qh = (_Float16 *)ws.qh.get((size_t)N_HEAD * T * HEAD_DIM * sizeof(_Float16));

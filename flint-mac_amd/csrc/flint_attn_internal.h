@@ -17,7 +17,7 @@ struct DecodeParams {
     const float *k_norm;        // [128]
     const float *sinks;         // [32]
     uint16_t *k_cache;          // sequence 0: [4][n_slots][128]
-    uint16_t *v_cache;          // sequence 0: [4][128][n_slots]
+    uint16_t *v_cache;          // sequence 0: [4][n_slots/32][128][32] (V^T in 32-slot tiles)
     long long seq_stride;       // elements between two sequences' K (and V) caches
     float *att;                 // [n_seq][4096]
     float *partial;             // [n_seq][32][max_split][132]
@@ -47,12 +47,12 @@ struct PrefillParams {
     _Float16 *qh;         // [32][T][128] normed/roped q * log2(e)/sqrt(128), f16
     // keys/values the attention reads: key position kp lives at row kp - kbase
     uint16_t *kd;         // [4][k_rows][128]
-    uint16_t *vd;         // [4][128][k_rows]
+    uint16_t *vd;         // [4][k_rows/32][128][32]
     int k_rows;           // row capacity per kv head (multiple of 32)
     int kbase;
     // SWA ring (cache) written for positions >= ring_from; copied into kd/vd for [kbase, p0)
     uint16_t *ring_k;     // [4][n_slots][128] or null
-    uint16_t *ring_v;     // [4][128][n_slots]
+    uint16_t *ring_v;     // [4][n_slots/32][128][32]
     int ring_slots, ring_from;
     float *att;           // [T][4096]
 };

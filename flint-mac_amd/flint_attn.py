@@ -121,8 +121,8 @@ def _ptr(t):
 
 
 class KVLayer:
-    """One attention layer on the GPU: KV cache in HBM (K [4][n_slots][128],
-    V transposed [4][128][n_slots]) and its q_norm / k_norm / sinks.
+    """One attention layer on the GPU: KV cache in HBM (K [4][n_slots][128], V transposed
+    in 32-slot tiles [4][n_slots/32][128][32]) and its q_norm / k_norm / sinks.
     `n_seq` > 1 allocates independent caches for that many sequences."""
 
     def __init__(self, is_swa, has_rope, n_slots=None, kv_dtype="f16", rope_theta=1e4, window=N_SWA,
@@ -134,7 +134,8 @@ class KVLayer:
             n_slots = SWA_RING if is_swa else 4096
         self.n_slots, self.n_seq = int(n_slots), int(n_seq)
         self.k = torch.zeros((n_seq, N_HEAD_KV, n_slots, HEAD_DIM), dtype=self.torch_dtype, device=device)
-        self.v = torch.zeros((n_seq, N_HEAD_KV, HEAD_DIM, n_slots), dtype=self.torch_dtype, device=device)
+        assert self.n_slots % 32 == 0, "n_slots must be a multiple of 32"
+        self.v = torch.zeros((n_seq, N_HEAD_KV, n_slots // 32, HEAD_DIM, 32), dtype=self.torch_dtype, device=device)
         f = lambda a, n, d: torch.as_tensor(a if a is not None else [d] * n, dtype=torch.float32).to(device)
         self.q_norm = f(q_norm, HEAD_DIM, 1.0).contiguous()
         self.k_norm = f(k_norm, HEAD_DIM, 1.0).contiguous()
@@ -148,6 +149,10 @@ class KVLayer:
     @property
     def seq_stride(self):
         return N_HEAD_KV * self.n_slots * HEAD_DIM
+
+    def v_slots(self):
+        """V as [n_seq][4][n_slots][128] (a copy out of the tiled layout)."""
+        return self.v.permute(0, 1, 2, 4, 3).reshape(self.n_seq, N_HEAD_KV, self.n_slots, HEAD_DIM)
 
     def slot(self, pos):
         return pos & (self.n_slots - 1) if self.is_swa else pos

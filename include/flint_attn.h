@@ -11,8 +11,8 @@
  * engine (/root/reference/src/capi.h:1).
  *
  * KV cache layout per layer and kv head (HBM, 16-bit elements):
- *   K: [N_HEAD_KV][n_slots][HEAD_DIM]   (row per slot)
- *   V: [N_HEAD_KV][HEAD_DIM][n_slots]   (transposed: column per slot)
+ *   K: [N_HEAD_KV][n_slots][HEAD_DIM]           (row per slot)
+ *   V: [N_HEAD_KV][n_slots/32][HEAD_DIM][32]    (transposed in tiles of 32 slots)
  * SWA layers: n_slots is a power of two >= window (1024 for Flint) and
  * position p lives in slot p & (n_slots-1); full-attention layers: slot = p.
  * (The reference keeps position-major [slot][kv_head][128] for both,
@@ -52,7 +52,7 @@ extern "C" {
  */
 typedef struct {
     void *k_cache;        /* device, layout above */
-    void *v_cache;        /* device, layout above */
+    void *v_cache;        /* device, layout above (element (h, slot, d) at ((h*n_slots/32 + slot/32)*128 + d)*32 + slot%32) */
     int32_t n_slots;      /* multiple of 32; SWA: power of two >= window */
     int32_t kv_dtype;     /* FLINT_KV_F16 or FLINT_KV_BF16 */
     int32_t is_swa;

@@ -39,15 +39,15 @@ def assert_close(got, want, what="", max_abs=MAX_ABS, mean_abs=MEAN_ABS):
 
 
 def to_cache_layout(K, V, n_slots, slots):
-    """Linear history rows K,V [n][512] placed at the given slots -> (K [4][n_slots][128], V^T [4][128][n_slots])."""
+    """Linear history rows K,V [n][512] placed at the given slots -> the cache layout:
+    K [4][n_slots][128] and V transposed in 32-slot tiles [4][n_slots/32][128][32]."""
     n = K.shape[0]
     Kc = np.zeros((N_HEAD_KV, n_slots, HEAD_DIM), np.float32)
-    Vc = np.zeros((N_HEAD_KV, HEAD_DIM, n_slots), np.float32)
-    Kh = K.reshape(n, N_HEAD_KV, HEAD_DIM)
-    Vh = V.reshape(n, N_HEAD_KV, HEAD_DIM)
+    Vs = np.zeros((N_HEAD_KV, n_slots, HEAD_DIM), np.float32)
     slots = np.asarray(slots)
-    Kc[:, slots, :] = Kh.transpose(1, 0, 2)
-    Vc[:, :, slots] = Vh.transpose(1, 2, 0)
+    Kc[:, slots, :] = K.reshape(n, N_HEAD_KV, HEAD_DIM).transpose(1, 0, 2)
+    Vs[:, slots, :] = V.reshape(n, N_HEAD_KV, HEAD_DIM).transpose(1, 0, 2)
+    Vc = np.ascontiguousarray(Vs.reshape(N_HEAD_KV, n_slots // 32, 32, HEAD_DIM).transpose(0, 1, 3, 2))
     return Kc, Vc
 
 

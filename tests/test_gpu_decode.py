@@ -60,11 +60,11 @@ def test_decode_swa_ring_steps_config2(cuda, store):
         assert_close(got[pos], want[pos], f"pos {pos}")
     assert_close(got, want, "all steps")
     # ring: slot p & 1023 holds position p for the last 1024 positions
-    vc = kv.v[0].float().cpu().numpy()  # [4][128][1024]
+    vc = kv.v_slots()[0].float().cpu().numpy()  # [4][1024][128]
     kc = kv.k[0].float().cpu().numpy()  # [4][1024][128]
     for p in range(max(0, n - 1024), n):
         s = p & 1023
-        assert np.array_equal(vc[:, :, s], V[p].reshape(N_HEAD_KV, HEAD_DIM)), f"V slot {s} pos {p}"
+        assert np.array_equal(vc[:, s, :], V[p].reshape(N_HEAD_KV, HEAD_DIM)), f"V slot {s} pos {p}"
         assert k_close(kc[:, s, :], K[p].reshape(N_HEAD_KV, HEAD_DIM), store), f"K slot {s} pos {p}"
 
 
@@ -113,7 +113,7 @@ def test_decode_split_k_32k_config3(cuda, store):
     for kps, o in outs.items():
         np.testing.assert_allclose(o, outs[32768], rtol=0, atol=2e-5 * max(1.0, np.abs(want).max()))
     # the current token's K/V landed in slot n
-    vc = kv.v[0, :, :, n].float().cpu().numpy()
+    vc = kv.v_slots()[0, :, n, :].float().cpu().numpy()
     assert np.array_equal(vc, fo.round_store(qkv[4608:], store).reshape(N_HEAD_KV, HEAD_DIM))
 
 

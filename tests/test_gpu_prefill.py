@@ -67,12 +67,12 @@ def test_prefill_4000_config4(cuda, store, is_swa):
     for p, w in want.items():
         assert_close(got[p], w, f"pos {p}")
     assert_close(np.stack([got[p] for p in want]), np.stack(list(want.values())), "probes")
-    vc = kv.v[0].float().cpu().numpy()
+    vc = kv.v_slots()[0].float().cpu().numpy()
     kc = kv.k[0].float().cpu().numpy()
     lo = T - 1024 if is_swa else 0
     for p in range(lo, T):
         s = kv.slot(p)
-        assert np.array_equal(vc[:, :, s], V[p].reshape(N_HEAD_KV, HEAD_DIM)), f"V slot {s} pos {p}"
+        assert np.array_equal(vc[:, s, :], V[p].reshape(N_HEAD_KV, HEAD_DIM)), f"V slot {s} pos {p}"
         assert k_close(kc[:, s, :], K[p].reshape(N_HEAD_KV, HEAD_DIM), store), f"K slot {s} pos {p}"
 
 
