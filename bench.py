@@ -26,35 +26,59 @@ sys.path.insert(0, os.path.join(ROOT, "flint-mac_amd"))
 HBM_PEAK_GBS = 8000.0       # MI355X HBM3E
 MFMA_PEAK_TFLOPS = 2500.0   # MI355X dense bf16/f16 MFMA
 N_FULL_FLINT, N_SWA_FLINT = 14, 35
+# HBM bytes per decode call (attn_decode_kernel + attn_combine_kernel) at 32k, from rocprofv3
+# --pmc FETCH_SIZE and WRITE_SIZE runs of `bench.py --only decode --no-cpu`, each scaled by the
+# counter's reading for the 64 MiB calibration copy (profiles/decode_32k_f16.md).
+DECODE_TRAFFIC_BYTES = 69734195
 
 
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def graph_replay_ms(torch, step, reps, warmup=2):
-    """Capture `step` (a sequence of library launches on the current stream) into a HIP graph,
-    replay it `reps` times between two events, return ms per replay. Graph replay keeps the
-    host's per-launch cost (Python + ctypes + hipLaunchKernel) out of the GPU timeline."""
-    side = torch.cuda.Stream()
-    side.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(side):
-        for _ in range(warmup):
-            step()
-    torch.cuda.current_stream().wait_stream(side)
-    torch.cuda.synchronize()
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
+_SLEEP_CYCLES_PER_MS = None
+
+
+def _sleep_ms(torch, ms):
+    """Occupy the current stream for about `ms` ms with torch's bounded clock-spin kernel."""
+    global _SLEEP_CYCLES_PER_MS
+    if _SLEEP_CYCLES_PER_MS is None:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(1000)
+        e0.record()
+        torch.cuda._sleep(2_000_000)
+        e1.record()
+        torch.cuda.synchronize()
+        _SLEEP_CYCLES_PER_MS = 2_000_000 / max(e0.elapsed_time(e1), 1e-3)
+    torch.cuda._sleep(int(ms * _SLEEP_CYCLES_PER_MS))
+
+
+def queued_launch_ms(torch, step, reps, warmup=2):
+    """GPU time per call of `step` (a sequence of library launches on torch's current stream).
+
+    The `reps` calls are enqueued back to back behind a spin kernel that keeps the stream busy
+    while the host enqueues them, so the two events bracket the kernels alone (the host's
+    per-call cost of Python + ctypes + hipLaunchKernel stays off the GPU timeline) and the
+    launches run as an engine issues them: direct dispatches, no graph. Returns
+    (ms per call, host-bound flag): the flag is set if the spin ended before the host had
+    enqueued every call (then the figure includes host gaps)."""
+    for _ in range(warmup):
         step()
-    g.replay()
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    step()
+    torch.cuda.synchronize()
+    host_ms = (time.perf_counter() - t0) * 1e3
+    e_spin, e0, e1 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+    _sleep_ms(torch, min(2.0 * host_ms * reps + 5.0, 2000.0))
+    e_spin.record()
     e0.record()
     for _ in range(reps):
-        g.replay()
+        step()
     e1.record()
+    host_bound = e_spin.query()  # the spin already finished: the GPU waited for the host
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / reps
+    return e0.elapsed_time(e1) / reps, bool(host_bound)
 
 
 def decode_bytes(n_keys):
@@ -86,14 +110,25 @@ def bench_decode_32k(torch, fa, steps, warmup, n_layers=8, ctx=32768):
             kv.decode(qkv[i], att[i], ctx)
 
     t0 = time.perf_counter()
-    ms_per_step = graph_replay_ms(torch, step, steps, warmup)
+    ms_per_step, host_bound = queued_launch_ms(torch, step, steps, warmup)
     wall = time.perf_counter() - t0
     avg_launch_ms = ms_per_step / n_layers
     nbytes = decode_bytes(ctx)
     del layers
     torch.cuda.empty_cache()
     return dict(ms_per_step=ms_per_step, avg_launch_ms=avg_launch_ms, bytes_per_launch=nbytes,
-                gbs=nbytes * n_layers / (ms_per_step * 1e-3) / 1e9, wall_s=wall, n_layers=n_layers)
+                gbs=nbytes * n_layers / (ms_per_step * 1e-3) / 1e9, wall_s=wall, n_layers=n_layers,
+                host_bound=host_bound)
+
+
+def calibration_copy(torch, nbytes=64 << 20):
+    """One plain elementwise pass over a known size (reads and writes nbytes): the reference
+    point that scales rocprofv3's FETCH_SIZE / WRITE_SIZE counters to bytes."""
+    src = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src)
+    torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    del src, dst
 
 
 def bench_decode_swa(torch, fa, reps=200, pos=32768):
@@ -114,7 +149,7 @@ def bench_decode_swa(torch, fa, reps=200, pos=32768):
         for i, kv in enumerate(layers):
             kv.decode(qkv[i], att[i], pos)
 
-    return graph_replay_ms(torch, step, max(1, reps // n)) / n
+    return queued_launch_ms(torch, step, max(1, reps // n))[0] / n
 
 
 def bench_prefill(torch, fa, T=4000, reps=10):
@@ -168,7 +203,7 @@ def bench_config5(torch, fa, steps=3):
         for kv in layers:
             kv.decode(qkv, att, ctx)
 
-    ms = graph_replay_ms(torch, step, steps, warmup=1)
+    ms, _ = queued_launch_ms(torch, step, steps, warmup=1)
     nbytes = sum(12 * decode_bytes(c) + 36 * decode_bytes(min(c, 512)) for c in ctx)
     del layers
     torch.cuda.empty_cache()
@@ -224,6 +259,7 @@ def main():
         res["decode"] = bench_decode_32k(torch, fa, args.steps, args.warmup)
         log(f"decode: {res['decode']}")
         res["swa_ms"] = bench_decode_swa(torch, fa)
+        calibration_copy(torch)
         log(f"swa decode per layer: {res['swa_ms']:.4f} ms")
     if args.only in (None, "prefill"):
         log("prefill 4000 (config 4)")
@@ -262,9 +298,10 @@ def main():
             "roofline": {"bound": "hbm", "achieved": round(d["bytes_per_launch"] / (t_full * 1e-3) / 1e9, 1),
                          "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(d["bytes_per_launch"] / (t_full * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                         "traffic": None,
-                         "kernel": "attn_decode_kernel<f16> (+ attn_combine_kernel inside the timed launch)",
-                         "bytes_per_launch": d["bytes_per_launch"]},
+                         "traffic": DECODE_TRAFFIC_BYTES,
+                         "kernel": "one flint_attn_decode call = attn_decode_kernel<f16> (256 blocks) + "
+                                   "attn_combine_kernel (split merge); time per call from HIP events",
+                         "bytes_per_launch": d["bytes_per_launch"], "host_bound": d["host_bound"]},
         })
     if "prefill" in res:
         line["prefill_4000_bf16"] = {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
