@@ -13,9 +13,10 @@
 //  * One 8-wave workgroup per (sequence, kv head, key split) serves all 8 q
 //    heads of the GQA group, so every K/V byte is read from HBM once (the
 //    reference re-reads K/V per q head).
-//  * KV layout is head-major: K [kvh][slot][128], V transposed in 32-slot tiles
-//    [kvh][slot/32][128][32], so a 32-key tile is two contiguous 8 KiB blocks and
-//    both MFMA operands are single 16-byte loads straight from HBM.
+//  * KV layout is head-major and tiled by 32 slots: K tiles stored in MFMA
+//    A-operand order, V transposed ([dim][slot] per tile), so a 32-key tile is
+//    two contiguous 8 KiB blocks, both MFMA operands are single 16-byte loads
+//    straight from HBM and every load instruction reads 1 KiB contiguous.
 //  * Scores are S^T = K * Q^T on v_mfma_f32_16x16x32: the 16 MFMA columns carry
 //    the 8 heads' q split into hi + lo halves of the 16-bit type, so the scores
 //    are fp32-accurate at no extra MFMA cost; P*V uses the same hi/lo trick on P.
@@ -32,8 +33,10 @@
 //    last-block merge inside the streaming kernel needs an agent-scope
 //    release/acquire per block and funnels every partial through one CU, which
 //    measured slower than the kernel boundary.)
-//  * Batched entry: blockIdx.x walks a flattened (sequence, split) table so one
-//    launch serves many independent sequences (one token each).
+//  * Batched entry: grid (max split, kv head, sequence), so one launch serves many
+//    independent sequences (one token each); blocks past a sequence's split count
+//    exit at once. Every kernel argument the block needs is read at wave start, so
+//    the kernel-argument fetch costs one memory round trip.
 #include "common.h"
 #include "flint_attn_internal.h"
 
@@ -50,22 +53,25 @@ struct KvTile {
     u32x4 v[8];     // V^T rows: dim tile d
 };
 
-// Issue the 16 loads of tile t (keys 32t .. 32t+31) for this lane. kc / vc are
-// wave-uniform bases; offsets stay 32-bit (a kv head's cache is < 2^31 elements)
-// so the loads take the scalar-base + vector-offset form.
+// Issue the 16 loads of tile t (keys 32t .. 32t+31) for this lane: 1 KiB contiguous per
+// load instruction in both tiled layouts. kc / vc are wave-uniform bases; offsets stay
+// 32-bit (a kv head's cache is < 2^31 elements) so the loads take the scalar-base +
+// vector-offset form. A wave with no tile left (live == false) still issues the 16 loads,
+// which keeps the compiler's wait counts static, but every lane reads the tile's first
+// 16 bytes, so each costs one cache line instead of eight.
 __device__ inline void load_tile(KvTile &T, const uint16_t *__restrict__ kc, const uint16_t *__restrict__ vc,
-                                 int t, int n, int g, int slot_mask, int n_slots) {
-    const uint32_t kb = (uint32_t)t * 32;
+                                 int t, int lane, int slot_mask, bool live) {
+    const uint32_t base = ((uint32_t)(t * 32) & (uint32_t)slot_mask) * HEAD_DIM;
+    // K: instruction (st, c) reads units (st*4 + c)*64 + lane: MFMA row n = lane & 15 holds
+    // key 8(n>>2) + 4st + (n&3) of the tile, dims 32c + 8(lane>>4) .. +7
+    const uint32_t ko = base + (live ? lane * 8 : 0);
 #pragma unroll
-    for (int st = 0; st < 2; st++) {
-        // MFMA row i = n holds key kb + 8(i/4) + 4st + (i%4)
-        const uint32_t key = kb + 8 * (n >> 2) + 4 * st + (n & 3);
-        const uint32_t ko = (key & (uint32_t)slot_mask) * HEAD_DIM + 8 * g;
+    for (int st = 0; st < 2; st++)
 #pragma unroll
-        for (int c = 0; c < 4; c++) T.k[st][c] = __builtin_nontemporal_load((const u32x4 *)(kc + ko + 32 * c));
-    }
-    // V^T tile of slots kb..kb+31 (8 KiB contiguous): row = dim 16d + n, keys kb + 8g .. +7
-    const uint32_t vo = ((kb & (uint32_t)slot_mask) * HEAD_DIM) + n * 32 + 8 * g;
+        for (int c = 0; c < 4; c++)
+            T.k[st][c] = __builtin_nontemporal_load((const u32x4 *)(kc + ko + (st * 4 + c) * 512));
+    // V^T tile (8 KiB): row = dim 16d + n, keys 8g .. 8g+7 of the tile
+    const uint32_t vo = base + (live ? (lane & 15) * 32 + 8 * (lane >> 4) : 0);
 #pragma unroll
     for (int d = 0; d < 8; d++) T.v[d] = __builtin_nontemporal_load((const u32x4 *)(vc + vo + 16 * d * 32));
 }
@@ -166,18 +172,6 @@ __device__ inline float2 norm_rope_pair(float2 x, float2 w, float eps, bool rope
     return make_float2(x0, x1);
 }
 
-// Accumulators of splits s0 + sg + 4i (i < 16), dims 8c..8c+7, for the final merge.
-// Indices past the last split are clamped to it (their weight is zero).
-__device__ inline void fetch_partials(float4 (&xa)[16], float4 (&xb)[16], const float *__restrict__ hp, int s0,
-                                      int n_split, int sg, int c) {
-#pragma unroll
-    for (int i = 0; i < 16; i++) {
-        const int sp = min(s0 + sg + 4 * i, n_split - 1);
-        xa[i] = *(const float4 *)(hp + sp * PART_STRIDE + 8 * c);
-        xb[i] = *(const float4 *)(hp + sp * PART_STRIDE + 8 * c + 4);
-    }
-}
-
 template <int DT>
 __global__ __launch_bounds__(DEC_THREADS) void attn_decode_kernel(const DecodeParams P) {
     typedef KvType<DT> KT;
@@ -186,25 +180,34 @@ __global__ __launch_bounds__(DEC_THREADS) void attn_decode_kernel(const DecodePa
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n = lane & 15, g = lane >> 4;   // MFMA column (q head x hi/lo) and k-group
     const int hloc = n & 7, hl = n >> 3;      // head within the GQA group, 0 = hi half, 1 = lo half
-    const int kvh = blockIdx.y;
+    const int split = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
 
-    // ---- which sequence / split this block serves ----
-    int seq = 0;
-    while (seq + 1 < P.n_seq && (int)blockIdx.x >= P.split_prefix[seq + 1]) seq++;
-    const int split = blockIdx.x - P.split_prefix[seq];
-    const int n_split = P.split_prefix[seq + 1] - P.split_prefix[seq];
+    // ---- every kernel argument is read here, in one batch of scalar loads at wave start
+    //      (left to itself the compiler sinks each load to its first use, and each sunk
+    //      load is one more memory round trip on the critical path) ----
+    const int n_split = P.n_split[seq], pos = P.pos[seq];
+    const int is_swa = P.is_swa, has_rope = P.has_rope, window = P.window, tps = P.tiles_per_split;
+    const int n_slots = P.n_slots, slot_mask = P.slot_mask, max_split = P.max_split;
+    const float rms_eps = P.rms_eps;
+    const long long seq_stride = P.seq_stride;
+    const float *const qkv = P.qkv, *const q_norm = P.q_norm, *const k_norm = P.k_norm, *const sinks = P.sinks;
+    uint16_t *const k_cache = P.k_cache, *const v_cache = P.v_cache;
+    float *const att = P.att, *const partial = P.partial;
+    pin_sgpr(n_split), pin_sgpr(pos), pin_sgpr(is_swa), pin_sgpr(has_rope), pin_sgpr(window), pin_sgpr(tps);
+    pin_sgpr(n_slots), pin_sgpr(slot_mask), pin_sgpr(max_split), pin_sgpr(rms_eps), pin_sgpr(seq_stride);
+    pin_sgpr(qkv), pin_sgpr(q_norm), pin_sgpr(k_norm), pin_sgpr(sinks), pin_sgpr(k_cache), pin_sgpr(v_cache);
+    pin_sgpr(att), pin_sgpr(partial);
+
+    if (split >= n_split) return;  // grid x covers the longest sequence's splits
     const bool last_split = split == n_split - 1;
-    const int pos = P.pos[seq];
-    const int k_begin = P.is_swa ? max(pos - (P.window - 1), 0) : 0;
+    const int k_begin = is_swa ? max(pos - (window - 1), 0) : 0;
     const int tile_lo = k_begin >> 5, tile_hi = (pos + 31) >> 5;  // tiles holding keys [k_begin, pos)
-    const int tps = P.tiles_per_split[seq];
     const int t_begin = tile_lo + split * tps;
     const int t_end = min(t_begin + tps, tile_hi);
-    const int slot_mask = P.slot_mask;
 
-    const uint16_t *__restrict__ kc = P.k_cache + (size_t)seq * P.seq_stride + (size_t)kvh * P.n_slots * HEAD_DIM;
-    const uint16_t *__restrict__ vc = P.v_cache + (size_t)seq * P.seq_stride + (size_t)kvh * HEAD_DIM * P.n_slots;
-    const float *__restrict__ row = P.qkv + (size_t)seq * QKV_DIM;
+    const uint16_t *__restrict__ kc = k_cache + (size_t)seq * seq_stride + (size_t)kvh * n_slots * HEAD_DIM;
+    const uint16_t *__restrict__ vc = v_cache + (size_t)seq * seq_stride + (size_t)kvh * HEAD_DIM * n_slots;
+    const float *__restrict__ row = qkv + (size_t)seq * QKV_DIM;
 
     // LDS: q halves in MFMA-operand order, q in fp32, the current token, the wave merge
     __shared__ uint16_t sm_qh[2][GQA][HEAD_DIM];   // [hi/lo][head][dim]
@@ -219,13 +222,14 @@ __global__ __launch_bounds__(DEC_THREADS) void attn_decode_kernel(const DecodePa
     const bool cur_wave = last_split && wave == DEC_WAVES - 1;  // also handles the current token
     const float *qr = row + (kvh * GQA + wave) * HEAD_DIM;
     const float2 qx = make_float2(qr[lane], qr[lane + 64]);
-    const float2 qw = make_float2(P.q_norm[lane], P.q_norm[lane + 64]);
+    const float2 qw = make_float2(q_norm[lane], q_norm[lane + 64]);
     const float rfreq = P.rope_freq[lane];
+    const float sink = sinks[kvh * GQA + wave] * LOG2E;  // head `wave` of the group, for the final merge
     float2 kx = {0.f, 0.f}, kw = {0.f, 0.f}, vx = {0.f, 0.f};
     if (cur_wave) {
         const float *kr = row + Q_DIM + kvh * HEAD_DIM, *vr = row + Q_DIM + KV_DIM + kvh * HEAD_DIM;
         kx = make_float2(kr[lane], kr[lane + 64]);
-        kw = make_float2(P.k_norm[lane], P.k_norm[lane + 64]);
+        kw = make_float2(k_norm[lane], k_norm[lane + 64]);
         vx = make_float2(vr[lane], vr[lane + 64]);
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -234,17 +238,17 @@ __global__ __launch_bounds__(DEC_THREADS) void attn_decode_kernel(const DecodePa
     // counting at the join conservative, and the prologue would then wait for the tiles.
     KvTile ta, tb;
     int t_a = t_begin + wave, t_b = t_a + DEC_WAVES;
-    load_tile(ta, kc, vc, t_a < t_end ? t_a : t_begin, n, g, slot_mask, P.n_slots);
-    load_tile(tb, kc, vc, t_b < t_end ? t_b : t_begin, n, g, slot_mask, P.n_slots);
+    load_tile(ta, kc, vc, t_a < t_end ? t_a : t_begin, lane, slot_mask, t_a < t_end);
+    load_tile(tb, kc, vc, t_b < t_end ? t_b : t_begin, lane, slot_mask, t_b < t_end);
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- prologue: wave w normalises q head w (+ RoPE), the last split's last wave also
     //      the current token's k and v (rounded to the cache dtype, written to slot(pos)) ----
     {
         float cs = 1.f, sn = 0.f;  // rotation of frequency `lane`
-        if (P.has_rope) rope_sincos((float)pos * rfreq, &sn, &cs);
+        if (has_rope) rope_sincos((float)pos * rfreq, &sn, &cs);
         const float qs = LOG2E / sqrtf((float)HEAD_DIM);
-        const float2 qv = norm_rope_pair(qx, qw, P.rms_eps, P.has_rope, cs, sn);
+        const float2 qv = norm_rope_pair(qx, qw, rms_eps, has_rope, cs, sn);
         const float q0 = qv.x * qs, q1 = qv.y * qs;
         sm_q[wave][lane] = q0;
         sm_q[wave][lane + 64] = q1;
@@ -256,7 +260,7 @@ __global__ __launch_bounds__(DEC_THREADS) void attn_decode_kernel(const DecodePa
         if (cur_wave) {
             // the current token: no key read by this launch lives in slot(pos) (in the ring it
             // held pos - n_slots, outside the window)
-            const float2 kv2 = norm_rope_pair(kx, kw, P.rms_eps, P.has_rope, cs, sn);
+            const float2 kv2 = norm_rope_pair(kx, kw, rms_eps, has_rope, cs, sn);
             const uint16_t k0 = KT::from_float(kv2.x), k1 = KT::from_float(kv2.y);
             const uint16_t v0 = KT::from_float(vx.x), v1 = KT::from_float(vx.y);
             sm_kv[0][lane] = KT::to_float(k0);
@@ -264,12 +268,12 @@ __global__ __launch_bounds__(DEC_THREADS) void attn_decode_kernel(const DecodePa
             sm_kv[1][lane] = KT::to_float(v0);
             sm_kv[1][lane + 64] = KT::to_float(v1);
             const int slot = pos & slot_mask;
-            uint16_t *kw_ = P.k_cache + (size_t)seq * P.seq_stride + ((size_t)kvh * P.n_slots + slot) * HEAD_DIM;
-            kw_[lane] = k0;
-            kw_[lane + 64] = k1;
-            uint16_t *vw = P.v_cache + (size_t)seq * P.seq_stride;
-            vw[vt_index(kvh, slot, lane, P.n_slots)] = v0;
-            vw[vt_index(kvh, slot, lane + 64, P.n_slots)] = v1;
+            uint16_t *kw_ = k_cache + (size_t)seq * seq_stride;
+            kw_[kt_index(kvh, slot, lane, n_slots)] = k0;
+            kw_[kt_index(kvh, slot, lane + 64, n_slots)] = k1;
+            uint16_t *vw = v_cache + (size_t)seq * seq_stride;
+            vw[vt_index(kvh, slot, lane, n_slots)] = v0;
+            vw[vt_index(kvh, slot, lane + 64, n_slots)] = v1;
         }
     }
     lds_barrier();  // the q operands are in LDS; the tile loads stay in flight
@@ -292,13 +296,13 @@ __global__ __launch_bounds__(DEC_THREADS) void attn_decode_kernel(const DecodePa
     __builtin_amdgcn_sched_barrier(0);
     if (t_b < t_end) {
         const int t_c = t_b + DEC_WAVES;
-        if (t_c < t_end) load_tile(ta, kc, vc, t_c, n, g, slot_mask, P.n_slots);
+        if (t_c < t_end) load_tile(ta, kc, vc, t_c, lane, slot_mask, true);
         __builtin_amdgcn_sched_barrier(0);
         consume_tile<DT>(S, tb, qb, t_b, k_begin, pos, g, hl);
         __builtin_amdgcn_sched_barrier(0);
         t_a = t_c;
         t_b = t_c + DEC_WAVES;
-        if (t_b < t_end) load_tile(tb, kc, vc, t_b, n, g, slot_mask, P.n_slots);
+        if (t_b < t_end) load_tile(tb, kc, vc, t_b, lane, slot_mask, true);
         __builtin_amdgcn_sched_barrier(0);
         while (t_a < t_end) {
             consume_tile<DT>(S, ta, qb, t_a, k_begin, pos, g, hl);
@@ -306,7 +310,7 @@ __global__ __launch_bounds__(DEC_THREADS) void attn_decode_kernel(const DecodePa
             ta = tb;
             t_a = t_b;
             t_b += DEC_WAVES;
-            if (t_b < t_end) load_tile(tb, kc, vc, t_b, n, g, slot_mask, P.n_slots);
+            if (t_b < t_end) load_tile(tb, kc, vc, t_b, lane, slot_mask, true);
             __builtin_amdgcn_sched_barrier(0);
         }
     }
@@ -336,76 +340,91 @@ __global__ __launch_bounds__(DEC_THREADS) void attn_decode_kernel(const DecodePa
             sm_l[DEC_WAVES][wave] = 1.f;
         }
     }
-    __syncthreads();
+    lds_barrier();
 
-    const int th = tid >> 6, d2 = (tid & 63) * 2;  // head th, dims d2, d2+1
-    float M = sm_m[0][th];
-    for (int w = 1; w < DEC_WAVES; w++) M = fmaxf(M, sm_m[w][th]);
-    if (last_split) M = fmaxf(M, sm_m[DEC_WAVES][th]);
-    float L = 0.f, A0 = 0.f, A1 = 0.f;
+    // wave th merges head th: 8 wave partials + the current token, branch-free (a wave
+    // without keys has m = -1e30 and l = 0, so its weight is 0)
+    const int th = wave, d2 = lane * 2;
+    float mw[DEC_WAVES + 1], lw[DEC_WAVES + 1];
+#pragma unroll
     for (int w = 0; w < DEC_WAVES; w++) {
-        if (sm_l[w][th] == 0.f) continue;
-        const float c = exp2f(sm_m[w][th] - M);
-        L += sm_l[w][th] * c;
-        A0 += sm_acc[w][th][d2] * c;
-        A1 += sm_acc[w][th][d2 + 1] * c;
+        mw[w] = sm_m[w][th];
+        lw[w] = sm_l[w][th];
     }
-    if (last_split) {
-        const float c = exp2f(sm_m[DEC_WAVES][th] - M);
-        L += c;
+    mw[DEC_WAVES] = last_split ? sm_m[DEC_WAVES][th] : -1e30f;
+    lw[DEC_WAVES] = last_split ? 1.f : 0.f;
+    float M = mw[0];
+#pragma unroll
+    for (int w = 1; w <= DEC_WAVES; w++) M = fmaxf(M, mw[w]);
+    float L = 0.f, A0 = 0.f, A1 = 0.f;
+#pragma unroll
+    for (int w = 0; w < DEC_WAVES; w++) {
+        const float c = exp2f(mw[w] - M);
+        const float2 a = *(const float2 *)&sm_acc[w][th][d2];
+        L += lw[w] * c;
+        A0 += a.x * c;
+        A1 += a.y * c;
+    }
+    {
+        const float c = last_split ? exp2f(mw[DEC_WAVES] - M) : 0.f;
+        L += lw[DEC_WAVES] * c;
         A0 += sm_kv[1][d2] * c;
         A1 += sm_kv[1][d2 + 1] * c;
     }
     const int hout = kvh * GQA + th;
-    float *out = P.att + (size_t)seq * Q_DIM + hout * HEAD_DIM + d2;
-    const float sink = P.sinks[hout] * LOG2E;
     if (n_split == 1) {
+        float *out = att + (size_t)seq * Q_DIM + hout * HEAD_DIM + d2;
         const float Mf = fmaxf(M, sink), cs = exp2f(M - Mf);
         const float inv = 1.0f / (L * cs + exp2f(sink - Mf));
         *(float2 *)out = make_float2(A0 * cs * inv, A1 * cs * inv);
         return;
     }
-    const size_t head_base = ((size_t)seq * N_HEAD + hout) * P.max_split;
-    float *pp = P.partial + (head_base + split) * PART_STRIDE;
+    float *pp = partial + (((size_t)seq * N_HEAD + hout) * max_split + split) * PART_STRIDE;
     *(float2 *)(pp + d2) = make_float2(A0, A1);
-    if (d2 == 0) {
-        pp[HEAD_DIM] = M;
-        pp[HEAD_DIM + 1] = L;
-    }
+    if (lane == 0) *(float2 *)(pp + HEAD_DIM) = make_float2(M, L);
 }
 
 // LSE merge of the split partials plus the sink (fused.metal:331-350).
-// grid = (N_HEAD, n_seq), 256 threads: thread (dim group dg, split group sg) sums
-// dims 4dg..4dg+3 over splits sg, sg+8, ...; the first 64 splits' accumulators are
-// requested before the split weights are known, so the merge waits on about one
-// memory round trip.
+// grid = (N_HEAD, n_seq), 256 threads. Thread (dim group dg, split group sg) sums
+// dims 4dg..4dg+3 over splits sg, sg+8, ...; thread t also holds (m, l) of splits
+// t, t+256, ... All of it is requested at once, so the merge waits on one memory
+// round trip after the kernel arguments.
 __global__ __launch_bounds__(256) void attn_combine_kernel(const DecodeParams P) {
     __shared__ float w_s[MERGE_MAX_SPLIT];
     __shared__ float red[2][4];
     __shared__ float4 part[8][32];
     const int hh = blockIdx.x, seq = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int ns = P.split_prefix[seq + 1] - P.split_prefix[seq];
+    const int ns = P.n_split[seq], max_split = P.max_split;
+    const float *const partial = P.partial, *const sinks = P.sinks;
+    float *const att = P.att;
+    pin_sgpr(ns), pin_sgpr(max_split), pin_sgpr(partial), pin_sgpr(sinks), pin_sgpr(att);
     if (ns <= 1) return;  // written directly by the decode kernel
-    const float *pp = P.partial + ((size_t)seq * N_HEAD + hh) * P.max_split * PART_STRIDE;
+    const float *pp = partial + ((size_t)seq * N_HEAD + hh) * max_split * PART_STRIDE;
     const int dg = tid & 31, sg = tid >> 5;
     float4 x[8];
 #pragma unroll
     for (int i = 0; i < 8; i++) x[i] = *(const float4 *)(pp + min(sg + 8 * i, ns - 1) * PART_STRIDE + 4 * dg);
-    const float sink = P.sinks[hh] * LOG2E;
+    float2 ml[MERGE_MAX_SPLIT / 256];
+#pragma unroll
+    for (int j = 0; j < MERGE_MAX_SPLIT / 256; j++)
+        ml[j] = *(const float2 *)(pp + min(tid + 256 * j, ns - 1) * PART_STRIDE + HEAD_DIM);
+    const float sink = sinks[hh] * LOG2E;
     float M = sink;
-    for (int s = tid; s < ns; s += 256)
-        if (pp[s * PART_STRIDE + HEAD_DIM + 1] != 0.f) M = fmaxf(M, pp[s * PART_STRIDE + HEAD_DIM]);
+#pragma unroll
+    for (int j = 0; j < MERGE_MAX_SPLIT / 256; j++)
+        if (tid + 256 * j < ns && ml[j].y != 0.f) M = fmaxf(M, ml[j].x);
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) M = wave_max_xor(M, o);
     if (lane == 0) red[0][wave] = M;
     __syncthreads();
     M = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
     float L = 0.f;
-    for (int s = tid; s < ns; s += 256) {
-        const float ls = pp[s * PART_STRIDE + HEAD_DIM + 1];
-        const float w = ls != 0.f ? exp2f(pp[s * PART_STRIDE + HEAD_DIM] - M) : 0.f;
-        w_s[s] = w;
-        L += ls * w;
+#pragma unroll
+    for (int j = 0; j < MERGE_MAX_SPLIT / 256; j++) {
+        const int s = tid + 256 * j;
+        const float w = (s < ns && ml[j].y != 0.f) ? exp2f(ml[j].x - M) : 0.f;
+        if (s < ns) w_s[s] = w;
+        L += ml[j].y * w;
     }
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) L = wave_sum_xor(L, o);
@@ -436,13 +455,13 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const DecodeParams P)
             t.x += u.x; t.y += u.y; t.z += u.z; t.w += u.w;
         }
         const float inv = 1.0f / L;
-        *(float4 *)(P.att + (size_t)seq * Q_DIM + hh * HEAD_DIM + 4 * dg) =
+        *(float4 *)(att + (size_t)seq * Q_DIM + hh * HEAD_DIM + 4 * dg) =
             make_float4(t.x * inv, t.y * inv, t.z * inv, t.w * inv);
     }
 }
 
-hipError_t launch_decode(const DecodeParams &P, int dtype, int total_splits, hipStream_t stream) {
-    dim3 grid(total_splits, N_HEAD_KV), block(DEC_THREADS);
+hipError_t launch_decode(const DecodeParams &P, int dtype, hipStream_t stream) {
+    dim3 grid(P.max_split, N_HEAD_KV, P.n_seq), block(DEC_THREADS);
     if (dtype == DT_F16)
         hipLaunchKernelGGL(attn_decode_kernel<DT_F16>, grid, block, 0, stream, P);
     else

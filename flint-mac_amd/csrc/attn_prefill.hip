@@ -5,9 +5,9 @@
 // chunk at /root/reference/src/engine.mm:1087-1104).
 //
 //  qk_prep: per token, RMSNorm (+ NEOX RoPE) of the 32 q heads and 4 k heads;
-//    q goes out as f16 [32][T][128] pre-scaled by log2(e)/sqrt(128); K goes
-//    into the key buffer [4][row][128] and V, transposed in 32-row tiles,
-//    into [4][row/32][128][32].
+//    q goes out as f16 [32][T][128] pre-scaled by log2(e)/sqrt(128); K and V
+//    go into the key/value buffers in the cache's tiled layouts (kt_index,
+//    vt_index: 32-row tiles, K in MFMA-operand order, V transposed).
 //    Full-attention layers use the layer's cache directly (row = position).
 //    SWA layers attend from a scratch buffer covering [max(0, p0-512), p0+T)
 //    (the ring prefix [kbase, p0) is copied in first), and the positions
@@ -71,13 +71,12 @@ __global__ __launch_bounds__(256) void qk_prep_kernel(const PrefillParams P, int
             } else {
                 const int kvh = hr - N_HEAD;
                 const uint16_t k0 = KT::from_float(x0), k1 = KT::from_float(x1);
-                uint16_t *kd = P.kd + ((size_t)kvh * P.k_rows + (pos - P.kbase)) * HEAD_DIM;
-                kd[lane] = k0;
-                kd[lane + 64] = k1;
+                P.kd[kt_index(kvh, pos - P.kbase, lane, P.k_rows)] = k0;
+                P.kd[kt_index(kvh, pos - P.kbase, lane + 64, P.k_rows)] = k1;
                 if (P.ring_k && pos >= P.ring_from) {
-                    uint16_t *kr = P.ring_k + ((size_t)kvh * P.ring_slots + (pos & (P.ring_slots - 1))) * HEAD_DIM;
-                    kr[lane] = k0;
-                    kr[lane + 64] = k1;
+                    const int slot = pos & (P.ring_slots - 1);
+                    P.ring_k[kt_index(kvh, slot, lane, P.ring_slots)] = k0;
+                    P.ring_k[kt_index(kvh, slot, lane + 64, P.ring_slots)] = k1;
                 }
             }
         }
@@ -118,8 +117,8 @@ __global__ __launch_bounds__(256) void ring_prefix_kernel(const PrefillParams P)
         const int r = i >> 4, u = i & 15;
         if (r >= nc) continue;
         const int pos = P.kbase + c0 + r;
-        const u16x8 v = *(const u16x8 *)(P.ring_k + ((size_t)kvh * P.ring_slots + (pos & mask)) * HEAD_DIM + 8 * u);
-        *(u16x8 *)(P.kd + ((size_t)kvh * P.k_rows + (pos - P.kbase)) * HEAD_DIM + 8 * u) = v;
+        const u16x8 v = *(const u16x8 *)(P.ring_k + kt_index(kvh, pos & mask, 8 * u, P.ring_slots));
+        *(u16x8 *)(P.kd + kt_index(kvh, pos - P.kbase, 8 * u, P.k_rows)) = v;
     }
     for (int i = threadIdx.x; i < 64 * HEAD_DIM; i += 256) {  // V^T columns
         const int d = i >> 6, r = i & 63;
@@ -193,10 +192,13 @@ __global__ __launch_bounds__(256) void flash_prefill_kernel(const PrefillParams 
         for (int i = 0; i < 2; i++) {
             const int u = tid + 256 * i;
             {
-                const int key = u & 31, dg = u >> 5;
+                // 16-byte unit u of the tiled K block (contiguous read): key and dim group
+                // from the tile order (kt_index)
+                const int st = (u >> 8) & 1, c = (u >> 6) & 3, g = (u >> 4) & 3, n = u & 15;
+                const int key = 8 * (n >> 2) + 4 * st + (n & 3), dg = 4 * c + g;
                 f16x8 v = {};
                 if (r0 + key < n_valid) {
-                    const u16x8 raw = *(const u16x8 *)(P.kd + ((size_t)kvh * P.k_rows + r0 + key) * HEAD_DIM + 8 * dg);
+                    const u16x8 raw = *(const u16x8 *)(P.kd + kt_index(kvh, r0, 0, P.k_rows) + 8 * u);
 #pragma unroll
                     for (int e = 0; e < 8; e++) v[e] = to_f16<DT>(raw[e]);
                 }

@@ -69,6 +69,16 @@ __device__ inline f32x16 mfma32_f16(f16x8 a, f16x8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
+// K cache layout: per kv head, tiles of 32 slots (8 KiB each) stored in the order the
+// decode kernel's 16x16x32 MFMA A operand reads them, so each of its load
+// instructions reads 1 KiB contiguous: 16-byte unit (st*4 + c)*64 + 16g + n of a
+// tile holds slot 8(n>>2) + 4st + (n&3) of the tile, dims 32c + 8g .. 32c + 8g + 7.
+__host__ __device__ inline size_t kt_index(int kvh, int row, int dim, int rows) {
+    const int r = row & 31, st = (r >> 2) & 1, n = ((r >> 3) << 2) | (r & 3);
+    const int c = dim >> 5, g = (dim >> 3) & 3;
+    return ((size_t)kvh * (rows >> 5) + (row >> 5)) * (32 * HEAD_DIM) + ((((st * 4 + c) * 64 + g * 16 + n) << 3) | (dim & 7));
+}
+
 // V cache layout: per kv head, V transposed in tiles of 32 slots,
 // [kvh][rows/32][HEAD_DIM][32], so one 32-key tile of V^T is 8 KiB contiguous.
 __host__ __device__ inline size_t vt_index(int kvh, int row, int dim, int rows) {
@@ -78,6 +88,14 @@ __host__ __device__ inline size_t vt_index(int kvh, int row, int dim, int rows) 
 // Workgroup barrier that orders LDS only. __syncthreads() also orders global
 // memory, which the compiler implements by waiting for every outstanding global
 // load (s_waitcnt vmcnt(0)); this one leaves in-flight loads in flight.
+// Make the compiler materialise a wave-uniform value at this point: its scalar load is
+// issued here, together with the others pinned next to it, instead of being sunk to
+// its first use.
+template <typename T>
+__device__ inline void pin_sgpr(T x) {
+    asm volatile("" ::"s"(x));
+}
+
 __device__ inline void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
     __builtin_amdgcn_s_barrier();

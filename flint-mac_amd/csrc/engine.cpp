@@ -109,10 +109,12 @@ void validate_layer(const flint_attn_layer *L) {
 // the extra tiles.
 int plan_tiles_per_split(int total_tiles, int max_tiles, int keys_per_split) {
     if (keys_per_split > 0) return std::max(1, keys_per_split / 32);
+    // one split (no merge kernel) while a workgroup's 8 waves need at most 3 tiles each;
+    // otherwise spread the key tiles of all sequences over the 256 CUs, 8 tiles at least
+    if (max_tiles <= 3 * 8 && total_tiles * N_HEAD_KV <= 256) return std::max(max_tiles, 1);
     const int cus = 256;
-    if (total_tiles * N_HEAD_KV <= 16 * cus / 8 && max_tiles <= 64) return std::max(max_tiles, 1);
-    int tps = (total_tiles * N_HEAD_KV + cus - 1) / cus;
-    return std::max(16, (tps + 7) / 8 * 8);
+    const int tps = (total_tiles * N_HEAD_KV + cus - 1) / cus;
+    return std::max(8, (tps + 7) / 8 * 8);
 }
 
 // theta^(-2i/128) table, cached for the last theta
@@ -163,16 +165,13 @@ void decode_impl(const flint_attn_layer *L, int n_seq, int64_t seq_stride, const
         max_tiles = std::max(max_tiles, tiles[s]);
     }
     const int tps = plan_tiles_per_split(total_tiles, max_tiles, keys_per_split);
-    int total = 0, max_split = 1;
+    int max_split = 1;
     for (int s = 0; s < n_seq; s++) {
-        const int ns = std::max(1, (tiles[s] + tps - 1) / tps);
         P.pos[s] = pos[s];
-        P.tiles_per_split[s] = tps;
-        P.split_prefix[s] = total;
-        total += ns;
-        max_split = std::max(max_split, ns);
+        P.n_split[s] = std::max(1, (tiles[s] + tps - 1) / tps);
+        max_split = std::max(max_split, P.n_split[s]);
     }
-    P.split_prefix[n_seq] = total;
+    P.tiles_per_split = tps;
     P.max_split = max_split;
     if (max_split > 1024) throw Error("too many key splits (max 1024): raise keys_per_split");
     DeviceScratch &ws = scratch();
@@ -180,7 +179,7 @@ void decode_impl(const flint_attn_layer *L, int n_seq, int64_t seq_stride, const
         const size_t need = (size_t)n_seq * N_HEAD * max_split * PART_STRIDE * sizeof(float);
         P.partial = (float *)ws.partial.get(need);
     }
-    check(launch_decode(P, L->kv_dtype, total, stream), "decode launch");
+    check(launch_decode(P, L->kv_dtype, stream), "decode launch");
 }
 
 void prefill_impl(const flint_attn_layer *L, const float *qkv, int q_stride, int p0, int T, float *att,

@@ -16,7 +16,7 @@ struct DecodeParams {
     const float *q_norm;        // [128]
     const float *k_norm;        // [128]
     const float *sinks;         // [32]
-    uint16_t *k_cache;          // sequence 0: [4][n_slots][128]
+    uint16_t *k_cache;          // sequence 0: [4][n_slots/32][32*128] (kt_index layout)
     uint16_t *v_cache;          // sequence 0: [4][n_slots/32][128][32] (V^T in 32-slot tiles)
     long long seq_stride;       // elements between two sequences' K (and V) caches
     float *att;                 // [n_seq][4096]
@@ -24,15 +24,15 @@ struct DecodeParams {
     int n_slots;                // slots per kv head
     int slot_mask;              // SWA: n_slots - 1 (power of two); full: all ones
     int is_swa, has_rope, window, max_split;
+    int tiles_per_split;        // 32-key tiles per split (all sequences)
     float rms_eps;
-    float rope_freq[64];        // theta^(-2i/128), computed on the host like ref_model.cpp:55
     int n_seq;
-    int split_prefix[MAX_SEQ + 1];  // blocks [split_prefix[s], split_prefix[s+1]) serve sequence s
-    int pos[MAX_SEQ];
-    int tiles_per_split[MAX_SEQ];   // 32-key tiles per split
+    float rope_freq[64];        // theta^(-2i/128), computed on the host like ref_model.cpp:55
+    int pos[MAX_SEQ];           // sequence s decodes the token at pos[s]
+    int n_split[MAX_SEQ];       // key splits of sequence s (grid x covers max_split)
 };
 
-hipError_t launch_decode(const DecodeParams &P, int dtype, int total_splits, hipStream_t stream);
+hipError_t launch_decode(const DecodeParams &P, int dtype, hipStream_t stream);
 
 // Prefill: q/k prep (k_qk_prefill, prefill.metal:99-133) + flash attention
 // (k_attn_prefill, prefill.metal:141-266).
@@ -46,12 +46,12 @@ struct PrefillParams {
     float rope_freq[64];
     _Float16 *qh;         // [32][T][128] normed/roped q * log2(e)/sqrt(128), f16
     // keys/values the attention reads: key position kp lives at row kp - kbase
-    uint16_t *kd;         // [4][k_rows][128]
+    uint16_t *kd;         // [4][k_rows/32][32*128] (kt_index layout)
     uint16_t *vd;         // [4][k_rows/32][128][32]
     int k_rows;           // row capacity per kv head (multiple of 32)
     int kbase;
     // SWA ring (cache) written for positions >= ring_from; copied into kd/vd for [kbase, p0)
-    uint16_t *ring_k;     // [4][n_slots][128] or null
+    uint16_t *ring_k;     // [4][n_slots/32][32*128] (kt_index layout) or null
     uint16_t *ring_v;     // [4][n_slots/32][128][32]
     int ring_slots, ring_from;
     float *att;           // [T][4096]

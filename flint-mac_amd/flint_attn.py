@@ -109,6 +109,17 @@ def _call(fn, *args):
         raise FlintAttnError(err.value.decode())
 
 
+def k_tile_offsets():
+    """[32][128] element offsets, within one 32-slot K tile (4096 elements), of (slot % 32, dim):
+    the tile order of the K cache (kt_index in csrc/common.h)."""
+    import numpy as np
+    r = np.arange(32)[:, None]
+    d = np.arange(HEAD_DIM)[None, :]
+    st, n = (r >> 2) & 1, ((r >> 3) << 2) | (r & 3)
+    c, g = d >> 5, (d >> 3) & 3
+    return (((st * 4 + c) * 64 + g * 16 + n) << 3) | (d & 7)
+
+
 def _stream(stream):
     if stream is None:
         import torch
@@ -121,8 +132,9 @@ def _ptr(t):
 
 
 class KVLayer:
-    """One attention layer on the GPU: KV cache in HBM (K [4][n_slots][128], V transposed
-    in 32-slot tiles [4][n_slots/32][128][32]) and its q_norm / k_norm / sinks.
+    """One attention layer on the GPU: KV cache in HBM in 32-slot tiles (K [4][n_slots/32][4096]
+    in MFMA-operand order, see k_tile_offsets; V transposed, [4][n_slots/32][128][32]) and its
+    q_norm / k_norm / sinks.
     `n_seq` > 1 allocates independent caches for that many sequences."""
 
     def __init__(self, is_swa, has_rope, n_slots=None, kv_dtype="f16", rope_theta=1e4, window=N_SWA,
@@ -133,8 +145,8 @@ class KVLayer:
         if n_slots is None:
             n_slots = SWA_RING if is_swa else 4096
         self.n_slots, self.n_seq = int(n_slots), int(n_seq)
-        self.k = torch.zeros((n_seq, N_HEAD_KV, n_slots, HEAD_DIM), dtype=self.torch_dtype, device=device)
         assert self.n_slots % 32 == 0, "n_slots must be a multiple of 32"
+        self.k = torch.zeros((n_seq, N_HEAD_KV, n_slots // 32, 32 * HEAD_DIM), dtype=self.torch_dtype, device=device)
         self.v = torch.zeros((n_seq, N_HEAD_KV, n_slots // 32, HEAD_DIM, 32), dtype=self.torch_dtype, device=device)
         f = lambda a, n, d: torch.as_tensor(a if a is not None else [d] * n, dtype=torch.float32).to(device)
         self.q_norm = f(q_norm, HEAD_DIM, 1.0).contiguous()
@@ -149,6 +161,12 @@ class KVLayer:
     @property
     def seq_stride(self):
         return N_HEAD_KV * self.n_slots * HEAD_DIM
+
+    def k_slots(self):
+        """K as [n_seq][4][n_slots][128] (a copy out of the tiled layout)."""
+        import torch
+        idx = torch.as_tensor(k_tile_offsets().reshape(-1), device=self.k.device)
+        return self.k[..., idx].reshape(self.n_seq, N_HEAD_KV, self.n_slots, HEAD_DIM)
 
     def v_slots(self):
         """V as [n_seq][4][n_slots][128] (a copy out of the tiled layout)."""

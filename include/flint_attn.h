@@ -10,9 +10,11 @@
  * device workspace; callers serialise, as the reference requires of its
  * engine (/root/reference/src/capi.h:1).
  *
- * KV cache layout per layer and kv head (HBM, 16-bit elements):
- *   K: [N_HEAD_KV][n_slots][HEAD_DIM]           (row per slot)
- *   V: [N_HEAD_KV][n_slots/32][HEAD_DIM][32]    (transposed in tiles of 32 slots)
+ * KV cache layout per layer and kv head (HBM, 16-bit elements), in tiles of 32 slots:
+ *   K: [N_HEAD_KV][n_slots/32][4096]; within a tile, (slot r = slot % 32, dim d) is at
+ *      element 8*(((r>>2)&1)*256 + (d>>5)*64 + ((d>>3)&3)*16 + ((r>>3)<<2 | (r&3))) + (d&7)
+ *      (the order the decode kernel's MFMA reads K, so each load reads 1 KiB contiguous)
+ *   V: [N_HEAD_KV][n_slots/32][HEAD_DIM][32]   (V transposed within the tile)
  * SWA layers: n_slots is a power of two >= window (1024 for Flint) and
  * position p lives in slot p & (n_slots-1); full-attention layers: slot = p.
  * (The reference keeps position-major [slot][kv_head][128] for both,
@@ -51,7 +53,7 @@ extern "C" {
  * is_swa and has_rope are independent flags.
  */
 typedef struct {
-    void *k_cache;        /* device, layout above */
+    void *k_cache;        /* device, layout above (tiled K) */
     void *v_cache;        /* device, layout above (element (h, slot, d) at ((h*n_slots/32 + slot/32)*128 + d)*32 + slot%32) */
     int32_t n_slots;      /* multiple of 32; SWA: power of two >= window */
     int32_t kv_dtype;     /* FLINT_KV_F16 or FLINT_KV_BF16 */

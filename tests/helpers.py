@@ -39,14 +39,18 @@ def assert_close(got, want, what="", max_abs=MAX_ABS, mean_abs=MEAN_ABS):
 
 
 def to_cache_layout(K, V, n_slots, slots):
-    """Linear history rows K,V [n][512] placed at the given slots -> the cache layout:
-    K [4][n_slots][128] and V transposed in 32-slot tiles [4][n_slots/32][128][32]."""
+    """Linear history rows K,V [n][512] placed at the given slots -> the cache layout in
+    32-slot tiles: K [4][n_slots/32][4096] in the tile order of fa.k_tile_offsets(), V
+    transposed, [4][n_slots/32][128][32]."""
+    import flint_attn as fa
     n = K.shape[0]
-    Kc = np.zeros((N_HEAD_KV, n_slots, HEAD_DIM), np.float32)
+    Ks = np.zeros((N_HEAD_KV, n_slots, HEAD_DIM), np.float32)
     Vs = np.zeros((N_HEAD_KV, n_slots, HEAD_DIM), np.float32)
     slots = np.asarray(slots)
-    Kc[:, slots, :] = K.reshape(n, N_HEAD_KV, HEAD_DIM).transpose(1, 0, 2)
+    Ks[:, slots, :] = K.reshape(n, N_HEAD_KV, HEAD_DIM).transpose(1, 0, 2)
     Vs[:, slots, :] = V.reshape(n, N_HEAD_KV, HEAD_DIM).transpose(1, 0, 2)
+    Kc = np.zeros((N_HEAD_KV, n_slots // 32, 32 * HEAD_DIM), np.float32)
+    Kc[:, :, fa.k_tile_offsets().reshape(-1)] = Ks.reshape(N_HEAD_KV, n_slots // 32, 32 * HEAD_DIM)
     Vc = np.ascontiguousarray(Vs.reshape(N_HEAD_KV, n_slots // 32, 32, HEAD_DIM).transpose(0, 1, 3, 2))
     return Kc, Vc
 

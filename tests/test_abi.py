@@ -138,3 +138,21 @@ def test_engine_create_rejects_bad_arguments():
     assert b"kv_dtype" in err.value
     assert L.flint_attn_engine_n_layer(None) == 0
     assert not L.flint_attn_engine_layer(None, 0)
+
+
+def test_k_tile_layout_is_a_permutation_read_in_contiguous_units():
+    """The K cache tile order (include/flint_attn.h): a bijection of the 32 x 128 tile onto its
+    4096 elements, in which the 16-byte unit read by lane l of the decode kernel's load
+    instruction (st, c) is unit (st*4 + c)*64 + l and holds 8 consecutive dims of one slot."""
+    import numpy as np
+    o = fa.k_tile_offsets()
+    assert sorted(o.reshape(-1).tolist()) == list(range(4096))
+    assert np.all(o[:, 0::8] % 8 == 0) and np.all(np.diff(o.reshape(32, 16, 8), axis=2) == 1)
+    for st in range(2):
+        for c in range(4):
+            units = []
+            for lane in range(64):
+                n, g = lane & 15, lane >> 4
+                slot = 8 * (n >> 2) + 4 * st + (n & 3)
+                units.append(o[slot, 32 * c + 8 * g] // 8)
+            assert units == list(range((st * 4 + c) * 64, (st * 4 + c) * 64 + 64))

@@ -61,7 +61,7 @@ def test_decode_swa_ring_steps_config2(cuda, store):
     assert_close(got, want, "all steps")
     # ring: slot p & 1023 holds position p for the last 1024 positions
     vc = kv.v_slots()[0].float().cpu().numpy()  # [4][1024][128]
-    kc = kv.k[0].float().cpu().numpy()  # [4][1024][128]
+    kc = kv.k_slots()[0].float().cpu().numpy()  # [4][1024][128]
     for p in range(max(0, n - 1024), n):
         s = p & 1023
         assert np.array_equal(vc[:, s, :], V[p].reshape(N_HEAD_KV, HEAD_DIM)), f"V slot {s} pos {p}"

@@ -68,7 +68,7 @@ def test_prefill_4000_config4(cuda, store, is_swa):
         assert_close(got[p], w, f"pos {p}")
     assert_close(np.stack([got[p] for p in want]), np.stack(list(want.values())), "probes")
     vc = kv.v_slots()[0].float().cpu().numpy()
-    kc = kv.k[0].float().cpu().numpy()
+    kc = kv.k_slots()[0].float().cpu().numpy()
     lo = T - 1024 if is_swa else 0
     for p in range(lo, T):
         s = kv.slot(p)
