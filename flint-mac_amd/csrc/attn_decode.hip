@@ -97,8 +97,8 @@ __device__ inline void consume_tile(DecodeState<DT> &S, KvTile &T, const typenam
     float sc[8];  // keys kb + 8g + j: j < 4 from s0, j >= 4 from s1; hi + lo columns summed
 #pragma unroll
     for (int r = 0; r < 4; r++) {
-        sc[r] = s0[r] + __shfl_xor(s0[r], 8, 64);
-        sc[4 + r] = s1[r] + __shfl_xor(s1[r], 8, 64);
+        sc[r] = s0[r] + lane_xor8(s0[r]);
+        sc[4 + r] = s1[r] + lane_xor8(s1[r]);
     }
     const int kb = t * 32;
     if (kb < k_begin || kb + 32 > pos) {  // wave-uniform: a tile at either end of the key range
@@ -121,8 +121,7 @@ __device__ inline void consume_tile(DecodeState<DT> &S, KvTile &T, const typenam
     float mt = sc[0];
 #pragma unroll
     for (int j = 1; j < 8; j++) mt = fmaxf(mt, sc[j]);
-    mt = wave_max_xor(mt, 16);
-    mt = wave_max_xor(mt, 32);
+    mt = xor32_max(xor16_max(mt));
     const float m_new = fmaxf(S.m, mt);
     const float corr = exp2f(S.m - m_new);
     float psum = 0.f;
@@ -159,9 +158,7 @@ __device__ inline void rope_sincos(float a, float *sn, float *cs) {
 // lane and lane + 64 (a NEOX pair, x) with their gains (w), cs/sn the rotation
 // of frequency `lane`.
 __device__ inline float2 norm_rope_pair(float2 x, float2 w, float eps, bool rope, float cs, float sn) {
-    float ss = x.x * x.x + x.y * x.y;
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    const float ss = wave_sum(x.x * x.x + x.y * x.y);
     const float scale = 1.0f / sqrtf(ss / HEAD_DIM + eps);
     float x0 = x.x * scale * w.x, x1 = x.y * scale * w.y;
     if (rope) {
@@ -316,13 +313,12 @@ __global__ __launch_bounds__(DEC_THREADS) void attn_decode_kernel(const DecodePa
     }
 
     // ---- merge hi/lo columns and the waves (and the current token) through LDS ----
-    S.l = wave_sum_xor(S.l, 16);
-    S.l = wave_sum_xor(S.l, 32);
+    S.l = xor32_sum(xor16_sum(S.l));
 #pragma unroll
     for (int d = 0; d < 8; d++) {
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-            const float v = S.acc[d][r] + __shfl_xor(S.acc[d][r], 8, 64);
+            const float v = S.acc[d][r] + lane_xor8(S.acc[d][r]);
             if (hl == 0) sm_acc[wave][hloc][16 * d + 4 * g + r] = v;
         }
     }
@@ -333,8 +329,7 @@ __global__ __launch_bounds__(DEC_THREADS) void attn_decode_kernel(const DecodePa
     if (last_split) {
         // score of the current token for head `wave` (q in fp32, k as the cache holds it)
         float dot = sm_q[wave][lane] * sm_kv[0][lane] + sm_q[wave][lane + 64] * sm_kv[0][lane + 64];
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) dot += __shfl_xor(dot, o, 64);
+        dot = wave_sum(dot);
         if (lane == 0) {
             sm_m[DEC_WAVES][wave] = dot;
             sm_l[DEC_WAVES][wave] = 1.f;
@@ -365,8 +360,8 @@ __global__ __launch_bounds__(DEC_THREADS) void attn_decode_kernel(const DecodePa
         A0 += a.x * c;
         A1 += a.y * c;
     }
-    {
-        const float c = last_split ? exp2f(mw[DEC_WAVES] - M) : 0.f;
+    if (last_split) {  // sm_kv is written only in the last split: elsewhere it is stale LDS
+        const float c = exp2f(mw[DEC_WAVES] - M);
         L += lw[DEC_WAVES] * c;
         A0 += sm_kv[1][d2] * c;
         A1 += sm_kv[1][d2 + 1] * c;
@@ -413,8 +408,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const DecodeParams P)
 #pragma unroll
     for (int j = 0; j < MERGE_MAX_SPLIT / 256; j++)
         if (tid + 256 * j < ns && ml[j].y != 0.f) M = fmaxf(M, ml[j].x);
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) M = wave_max_xor(M, o);
+    M = wave_max(M);
     if (lane == 0) red[0][wave] = M;
     __syncthreads();
     M = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
@@ -426,8 +420,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const DecodeParams P)
         if (s < ns) w_s[s] = w;
         L += ml[j].y * w;
     }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) L = wave_sum_xor(L, o);
+    L = wave_sum(L);
     if (lane == 0) red[1][wave] = L;
     __syncthreads();
     L = red[1][0] + red[1][1] + red[1][2] + red[1][3] + exp2f(sink - M);

@@ -105,4 +105,51 @@ __device__ inline void lds_barrier() {
 __device__ inline float wave_sum_xor(float v, int mask) { return v + __shfl_xor(v, mask, 64); }
 __device__ inline float wave_max_xor(float v, int mask) { return fmaxf(v, __shfl_xor(v, mask, 64)); }
 
+// Cross-lane steps on VALU lane permutes instead of LDS shuffles (ds_bpermute, one LDS
+// round trip each): DPP rotations within a row of 16 lanes, and gfx950's
+// v_permlane16_swap / v_permlane32_swap across rows and wave halves.
+template <int CTRL>
+__device__ inline float dpp(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false));
+}
+constexpr int DPP_ROR1 = 0x121, DPP_ROR2 = 0x122, DPP_ROR4 = 0x124, DPP_ROR8 = 0x128;  // row_ror:n
+
+// x of lane l ^ 8 (a rotation by 8 within the row of 16)
+__device__ inline float lane_xor8(float x) { return dpp<DPP_ROR8>(x); }
+
+// f(x of lane l, x of lane l ^ 16): the swap leaves rows (0,0,2,2) in one register and
+// (1,1,3,3) in the other, so every lane combines the same pair in the same order.
+__device__ inline float xor16_sum(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ inline float xor16_max(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+// f(x of lane l, x of lane l ^ 32): halves (lo, lo) and (hi, hi)
+__device__ inline float xor32_sum(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ inline float xor32_max(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+// Sum / max over the 64 lanes of the wave (every lane gets it).
+__device__ inline float wave_sum(float x) {
+    x += dpp<DPP_ROR8>(x);
+    x += dpp<DPP_ROR4>(x);
+    x += dpp<DPP_ROR2>(x);
+    x += dpp<DPP_ROR1>(x);
+    return xor32_sum(xor16_sum(x));
+}
+__device__ inline float wave_max(float x) {
+    x = fmaxf(x, dpp<DPP_ROR8>(x));
+    x = fmaxf(x, dpp<DPP_ROR4>(x));
+    x = fmaxf(x, dpp<DPP_ROR2>(x));
+    x = fmaxf(x, dpp<DPP_ROR1>(x));
+    return xor32_max(xor16_max(x));
+}
+
 }  // namespace flint
