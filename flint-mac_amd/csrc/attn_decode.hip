@@ -47,6 +47,9 @@ constexpr int PART_STRIDE = 132;
 constexpr int DEC_WAVES = 8;
 constexpr int DEC_THREADS = DEC_WAVES * 64;
 constexpr int MERGE_MAX_SPLIT = 1024;
+// LDS row of a wave's partial accumulator for one head: 128 floats + 4 of padding, so the
+// 32 lanes that write 16 bytes each spread evenly over the banks
+constexpr int ACC_ROW = HEAD_DIM + 4;
 
 struct KvTile {
     u32x4 k[2][4];  // K rows: sub-tile st, dim chunk c (8 packed 16-bit values each)
@@ -83,6 +86,29 @@ struct DecodeState {
     f32x4 acc[8];    // O^T tile d: rows = dims 16d + 4g + r, column = this lane's (head, hi/lo)
 };
 
+// The running max is raised only when a score exceeds it by more than this (log2 units),
+// so p = 2^(s - m) stays below 2^8 and the rescale of l and acc runs on few tiles.
+constexpr float RESCALE_LOG2 = 8.f;
+
+// P in two 16-bit halves: word = (p0, p1) packed as hi parts (hl == 0) or as the
+// residuals p - hi (hl == 1). Both halves are rounded toward zero; their sum carries p
+// to ~2^-22 relative for f16 (2^-16 for bf16).
+template <int DT>
+__device__ inline uint32_t split_pack(float p0, float p1, int hl);
+template <>
+__device__ inline uint32_t split_pack<DT_F16>(float p0, float p1, int hl) {
+    const auto h = __builtin_amdgcn_cvt_pkrtz(p0, p1);
+    const auto l = __builtin_amdgcn_cvt_pkrtz(p0 - (float)h[0], p1 - (float)h[1]);
+    return hl ? __builtin_bit_cast(uint32_t, l) : __builtin_bit_cast(uint32_t, h);
+}
+template <>
+__device__ inline uint32_t split_pack<DT_BF16>(float p0, float p1, int hl) {
+    const uint32_t b0 = __float_as_uint(p0), b1 = __float_as_uint(p1);
+    const float r0 = p0 - __uint_as_float(b0 & 0xffff0000u), r1 = p1 - __uint_as_float(b1 & 0xffff0000u);
+    const uint32_t c0 = hl ? __float_as_uint(r0) : b0, c1 = hl ? __float_as_uint(r1) : b1;
+    return (c1 & 0xffff0000u) | (c0 >> 16);
+}
+
 // Online-softmax update with one 32-key tile.
 template <int DT>
 __device__ inline void consume_tile(DecodeState<DT> &S, KvTile &T, const typename KvType<DT>::vec8 (&qb)[4], int t,
@@ -118,31 +144,25 @@ __device__ inline void consume_tile(DecodeState<DT> &S, KvTile &T, const typenam
 #pragma unroll
             for (int w = 0; w < 4; w++) T.v[d][w] &= vmask[w];
     }
-    float mt = sc[0];
-#pragma unroll
-    for (int j = 1; j < 8; j++) mt = fmaxf(mt, sc[j]);
+    float mt = fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])), fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7])));
     mt = xor32_max(xor16_max(mt));
-    const float m_new = fmaxf(S.m, mt);
-    const float corr = exp2f(S.m - m_new);
-    float psum = 0.f;
-    uint16_t ph[8];
+    if (__builtin_amdgcn_ballot_w64(mt > S.m + RESCALE_LOG2) != 0) {  // wave-uniform
+        const float m_new = fmaxf(S.m, mt);
+        const float corr = __builtin_amdgcn_exp2f(S.m - m_new);
+        S.l *= corr;
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
-        const float p = exp2f(sc[j] - m_new);
-        psum += p;
-        const uint16_t hi = KT::from_float(p);
-        const uint16_t lo = KT::from_float(p - KT::to_float(hi));
-        ph[j] = hl ? lo : hi;
+        for (int d = 0; d < 8; d++) S.acc[d] *= corr;
+        S.m = m_new;
     }
-    const u32x4 pu = {pack2(ph[0], ph[1]), pack2(ph[2], ph[3]), pack2(ph[4], ph[5]), pack2(ph[6], ph[7])};
-    S.l = S.l * corr + psum;
-    S.m = m_new;
+    float p[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) p[j] = __builtin_amdgcn_exp2f(sc[j] - S.m);
+    S.l += ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+    const u32x4 pu = {split_pack<DT>(p[0], p[1], hl), split_pack<DT>(p[2], p[3], hl), split_pack<DT>(p[4], p[5], hl),
+                      split_pack<DT>(p[6], p[7], hl)};
     const typename KT::vec8 pb = __builtin_bit_cast(typename KT::vec8, pu);
 #pragma unroll
-    for (int d = 0; d < 8; d++) {
-        S.acc[d] *= corr;
-        S.acc[d] = KT::mfma16(__builtin_bit_cast(typename KT::vec8, T.v[d]), pb, S.acc[d]);
-    }
+    for (int d = 0; d < 8; d++) S.acc[d] = KT::mfma16(__builtin_bit_cast(typename KT::vec8, T.v[d]), pb, S.acc[d]);
 }
 
 // sin/cos of a RoPE angle (a float, as the reference computes it): the angle
@@ -210,7 +230,7 @@ __global__ __launch_bounds__(DEC_THREADS) void attn_decode_kernel(const DecodePa
     __shared__ uint16_t sm_qh[2][GQA][HEAD_DIM];   // [hi/lo][head][dim]
     __shared__ float sm_q[GQA][HEAD_DIM];          // log2(e)/sqrt(D)-scaled q (for the current token)
     __shared__ float sm_kv[2][HEAD_DIM];           // current token: k and v as the cache holds them
-    __shared__ float sm_acc[DEC_WAVES][GQA][HEAD_DIM];  // reused as split weights by the final merge
+    __shared__ float sm_acc[DEC_WAVES][GQA][ACC_ROW];  // wave partial accumulators (padded rows)
     __shared__ float sm_m[DEC_WAVES + 1][GQA], sm_l[DEC_WAVES + 1][GQA];
 
     // ---- the prologue's inputs first, then this wave's first two tiles: vmcnt counts
@@ -230,9 +250,13 @@ __global__ __launch_bounds__(DEC_THREADS) void attn_decode_kernel(const DecodePa
         vx = make_float2(vr[lane], vr[lane + 64]);
     }
     __builtin_amdgcn_sched_barrier(0);
-    // Issued unconditionally (a wave without such a tile re-reads tile t_begin, which
-    // is in range and never consumed): loads under a branch make the compiler's wait
-    // counting at the join conservative, and the prologue would then wait for the tiles.
+    // The first two tiles, before the prologue waits for its own loads, so tile latency
+    // overlaps the prologue. Issued unconditionally (a wave without such a tile reads 16
+    // bytes per load of tile t_begin, never consumed), since loads under a branch make the
+    // compiler's wait counting at the join conservative. (Under a full stream a wave's
+    // later load instructions stall at issue until the CU has room for them, so at long
+    // contexts the prologue ends only as the stream does; the tiles land no earlier when
+    // the prologue goes first, so nothing is gained by reordering.)
     KvTile ta, tb;
     int t_a = t_begin + wave, t_b = t_a + DEC_WAVES;
     load_tile(ta, kc, vc, t_a < t_end ? t_a : t_begin, lane, slot_mask, t_a < t_end);
@@ -277,6 +301,16 @@ __global__ __launch_bounds__(DEC_THREADS) void attn_decode_kernel(const DecodePa
     vec8 qb[4];  // MFMA B operand: column n = head hloc, hi or lo half; k = dims 32c + 8g + e
 #pragma unroll
     for (int c = 0; c < 4; c++) qb[c] = *(const vec8 *)&sm_qh[hl][hloc][32 * c + 8 * g];
+    if (last_split) {
+        // score of the current token for head `wave` (q in fp32, k as the cache holds it),
+        // computed while the first tiles stream in
+        float dot = sm_q[wave][lane] * sm_kv[0][lane] + sm_q[wave][lane + 64] * sm_kv[0][lane + 64];
+        dot = wave_sum(dot);
+        if (lane == 0) {
+            sm_m[DEC_WAVES][wave] = dot;
+            sm_l[DEC_WAVES][wave] = 1.f;
+        }
+    }
 
     // ---- stream this wave's tiles t_begin + wave + 8i, two in flight ----
     DecodeState<DT> S;
@@ -284,56 +318,42 @@ __global__ __launch_bounds__(DEC_THREADS) void attn_decode_kernel(const DecodePa
     S.l = 0.f;
 #pragma unroll
     for (int d = 0; d < 8; d++) S.acc[d] = f32x4{0.f, 0.f, 0.f, 0.f};
-    // The first pair runs straight-line (exact wait counts: consuming tile a leaves
-    // tile b in flight). Later tiles go through a loop in which b streams in while a
-    // is consumed, then moves into a's registers while the next tile is requested.
-    // The scheduling barriers keep each refill after the consumption of the tile it
-    // replaces (a third tile of registers would spill).
-    if (t_a < t_end) consume_tile<DT>(S, ta, qb, t_a, k_begin, pos, g, hl);
-    __builtin_amdgcn_sched_barrier(0);
-    if (t_b < t_end) {
-        const int t_c = t_b + DEC_WAVES;
-        if (t_c < t_end) load_tile(ta, kc, vc, t_c, lane, slot_mask, true);
-        __builtin_amdgcn_sched_barrier(0);
+    // Two register sets, each refilled with the tile 16 further on as soon as it is
+    // consumed. The steady-state loop runs while both refills are needed, so its loads
+    // are unconditional and the wait counts static (consuming a tile waits for its own
+    // 16 loads only); the drain then handles the last two or three tiles, issuing no
+    // load that will not be consumed except in the three-tile case.
+    while (t_b + 2 * DEC_WAVES < t_end) {
+        consume_tile<DT>(S, ta, qb, t_a, k_begin, pos, g, hl);
+        t_a += 2 * DEC_WAVES;
+        load_tile(ta, kc, vc, t_a, lane, slot_mask, true);
         consume_tile<DT>(S, tb, qb, t_b, k_begin, pos, g, hl);
-        __builtin_amdgcn_sched_barrier(0);
-        t_a = t_c;
-        t_b = t_c + DEC_WAVES;
-        if (t_b < t_end) load_tile(tb, kc, vc, t_b, lane, slot_mask, true);
-        __builtin_amdgcn_sched_barrier(0);
-        while (t_a < t_end) {
-            consume_tile<DT>(S, ta, qb, t_a, k_begin, pos, g, hl);
-            __builtin_amdgcn_sched_barrier(0);
-            ta = tb;
-            t_a = t_b;
-            t_b += DEC_WAVES;
-            if (t_b < t_end) load_tile(tb, kc, vc, t_b, lane, slot_mask, true);
-            __builtin_amdgcn_sched_barrier(0);
-        }
+        t_b += 2 * DEC_WAVES;
+        load_tile(tb, kc, vc, t_b, lane, slot_mask, true);
+    }
+    if (t_a < t_end) {
+        consume_tile<DT>(S, ta, qb, t_a, k_begin, pos, g, hl);
+        t_a += 2 * DEC_WAVES;
+        const bool third = t_a < t_end;
+        // unconditional (16 bytes per load when there is no third tile): tile b's wait
+        // stays exact while the third tile streams in
+        load_tile(ta, kc, vc, third ? t_a : t_begin, lane, slot_mask, third);
+        if (t_b < t_end) consume_tile<DT>(S, tb, qb, t_b, k_begin, pos, g, hl);
+        if (third) consume_tile<DT>(S, ta, qb, t_a, k_begin, pos, g, hl);
     }
 
     // ---- merge hi/lo columns and the waves (and the current token) through LDS ----
     S.l = xor32_sum(xor16_sum(S.l));
 #pragma unroll
     for (int d = 0; d < 8; d++) {
+        f32x4 v;
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const float v = S.acc[d][r] + lane_xor8(S.acc[d][r]);
-            if (hl == 0) sm_acc[wave][hloc][16 * d + 4 * g + r] = v;
-        }
+        for (int r = 0; r < 4; r++) v[r] = S.acc[d][r] + lane_xor8(S.acc[d][r]);
+        if (hl == 0) *(f32x4 *)&sm_acc[wave][hloc][16 * d + 4 * g] = v;
     }
     if (hl == 0 && g == 0) {
         sm_m[wave][hloc] = S.m;
         sm_l[wave][hloc] = S.l;
-    }
-    if (last_split) {
-        // score of the current token for head `wave` (q in fp32, k as the cache holds it)
-        float dot = sm_q[wave][lane] * sm_kv[0][lane] + sm_q[wave][lane + 64] * sm_kv[0][lane + 64];
-        dot = wave_sum(dot);
-        if (lane == 0) {
-            sm_m[DEC_WAVES][wave] = dot;
-            sm_l[DEC_WAVES][wave] = 1.f;
-        }
     }
     lds_barrier();
 
@@ -354,14 +374,14 @@ __global__ __launch_bounds__(DEC_THREADS) void attn_decode_kernel(const DecodePa
     float L = 0.f, A0 = 0.f, A1 = 0.f;
 #pragma unroll
     for (int w = 0; w < DEC_WAVES; w++) {
-        const float c = exp2f(mw[w] - M);
+        const float c = __builtin_amdgcn_exp2f(mw[w] - M);
         const float2 a = *(const float2 *)&sm_acc[w][th][d2];
         L += lw[w] * c;
         A0 += a.x * c;
         A1 += a.y * c;
     }
     if (last_split) {  // sm_kv is written only in the last split: elsewhere it is stale LDS
-        const float c = exp2f(mw[DEC_WAVES] - M);
+        const float c = __builtin_amdgcn_exp2f(mw[DEC_WAVES] - M);
         L += lw[DEC_WAVES] * c;
         A0 += sm_kv[1][d2] * c;
         A1 += sm_kv[1][d2 + 1] * c;
@@ -369,8 +389,8 @@ __global__ __launch_bounds__(DEC_THREADS) void attn_decode_kernel(const DecodePa
     const int hout = kvh * GQA + th;
     if (n_split == 1) {
         float *out = att + (size_t)seq * Q_DIM + hout * HEAD_DIM + d2;
-        const float Mf = fmaxf(M, sink), cs = exp2f(M - Mf);
-        const float inv = 1.0f / (L * cs + exp2f(sink - Mf));
+        const float Mf = fmaxf(M, sink), cs = __builtin_amdgcn_exp2f(M - Mf);
+        const float inv = 1.0f / (L * cs + __builtin_amdgcn_exp2f(sink - Mf));
         *(float2 *)out = make_float2(A0 * cs * inv, A1 * cs * inv);
         return;
     }
