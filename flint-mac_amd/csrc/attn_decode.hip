@@ -165,30 +165,6 @@ __device__ inline void consume_tile(DecodeState<DT> &S, KvTile &T, const typenam
     for (int d = 0; d < 8; d++) S.acc[d] = KT::mfma16(__builtin_bit_cast(typename KT::vec8, T.v[d]), pb, S.acc[d]);
 }
 
-// sin/cos of a RoPE angle (a float, as the reference computes it): the angle
-// reaches ~6.5e4 rad at long context, so it is first reduced modulo 2*pi in
-// double precision (error ~1e-11 rad) to keep sincosf on its short path.
-__device__ inline void rope_sincos(float a, float *sn, float *cs) {
-    const double twopi = 6.283185307179586476925286766559;
-    const double r = (double)a - twopi * rint((double)a * (1.0 / twopi));
-    sincosf((float)r, sn, cs);
-}
-
-// RMSNorm (+ NEOX RoPE) of one 128-dim head row by one wave: lane holds dims
-// lane and lane + 64 (a NEOX pair, x) with their gains (w), cs/sn the rotation
-// of frequency `lane`.
-__device__ inline float2 norm_rope_pair(float2 x, float2 w, float eps, bool rope, float cs, float sn) {
-    const float ss = wave_sum(x.x * x.x + x.y * x.y);
-    const float scale = 1.0f / sqrtf(ss / HEAD_DIM + eps);
-    float x0 = x.x * scale * w.x, x1 = x.y * scale * w.y;
-    if (rope) {
-        const float y0 = x0 * cs - x1 * sn, y1 = x0 * sn + x1 * cs;
-        x0 = y0;
-        x1 = y1;
-    }
-    return make_float2(x0, x1);
-}
-
 template <int DT>
 __global__ __launch_bounds__(DEC_THREADS) void attn_decode_kernel(const DecodeParams P) {
     typedef KvType<DT> KT;

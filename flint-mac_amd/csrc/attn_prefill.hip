@@ -4,26 +4,57 @@
 // (/root/reference/src/metal/prefill.metal:99-266, dispatched per 512-token
 // chunk at /root/reference/src/engine.mm:1087-1104).
 //
-//  qk_prep: per token, RMSNorm (+ NEOX RoPE) of the 32 q heads and 4 k heads;
-//    q goes out as f16 [32][T][128] pre-scaled by log2(e)/sqrt(128); K and V
-//    go into the key/value buffers in the cache's tiled layouts (kt_index,
-//    vt_index: 32-row tiles, K in MFMA-operand order, V transposed).
-//    Full-attention layers use the layer's cache directly (row = position).
-//    SWA layers attend from a scratch buffer covering [max(0, p0-512), p0+T)
-//    (the ring prefix [kbase, p0) is copied in first), and the positions
-//    p >= p0 + T - n_slots are also written to ring slot p & (n_slots-1),
-//    so one launch serves any T (the reference chunks by 512 for ring room,
-//    flint_config.h:29-31).
-//  flash attention: one workgroup per (32-position query block, kv head) and
-//    all 8 q heads of the group, so a K/V tile is staged in LDS once for 256
-//    query rows. Scores are S^T = K * Q^T and O^T += V^T * P^T on
-//    v_mfma_f32_32x32x16_f16 with fp32 accumulation; the online softmax starts
-//    from m = sink, l = 1 (the sink is in the denominator only, prefill.metal:162);
-//    mask: kp <= qp and (full or qp - kp < window) (prefill.metal:212).
+// Three launches per layer call, stream-ordered:
+//  prefix:  positions [kbase, p0) already in the layer's cache are converted
+//           into the attention copy (f16, below). kbase = 0 for full layers,
+//           max(0, p0 - 512) for SWA layers (the window of the first new token).
+//  kv_prep: per new token, RMSNorm (+ NEOX RoPE) of the 4 k heads and the v
+//           rows, rounded to the cache dtype, into the cache (SWA: only the last
+//           n_slots positions, slot p & (n_slots-1)) and into the attention copy.
+//           The prefix runs first because a long SWA prefill overwrites ring
+//           slots the prefix reads.
+//  flash:   one workgroup per (32-position query block, kv head) serves the 8 q
+//           heads of the group (256 query rows, 8 waves x 1 head x 32 rows), so
+//           a K/V tile is staged in LDS once per 256 rows. Q is normalised,
+//           rotated and scaled in the prologue (q never round-trips through HBM).
+//           Scores are S^T = K Q^T and O^T += V^T P^T on v_mfma_f32_32x32x16_f16
+//           with fp32 accumulation; K/V stream in 64-key stages, double-buffered
+//           in LDS with the next stage's loads in flight during the MFMAs; the
+//           online softmax starts from m = sink, l = 1 (the sink is in the
+//           denominator only, prefill.metal:162), raises its running max lazily
+//           (only past a margin of 2^8) and masks kp <= qp and, on SWA layers,
+//           qp - kp < window (prefill.metal:212).
+// Any T in one call: the attention copy is a linear buffer of kbase..p0+T, so
+// the reference's 512-token chunking (ring room, flint_config.h:29-31) is not
+// needed.
 #include "common.h"
 #include "flint_attn_internal.h"
 
 namespace flint {
+
+constexpr int PF_BQ = 32;  // query positions per workgroup
+constexpr int PF_BK = 64;  // keys per LDS stage (two 32-key MFMA tiles)
+constexpr float PF_RESCALE_LOG2 = 8.f;  // lazy running-max margin (p stays below 2^8)
+
+// S^T row i (MFMA A row) holds key sigma(i) of its 32-key tile: bits 2 and 3 of i
+// swapped, so that a lane's 16 score rows are, per 16-key half, 8 consecutive keys
+// (the P^T operand of the P*V MFMA then needs no data movement). An involution.
+__host__ __device__ inline int pf_sigma(int i) { return (i & 0x13) | ((i & 4) << 1) | ((i & 8) >> 1); }
+
+// Attention copy of K and V (f16), per kv head in 32-key tiles of 16 rows x 64
+// units of 16 bytes (16 KiB), in the order the flash kernel's MFMAs read them from
+// LDS, one unit per lane:
+//   rows 0..7  (K, row st):            unit l = key pf_sigma(l & 31), dims 16st + 8(l>>5) .. +7
+//   rows 8..15 (V^T, row 8 + 2dt + kk): unit l = dim 32dt + (l & 31), keys 16kk + 8(l>>5) .. +7
+__device__ inline size_t pk_index(int kvh, int row, int dim, int rows) {
+    const size_t tile = (size_t)kvh * (rows >> 5) + (row >> 5);
+    return (tile * 16 + (dim >> 4)) * 512 + ((((dim >> 3) & 1) * 32 + pf_sigma(row & 31)) << 3) + (dim & 7);
+}
+__device__ inline size_t pv_index(int kvh, int row, int dim, int rows) {
+    const size_t tile = (size_t)kvh * (rows >> 5) + (row >> 5);
+    const int k = row & 31;
+    return (tile * 16 + 8 + (dim >> 5) * 2 + (k >> 4)) * 512 + ((((k >> 3) & 1) * 32 + (dim & 31)) << 3) + (k & 7);
+}
 
 template <int DT>
 __device__ inline _Float16 to_f16(uint16_t u) {
@@ -31,204 +62,172 @@ __device__ inline _Float16 to_f16(uint16_t u) {
 }
 
 // ---------------------------------------------------------------------------
-// qk_prep. Blocks [0, T): q/k of one token. Blocks [T, T + nv): a 64-token V
-// tile of one kv head.
+// prefix: cache -> attention copy for positions [kbase, p0). grid (chunks of 64, kv head).
 template <int DT>
-__global__ __launch_bounds__(256) void qk_prep_kernel(const PrefillParams P, int nv) {
-    typedef KvType<DT> KT;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int b = blockIdx.x;
-    if (b < P.T) {
-        const int t = b, pos = P.p0 + t;
-        const float *row = P.qkv + (size_t)t * P.q_stride;
-        float cs = 1.f, sn = 0.f;
-        if (P.has_rope) {
-            const float a = (float)pos * P.rope_freq[lane];
-            cs = cosf(a);
-            sn = sinf(a);
-        }
-        const float qs = LOG2E / sqrtf((float)HEAD_DIM);
-        for (int hr = wave; hr < N_HEAD + N_HEAD_KV; hr += 4) {
-            const bool is_q = hr < N_HEAD;
-            const float *src = is_q ? row + hr * HEAD_DIM : row + Q_DIM + (hr - N_HEAD) * HEAD_DIM;
-            const float *w = is_q ? P.q_norm : P.k_norm;
-            float x0 = src[lane], x1 = src[lane + 64];
-            double ss = (double)x0 * x0 + (double)x1 * x1;
-#pragma unroll
-            for (int o = 1; o < 64; o <<= 1) ss += __shfl_xor(ss, o, 64);
-            const float scale = 1.0f / sqrtf((float)(ss / HEAD_DIM) + P.rms_eps);
-            x0 = x0 * scale * w[lane];
-            x1 = x1 * scale * w[lane + 64];
-            if (P.has_rope) {
-                const float y0 = x0 * cs - x1 * sn, y1 = x0 * sn + x1 * cs;
-                x0 = y0;
-                x1 = y1;
-            }
-            if (is_q) {
-                _Float16 *qd = P.qh + ((size_t)hr * P.T + t) * HEAD_DIM;
-                qd[lane] = (_Float16)(x0 * qs);
-                qd[lane + 64] = (_Float16)(x1 * qs);
-            } else {
-                const int kvh = hr - N_HEAD;
-                const uint16_t k0 = KT::from_float(x0), k1 = KT::from_float(x1);
-                P.kd[kt_index(kvh, pos - P.kbase, lane, P.k_rows)] = k0;
-                P.kd[kt_index(kvh, pos - P.kbase, lane + 64, P.k_rows)] = k1;
-                if (P.ring_k && pos >= P.ring_from) {
-                    const int slot = pos & (P.ring_slots - 1);
-                    P.ring_k[kt_index(kvh, slot, lane, P.ring_slots)] = k0;
-                    P.ring_k[kt_index(kvh, slot, lane + 64, P.ring_slots)] = k1;
-                }
-            }
-        }
-        return;
-    }
-    // V tile: tokens t0..t0+63 of kv head kvh, transposed into [dim][row]
-    __shared__ uint16_t tile[64][HEAD_DIM + 2];
-    {
-        const int vb = b - P.T, kvh = vb & 3, t0 = (vb >> 2) * 64;
-        const int nt = min(64, P.T - t0);
-        for (int i = threadIdx.x; i < 64 * HEAD_DIM; i += 256) {
-            const int tt = i >> 7, d = i & 127;
-            if (tt < nt)
-                tile[tt][d] = KT::from_float(P.qkv[(size_t)(t0 + tt) * P.q_stride + Q_DIM + KV_DIM + kvh * HEAD_DIM + d]);
-        }
-        __syncthreads();
-        for (int i = threadIdx.x; i < 64 * HEAD_DIM; i += 256) {
-            const int d = i >> 6, tt = i & 63;
-            if (tt >= nt) continue;
-            const int pos = P.p0 + t0 + tt;
-            const uint16_t v = tile[tt][d];
-            P.vd[vt_index(kvh, pos - P.kbase, d, P.k_rows)] = v;
-            if (P.ring_v && pos >= P.ring_from)
-                P.ring_v[vt_index(kvh, pos & (P.ring_slots - 1), d, P.ring_slots)] = v;
-        }
-        return;
+__global__ __launch_bounds__(256) void prefix_kernel(const PrefillParams P) {
+    const int kvh = blockIdx.y, c0 = blockIdx.x * 64;
+    const int n_pre = P.p0 - P.kbase, nc = min(64, n_pre - c0);
+    for (int i = threadIdx.x; i < 64 * HEAD_DIM; i += 256) {
+        const int r = i >> 7, d = i & 127;
+        if (r >= nc) break;
+        const int pos = P.kbase + c0 + r, slot = pos & P.cache_mask, row = pos - P.kbase;
+        P.sk[pk_index(kvh, row, d, P.k_rows)] = to_f16<DT>(P.cache_k[kt_index(kvh, slot, d, P.n_slots)]);
+        P.sk[pv_index(kvh, row, d, P.k_rows)] = to_f16<DT>(P.cache_v[vt_index(kvh, slot, d, P.n_slots)]);
     }
 }
 
-// SWA ring prefix -> scratch key buffer: positions kbase + c0 .. +63 (< p0) of
-// kv head kvh. Runs before qk_prep on the same stream: when T > n_slots - 512
-// the new positions' ring writes reuse the slots read here.
-__global__ __launch_bounds__(256) void ring_prefix_kernel(const PrefillParams P) {
-    const int cb = blockIdx.x, kvh = cb & 3, c0 = (cb >> 2) * 64;
-    const int n_pre = P.p0 - P.kbase, nc = min(64, n_pre - c0);
-    const int mask = P.ring_slots - 1;
-    for (int i = threadIdx.x; i < 64 * 16; i += 256) {  // K rows, 16-byte units
-        const int r = i >> 4, u = i & 15;
-        if (r >= nc) continue;
-        const int pos = P.kbase + c0 + r;
-        const u16x8 v = *(const u16x8 *)(P.ring_k + kt_index(kvh, pos & mask, 8 * u, P.ring_slots));
-        *(u16x8 *)(P.kd + kt_index(kvh, pos - P.kbase, 8 * u, P.k_rows)) = v;
-    }
-    for (int i = threadIdx.x; i < 64 * HEAD_DIM; i += 256) {  // V^T columns
-        const int d = i >> 6, r = i & 63;
-        if (r >= nc) continue;
-        const int pos = P.kbase + c0 + r;
-        P.vd[vt_index(kvh, pos - P.kbase, d, P.k_rows)] = P.ring_v[vt_index(kvh, pos & mask, d, P.ring_slots)];
+// ---------------------------------------------------------------------------
+// kv_prep: the new tokens' K and V. grid (chunks of 64 tokens, kv head), 256 threads;
+// each wave handles every 4th token, lane = a NEOX pair of dims (lane, lane + 64).
+template <int DT>
+__global__ __launch_bounds__(256) void kv_prep_kernel(const PrefillParams P) {
+    typedef KvType<DT> KT;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int kvh = blockIdx.y, t0 = blockIdx.x * 64, nt = min(64, P.T - t0);
+    const float rf = P.rope_freq[lane];
+    const float2 kw = make_float2(P.k_norm[lane], P.k_norm[lane + 64]);
+    for (int tt = wave; tt < nt; tt += 4) {
+        const int t = t0 + tt, pos = P.p0 + t, row = pos - P.kbase;
+        const float *kr = P.qkv + (size_t)t * P.q_stride + Q_DIM + kvh * HEAD_DIM;
+        const float *vr = kr + KV_DIM;
+        float cs = 1.f, sn = 0.f;
+        if (P.has_rope) rope_sincos((float)pos * rf, &sn, &cs);
+        const float2 k2 = norm_rope_pair(make_float2(kr[lane], kr[lane + 64]), kw, P.rms_eps, P.has_rope, cs, sn);
+        const uint16_t k0 = KT::from_float(k2.x), k1 = KT::from_float(k2.y);
+        const uint16_t v0 = KT::from_float(vr[lane]), v1 = KT::from_float(vr[lane + 64]);
+        P.sk[pk_index(kvh, row, lane, P.k_rows)] = (_Float16)KT::to_float(k0);
+        P.sk[pk_index(kvh, row, lane + 64, P.k_rows)] = (_Float16)KT::to_float(k1);
+        P.sk[pv_index(kvh, row, lane, P.k_rows)] = (_Float16)KT::to_float(v0);
+        P.sk[pv_index(kvh, row, lane + 64, P.k_rows)] = (_Float16)KT::to_float(v1);
+        if (pos >= P.cache_from) {
+            const int slot = pos & P.cache_mask;
+            P.cache_k[kt_index(kvh, slot, lane, P.n_slots)] = k0;
+            P.cache_k[kt_index(kvh, slot, lane + 64, P.n_slots)] = k1;
+            P.cache_v[vt_index(kvh, slot, lane, P.n_slots)] = v0;
+            P.cache_v[vt_index(kvh, slot, lane + 64, P.n_slots)] = v1;
+        }
     }
 }
 
 // ---------------------------------------------------------------------------
 // flash attention
-constexpr int PF_BQ = 32;  // query positions per workgroup
-constexpr int PF_BK = 32;  // keys per tile
+constexpr int PF_WAVES = 8;                  // one q head of the GQA group per wave
+constexpr int PF_THREADS = PF_WAVES * 64;
+constexpr int PF_STAGE_UNITS = 2 * 16 * 64;  // 16-byte units per 64-key stage (two tiles)
+constexpr int PF_UNITS_PER_THREAD = PF_STAGE_UNITS / PF_THREADS;
 
-// S^T row i (MFMA A row) holds key sigma(i): bits 2 and 3 of i swapped, so that
-// a lane's 16 score rows are, per 16-key half, 8 consecutive keys (the P^T
-// operand of the P*V MFMA then needs no data movement).
-__device__ inline int pf_sigma(int i) { return (i & 0x13) | ((i & 4) << 1) | ((i & 8) >> 1); }
+// One 64-key stage of the attention copy (two 16 KiB tiles) as 16-byte units, 4 per
+// thread: units tid + 512 i, read contiguously.
+struct PfStage {
+    u32x4 u[PF_UNITS_PER_THREAD];
+};
+__device__ inline void pf_gload(PfStage &R, const _Float16 *__restrict__ src, int tid) {
+#pragma unroll
+    for (int i = 0; i < PF_UNITS_PER_THREAD; i++) R.u[i] = *(const u32x4 *)(src + 8 * (tid + PF_THREADS * i));
+}
+__device__ inline void pf_lstore(const PfStage &R, f16x8 (*dst)[16][64], int tid) {
+#pragma unroll
+    for (int i = 0; i < PF_UNITS_PER_THREAD; i++) {
+        const int u = tid + PF_THREADS * i;
+        dst[u >> 10][(u >> 6) & 15][u & 63] = __builtin_bit_cast(f16x8, R.u[i]);
+    }
+}
 
-template <int DT>
-__global__ __launch_bounds__(256) void flash_prefill_kernel(const PrefillParams P, int n_qblocks) {
-    // LDS tiles of 16-byte units (8 f16): K as [dim group][key], V^T as [key group][dim]
-    __shared__ f16x8 ks[16][PF_BK];
-    __shared__ f16x8 vs[PF_BK / 8][HEAD_DIM];
+// Workgroup: 32 query positions x the 8 q heads of kv head kvh, wave w = head 8 kvh + w.
+// Two waves per SIMD (about 170 registers each), so one wave's softmax overlaps the
+// other's MFMAs.
+__global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const PrefillParams P, int n_qblocks) {
+    // LDS: two stages (double buffer) of two tiles in the attention-copy order
+    __shared__ f16x8 stage[2][2][16][64];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int col = lane & 31, hh = lane >> 5;
-    const int kvh = blockIdx.x & 3;
+    const int kvh = blockIdx.x & 3, hq = kvh * GQA + wave;
     const int qb = n_qblocks - 1 - (int)(blockIdx.x >> 2);  // longest (causal) blocks first
     const int t0 = qb * PF_BQ;
     const int q_first = P.p0 + t0, q_last = P.p0 + min(t0 + PF_BQ, P.T) - 1;
     const int my_t = t0 + col, my_qp = P.p0 + my_t;
     const bool row_ok = my_t < P.T;
 
-    // Q fragments (B operand of S^T = K Q^T): column = query row, k = dims 16s + 8hh + e
-    f16x8 qf[2][8];
-#pragma unroll
-    for (int qt = 0; qt < 2; qt++) {
-        const int hq = kvh * GQA + 2 * wave + qt;
-        const _Float16 *qp = P.qh + ((size_t)hq * P.T + (row_ok ? my_t : 0)) * HEAD_DIM + 8 * hh;
+    const int k_lo = P.is_swa ? max(P.kbase, q_first - (P.window - 1)) : 0;
+    const int st_lo = (k_lo - P.kbase) / PF_BK, st_hi = (q_last - P.kbase) / PF_BK;  // stages
+    const _Float16 *__restrict__ skv = P.sk + (size_t)kvh * (P.k_rows >> 5) * (16 * 64 * 8);
+
+    // first stage in flight while Q is prepared
+    PfStage R;
+    pf_gload(R, skv + (size_t)st_lo * (PF_STAGE_UNITS * 8), tid);
+
+    // ---- Q fragments (B operand of S^T = K Q^T): column = query row `col`, k = dims
+    //      16s + 8hh + e. RMSNorm over the row (this lane's 64 dims + lane ^ 32's), NEOX
+    //      RoPE on the pairs (i, i + 64) = chunks (s, s + 4), scale log2(e)/sqrt(128), f16
+    //      (the reference's half Q block, prefill.metal:158-161) ----
+    f16x8 qf[8];
+    {
+        const float *qp = P.qkv + (size_t)(row_ok ? my_t : 0) * P.q_stride + hq * HEAD_DIM + 8 * hh;
+        float ss = 0.f;
 #pragma unroll
         for (int s = 0; s < 8; s++) {
-            f16x8 v = *(const f16x8 *)(qp + 16 * s);
-            qf[qt][s] = row_ok ? v : f16x8{};
+            const float4 a = *(const float4 *)(qp + 16 * s), b = *(const float4 *)(qp + 16 * s + 4);
+            ss += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w + b.x * b.x + b.y * b.y + b.z * b.z + b.w * b.w;
+        }
+        ss = xor32_sum(ss);  // the row's other 64 dims are in lane ^ 32
+        const float scale = 1.0f / sqrtf(ss / HEAD_DIM + P.rms_eps);
+        const float qs = LOG2E / sqrtf((float)HEAD_DIM);
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            float x0[8], x1[8], w0[8], w1[8];
+            *(float4 *)&x0[0] = *(const float4 *)(qp + 16 * s);
+            *(float4 *)&x0[4] = *(const float4 *)(qp + 16 * s + 4);
+            *(float4 *)&x1[0] = *(const float4 *)(qp + 16 * s + 64);
+            *(float4 *)&x1[4] = *(const float4 *)(qp + 16 * s + 68);
+            *(float4 *)&w0[0] = *(const float4 *)(P.q_norm + 16 * s + 8 * hh);
+            *(float4 *)&w0[4] = *(const float4 *)(P.q_norm + 16 * s + 8 * hh + 4);
+            *(float4 *)&w1[0] = *(const float4 *)(P.q_norm + 16 * s + 64 + 8 * hh);
+            *(float4 *)&w1[4] = *(const float4 *)(P.q_norm + 16 * s + 64 + 8 * hh + 4);
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                float cs = 1.f, sn = 0.f;
+                if (P.has_rope) rope_sincos_fast((float)my_qp * P.rope_freq[16 * s + 8 * hh + e], &sn, &cs);
+                const float a = x0[e] * scale * w0[e], b = x1[e] * scale * w1[e];
+                qf[s][e] = row_ok ? (_Float16)((a * cs - b * sn) * qs) : (_Float16)0;
+                qf[s + 4][e] = row_ok ? (_Float16)((a * sn + b * cs) * qs) : (_Float16)0;
+            }
         }
     }
-    float m[2], l[2];
-    f32x16 acc[2][4];
-#pragma unroll
-    for (int qt = 0; qt < 2; qt++) {
-        m[qt] = P.sinks[kvh * GQA + 2 * wave + qt] * LOG2E;
-        l[qt] = hh == 0 ? 1.f : 0.f;
-#pragma unroll
-        for (int dt = 0; dt < 4; dt++) acc[qt][dt] = f32x16{};
-    }
 
-    const int k_lo = P.is_swa ? max(P.kbase, q_first - (P.window - 1)) : 0;
-    const int tile_lo = (k_lo - P.kbase) / PF_BK, tile_hi = (q_last - P.kbase) / PF_BK;
-    const int n_valid = P.p0 + P.T - P.kbase;  // rows holding keys
-    const int sig = pf_sigma(col);
+    float m = P.sinks[hq] * LOG2E, l = hh == 0 ? 1.f : 0.f;
+    f32x16 acc[4];
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++) acc[dt] = f32x16{};
     // this lane's query row attends to key positions [key_lo, key_hi] (causal, SWA window);
     // rows past T attend to nothing
     const int key_hi = row_ok ? my_qp : -1;
     const int key_lo = P.is_swa ? max(my_qp - (P.window - 1), 0) : 0;
 
-    for (int kt = tile_lo; kt <= tile_hi; kt++) {
-        const int r0 = kt * PF_BK;  // first row of the tile
-        __syncthreads();
-        // stage K (32 rows x 16 units) and V^T (128 dims x 4 units); rows >= n_valid are zero
-#pragma unroll
-        for (int i = 0; i < 2; i++) {
-            const int u = tid + 256 * i;
-            {
-                // 16-byte unit u of the tiled K block (contiguous read): key and dim group
-                // from the tile order (kt_index)
-                const int st = (u >> 8) & 1, c = (u >> 6) & 3, g = (u >> 4) & 3, n = u & 15;
-                const int key = 8 * (n >> 2) + 4 * st + (n & 3), dg = 4 * c + g;
-                f16x8 v = {};
-                if (r0 + key < n_valid) {
-                    const u16x8 raw = *(const u16x8 *)(P.kd + kt_index(kvh, r0, 0, P.k_rows) + 8 * u);
-#pragma unroll
-                    for (int e = 0; e < 8; e++) v[e] = to_f16<DT>(raw[e]);
-                }
-                ks[dg][key] = v;
-            }
-            {
-                const int d = u & 127, kg = u >> 7;
-                f16x8 v = {};
-                const int rr = r0 + 8 * kg;
-                if (rr < n_valid) {
-                    const u16x8 raw = *(const u16x8 *)(P.vd + vt_index(kvh, rr, d, P.k_rows));
-#pragma unroll
-                    for (int e = 0; e < 8; e++) v[e] = rr + e < n_valid ? to_f16<DT>(raw[e]) : (_Float16)0;
-                }
-                vs[kg][d] = v;
-            }
-        }
-        __syncthreads();
+    pf_lstore(R, stage[0], tid);
+    if (st_lo + 1 <= st_hi) pf_gload(R, skv + (size_t)(st_lo + 1) * (PF_STAGE_UNITS * 8), tid);
+    __syncthreads();
 
-        const int kp0 = P.kbase + r0;  // key position of row 0
-        // wave-uniform: does any row of this block need masking in this tile?
-        const bool need_mask = kp0 + PF_BK - 1 > q_first || (P.is_swa && q_last - kp0 >= P.window) ||
-                               t0 + PF_BQ > P.T;
+    for (int sk = st_lo; sk <= st_hi; sk++) {
+        const int buf = (sk - st_lo) & 1;
 #pragma unroll
-        for (int qt = 0; qt < 2; qt++) {
+        for (int h = 0; h < 2; h++) {  // two 32-key MFMA tiles per stage
+            const int kp0 = P.kbase + sk * PF_BK + 32 * h;  // key position of the tile's first key
+            if (kp0 > q_last) break;   // wave-uniform: past the block's last query
+            // all 16 operand fragments of the tile requested at once: the K ones feed the
+            // score MFMAs back to back, the V ones land during the softmax
+            f16x8 kf[8], vf[8];
+#pragma unroll
+            for (int st = 0; st < 8; st++) kf[st] = stage[buf][h][st][lane];
+#pragma unroll
+            for (int i = 0; i < 8; i++) vf[i] = stage[buf][h][8 + i][lane];
+            __builtin_amdgcn_sched_barrier(0);
             f32x16 s = {};
 #pragma unroll
-            for (int st = 0; st < 8; st++) s = mfma32_f16(ks[2 * st + hh][sig], qf[qt][st], s);
-            // lane holds query row `col`, keys kp0 + 16(j>>1) + 8hh + 4(j&1) + r for element 4j + r
-            if (need_mask) {
+            for (int st = 0; st < 8; st++) s = mfma32_f16(kf[st], qf[st], s);
+            // wave-uniform: does any row of this block need masking in this tile?
+            if (kp0 + 31 > q_first || (P.is_swa && q_last - kp0 >= P.window) || t0 + PF_BQ > P.T) {
+                // lane holds query row `col`, keys kp0 + 16(j>>1) + 8hh + 4(j&1) + r for element 4j + r
 #pragma unroll
                 for (int e = 0; e < 16; e++) {
                     const int j = e >> 2, r = e & 3;
@@ -237,63 +236,65 @@ __global__ __launch_bounds__(256) void flash_prefill_kernel(const PrefillParams 
                     s[e] = ok ? s[e] : -INFINITY;
                 }
             }
-            float mt = s[0];
+            float mt = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
+            mt = fmaxf(mt, fmaxf(fmaxf(fmaxf(s[8], s[9]), fmaxf(s[10], s[11])), fmaxf(fmaxf(s[12], s[13]), fmaxf(s[14], s[15]))));
+            mt = xor32_max(mt);
+            if (__builtin_amdgcn_ballot_w64(mt > m + PF_RESCALE_LOG2) != 0) {  // wave-uniform, rare
+                const float m_new = fmaxf(m, mt);
+                const float corr = __builtin_amdgcn_exp2f(m - m_new);
+                m = m_new;
+                l *= corr;
 #pragma unroll
-            for (int e = 1; e < 16; e++) mt = fmaxf(mt, s[e]);
-            mt = wave_max_xor(mt, 32);
-            const float m_new = fmaxf(m[qt], mt);
-            const float corr = exp2f(m[qt] - m_new);
-            m[qt] = m_new;
+                for (int dt = 0; dt < 4; dt++) acc[dt] *= corr;
+            }
             float psum = 0.f;
             f16x8 pf[2];
 #pragma unroll
             for (int e = 0; e < 16; e++) {
-                const float p = exp2f(s[e] - m_new);
+                const float p = __builtin_amdgcn_exp2f(s[e] - m);
                 psum += p;
                 pf[e >> 3][e & 7] = (_Float16)p;
             }
-            l[qt] = l[qt] * corr + psum;
+            l += psum;
 #pragma unroll
-            for (int dt = 0; dt < 4; dt++) {
-                acc[qt][dt] *= corr;
+            for (int dt = 0; dt < 4; dt++)
 #pragma unroll
                 for (int kk = 0; kk < 2; kk++)
-                    acc[qt][dt] = mfma32_f16(vs[2 * kk + hh][32 * dt + col], pf[kk], acc[qt][dt]);
-            }
+                    acc[dt] = mfma32_f16(vf[2 * dt + kk], pf[kk], acc[dt]);
         }
+        if (sk + 1 <= st_hi) {
+            // stage sk + 1 into the other buffer (read by no wave since the last barrier)
+            // and request stage sk + 2
+            pf_lstore(R, stage[buf ^ 1], tid);
+            if (sk + 2 <= st_hi) pf_gload(R, skv + (size_t)(sk + 2) * (PF_STAGE_UNITS * 8), tid);
+        }
+        __syncthreads();
     }
 
     if (!row_ok) return;
+    const float inv = 1.0f / xor32_sum(l);
+    float *o = P.att + (size_t)my_t * Q_DIM + hq * HEAD_DIM;
 #pragma unroll
-    for (int qt = 0; qt < 2; qt++) {
-        const float lt = l[qt] + __shfl_xor(l[qt], 32, 64);
-        const float inv = 1.0f / lt;
-        const int hq = kvh * GQA + 2 * wave + qt;
-        float *o = P.att + (size_t)my_t * Q_DIM + hq * HEAD_DIM;
+    for (int dt = 0; dt < 4; dt++)
 #pragma unroll
-        for (int dt = 0; dt < 4; dt++)
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                float4 v = {acc[qt][dt][4 * j] * inv, acc[qt][dt][4 * j + 1] * inv, acc[qt][dt][4 * j + 2] * inv,
-                            acc[qt][dt][4 * j + 3] * inv};
-                *(float4 *)(o + 32 * dt + 8 * j + 4 * hh) = v;
-            }
-    }
+        for (int j = 0; j < 4; j++) {
+            float4 v = {acc[dt][4 * j] * inv, acc[dt][4 * j + 1] * inv, acc[dt][4 * j + 2] * inv, acc[dt][4 * j + 3] * inv};
+            *(float4 *)(o + 32 * dt + 8 * j + 4 * hh) = v;
+        }
 }
 
 hipError_t launch_prefill(const PrefillParams &P, int dtype, hipStream_t stream) {
-    const int nv = ((P.T + 63) / 64) * N_HEAD_KV;
     const int n_pre = P.p0 - P.kbase;
-    const int np = (P.ring_k && n_pre > 0 && P.kd != P.ring_k) ? ((n_pre + 63) / 64) * N_HEAD_KV : 0;
     const int nqb = (P.T + PF_BQ - 1) / PF_BQ;
-    if (np > 0) hipLaunchKernelGGL(ring_prefix_kernel, dim3(np), dim3(256), 0, stream, P);
+    const dim3 gp((n_pre + 63) / 64, N_HEAD_KV), gk((P.T + 63) / 64, N_HEAD_KV);
     if (dtype == DT_F16) {
-        hipLaunchKernelGGL(qk_prep_kernel<DT_F16>, dim3(P.T + nv), dim3(256), 0, stream, P, nv);
-        hipLaunchKernelGGL(flash_prefill_kernel<DT_F16>, dim3(nqb * N_HEAD_KV), dim3(256), 0, stream, P, nqb);
+        if (n_pre > 0) hipLaunchKernelGGL(prefix_kernel<DT_F16>, gp, dim3(256), 0, stream, P);
+        hipLaunchKernelGGL(kv_prep_kernel<DT_F16>, gk, dim3(256), 0, stream, P);
     } else {
-        hipLaunchKernelGGL(qk_prep_kernel<DT_BF16>, dim3(P.T + nv), dim3(256), 0, stream, P, nv);
-        hipLaunchKernelGGL(flash_prefill_kernel<DT_BF16>, dim3(nqb * N_HEAD_KV), dim3(256), 0, stream, P, nqb);
+        if (n_pre > 0) hipLaunchKernelGGL(prefix_kernel<DT_BF16>, gp, dim3(256), 0, stream, P);
+        hipLaunchKernelGGL(kv_prep_kernel<DT_BF16>, gk, dim3(256), 0, stream, P);
     }
+    hipLaunchKernelGGL(flash_prefill_kernel, dim3(nqb * N_HEAD_KV), dim3(PF_THREADS), 0, stream, P, nqb);
     return hipGetLastError();
 }
 

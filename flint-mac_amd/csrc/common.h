@@ -152,4 +152,38 @@ __device__ inline float wave_max(float x) {
     return xor32_max(xor16_max(x));
 }
 
+// sin/cos of a RoPE angle (a float, as the reference computes it): the angle
+// reaches ~6.5e4 rad at long context, so it is first reduced modulo 2*pi in
+// double precision (error ~1e-11 rad) to keep sincosf on its short path.
+__device__ inline void rope_sincos(float a, float *sn, float *cs) {
+    const double twopi = 6.283185307179586476925286766559;
+    const double r = (double)a - twopi * rint((double)a * (1.0 / twopi));
+    sincosf((float)r, sn, cs);
+}
+
+// RMSNorm (+ NEOX RoPE) of one 128-dim head row by one wave: lane holds dims
+// lane and lane + 64 (a NEOX pair, x) with their gains (w), cs/sn the rotation
+// of frequency `lane`.
+__device__ inline float2 norm_rope_pair(float2 x, float2 w, float eps, bool rope, float cs, float sn) {
+    const float ss = wave_sum(x.x * x.x + x.y * x.y);
+    const float scale = 1.0f / sqrtf(ss / HEAD_DIM + eps);
+    float x0 = x.x * scale * w.x, x1 = x.y * scale * w.y;
+    if (rope) {
+        const float y0 = x0 * cs - x1 * sn, y1 = x0 * sn + x1 * cs;
+        x0 = y0;
+        x1 = y1;
+    }
+    return make_float2(x0, x1);
+}
+
+// The same angle's sin/cos on the hardware sine/cosine (v_sin_f32 / v_cos_f32, whose
+// argument is in turns) after the double-precision reduction: about 1e-6 absolute, for
+// operands that are rounded to f16 right after (prefill's q).
+__device__ inline void rope_sincos_fast(float a, float *sn, float *cs) {
+    const double turns = (double)a * 0.15915494309189533576888376337251;  // 1 / (2 pi)
+    const float r = (float)(turns - rint(turns));
+    *sn = __builtin_amdgcn_sinf(r);
+    *cs = __builtin_amdgcn_cosf(r);
+}
+
 }  // namespace flint

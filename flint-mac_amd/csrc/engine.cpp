@@ -60,19 +60,20 @@ void rope_freqs(float theta, float *freq) {
 struct Workspace {
     void *ptr = nullptr;
     size_t bytes = 0;
-    void *get(size_t need) {
+    void *get(size_t need, bool zero = false) {
         if (need <= bytes) return ptr;
         if (ptr) check(hipFree(ptr), "hipFree");
         ptr = nullptr;
         bytes = 0;
         check(hipMalloc(&ptr, need), "hipMalloc workspace");
+        if (zero) check(hipMemset(ptr, 0, need), "hipMemset workspace");
         bytes = need;
         return ptr;
     }
 };
 
 struct DeviceScratch {
-    Workspace partial, qh, kv;
+    Workspace partial, kv;
 };
 
 std::mutex g_scratch_mu;
@@ -204,27 +205,22 @@ void prefill_impl(const flint_attn_layer *L, const float *qkv, int q_stride, int
     P.window = L->window;
     rope_freqs_cached(L->rope_theta, P.rope_freq);
     P.att = att;
-    DeviceScratch &ws = scratch();
-    P.qh = (_Float16 *)ws.qh.get((size_t)N_HEAD * T * HEAD_DIM * sizeof(_Float16));
+    P.cache_k = (uint16_t *)L->k_cache;
+    P.cache_v = (uint16_t *)L->v_cache;
+    P.n_slots = L->n_slots;
     if (L->is_swa) {
+        P.cache_mask = L->n_slots - 1;
+        P.cache_from = std::max(p0, p0 + T - L->n_slots);  // the ring keeps the last n_slots
         P.kbase = std::max(0, p0 - (L->window - 1));
-        P.k_rows = ((p0 + T - P.kbase) + 31) / 32 * 32;
-        uint16_t *kv = (uint16_t *)ws.kv.get((size_t)2 * N_HEAD_KV * P.k_rows * HEAD_DIM * sizeof(uint16_t));
-        P.kd = kv;
-        P.vd = kv + (size_t)N_HEAD_KV * P.k_rows * HEAD_DIM;
-        P.ring_k = (uint16_t *)L->k_cache;
-        P.ring_v = (uint16_t *)L->v_cache;
-        P.ring_slots = L->n_slots;
-        P.ring_from = std::max(p0, p0 + T - L->n_slots);
     } else {
+        P.cache_mask = -1;
+        P.cache_from = p0;
         P.kbase = 0;
-        P.k_rows = L->n_slots;
-        P.kd = (uint16_t *)L->k_cache;
-        P.vd = (uint16_t *)L->v_cache;
-        P.ring_k = P.ring_v = nullptr;
-        P.ring_slots = 0;
-        P.ring_from = 0;
     }
+    P.k_rows = ((p0 + T - P.kbase) + 63) / 64 * 64;
+    DeviceScratch &ws = scratch();
+    // zeroed when allocated: rows past the valid keys must hold finite values
+    P.sk = (_Float16 *)ws.kv.get((size_t)N_HEAD_KV * P.k_rows * 2 * HEAD_DIM * sizeof(_Float16), true);
     check(launch_prefill(P, L->kv_dtype, stream), "prefill launch");
 }
 

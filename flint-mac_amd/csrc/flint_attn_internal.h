@@ -34,8 +34,8 @@ struct DecodeParams {
 
 hipError_t launch_decode(const DecodeParams &P, int dtype, hipStream_t stream);
 
-// Prefill: q/k prep (k_qk_prefill, prefill.metal:99-133) + flash attention
-// (k_attn_prefill, prefill.metal:141-266).
+// Prefill: k/v prep (k_qk_prefill, prefill.metal:99-133) + flash attention with
+// the q prep fused (k_attn_prefill, prefill.metal:141-266).
 struct PrefillParams {
     const float *qkv;     // [T] rows of q_stride floats
     int q_stride;
@@ -44,16 +44,14 @@ struct PrefillParams {
     float rms_eps;
     int is_swa, has_rope, window;
     float rope_freq[64];
-    _Float16 *qh;         // [32][T][128] normed/roped q * log2(e)/sqrt(128), f16
-    // keys/values the attention reads: key position kp lives at row kp - kbase
-    uint16_t *kd;         // [4][k_rows/32][32*128] (kt_index layout)
-    uint16_t *vd;         // [4][k_rows/32][128][32]
-    int k_rows;           // row capacity per kv head (multiple of 32)
-    int kbase;
-    // SWA ring (cache) written for positions >= ring_from; copied into kd/vd for [kbase, p0)
-    uint16_t *ring_k;     // [4][n_slots/32][32*128] (kt_index layout) or null
-    uint16_t *ring_v;     // [4][n_slots/32][128][32]
-    int ring_slots, ring_from;
+    // the layer's cache (kt_index / vt_index layouts): position p lives in slot
+    // p & cache_mask; positions >= cache_from among the new ones are written to it
+    uint16_t *cache_k, *cache_v;
+    int n_slots, cache_mask, cache_from;
+    // attention copy (f16, pk_index / pv_index layouts) of key positions
+    // kbase .. p0 + T - 1 at rows 0 .., k_rows rows per kv head (multiple of 64)
+    _Float16 *sk;
+    int k_rows, kbase;
     float *att;           // [T][4096]
 };
 
