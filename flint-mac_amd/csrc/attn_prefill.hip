@@ -77,35 +77,36 @@ __global__ __launch_bounds__(256) void prefix_kernel(const PrefillParams P) {
 }
 
 // ---------------------------------------------------------------------------
-// kv_prep: the new tokens' K and V. grid (chunks of 64 tokens, kv head), 256 threads;
-// each wave handles every 4th token, lane = a NEOX pair of dims (lane, lane + 64).
+// kv_prep: the new tokens' K and V. grid (T / 4, kv head), 256 threads: one token per
+// wave (its loads are the only memory round trip on the wave's path), lane = a NEOX pair
+// of dims (lane, lane + 64).
 template <int DT>
 __global__ __launch_bounds__(256) void kv_prep_kernel(const PrefillParams P) {
     typedef KvType<DT> KT;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int kvh = blockIdx.y, t0 = blockIdx.x * 64, nt = min(64, P.T - t0);
-    const float rf = P.rope_freq[lane];
+    const int kvh = blockIdx.y, t = blockIdx.x * 4 + wave;
+    if (t >= P.T) return;
+    const int pos = P.p0 + t, row = pos - P.kbase;
+    const float *kr = P.qkv + (size_t)t * P.q_stride + Q_DIM + kvh * HEAD_DIM;
+    const float *vr = kr + KV_DIM;
+    const float2 kx = make_float2(kr[lane], kr[lane + 64]), vx = make_float2(vr[lane], vr[lane + 64]);
     const float2 kw = make_float2(P.k_norm[lane], P.k_norm[lane + 64]);
-    for (int tt = wave; tt < nt; tt += 4) {
-        const int t = t0 + tt, pos = P.p0 + t, row = pos - P.kbase;
-        const float *kr = P.qkv + (size_t)t * P.q_stride + Q_DIM + kvh * HEAD_DIM;
-        const float *vr = kr + KV_DIM;
-        float cs = 1.f, sn = 0.f;
-        if (P.has_rope) rope_sincos((float)pos * rf, &sn, &cs);
-        const float2 k2 = norm_rope_pair(make_float2(kr[lane], kr[lane + 64]), kw, P.rms_eps, P.has_rope, cs, sn);
-        const uint16_t k0 = KT::from_float(k2.x), k1 = KT::from_float(k2.y);
-        const uint16_t v0 = KT::from_float(vr[lane]), v1 = KT::from_float(vr[lane + 64]);
-        P.sk[pk_index(kvh, row, lane, P.k_rows)] = (_Float16)KT::to_float(k0);
-        P.sk[pk_index(kvh, row, lane + 64, P.k_rows)] = (_Float16)KT::to_float(k1);
-        P.sk[pv_index(kvh, row, lane, P.k_rows)] = (_Float16)KT::to_float(v0);
-        P.sk[pv_index(kvh, row, lane + 64, P.k_rows)] = (_Float16)KT::to_float(v1);
-        if (pos >= P.cache_from) {
-            const int slot = pos & P.cache_mask;
-            P.cache_k[kt_index(kvh, slot, lane, P.n_slots)] = k0;
-            P.cache_k[kt_index(kvh, slot, lane + 64, P.n_slots)] = k1;
-            P.cache_v[vt_index(kvh, slot, lane, P.n_slots)] = v0;
-            P.cache_v[vt_index(kvh, slot, lane + 64, P.n_slots)] = v1;
-        }
+    const float rf = P.rope_freq[lane];
+    float cs = 1.f, sn = 0.f;
+    if (P.has_rope) rope_sincos((float)pos * rf, &sn, &cs);
+    const float2 k2 = norm_rope_pair(kx, kw, P.rms_eps, P.has_rope, cs, sn);
+    const uint16_t k0 = KT::from_float(k2.x), k1 = KT::from_float(k2.y);
+    const uint16_t v0 = KT::from_float(vx.x), v1 = KT::from_float(vx.y);
+    P.sk[pk_index(kvh, row, lane, P.k_rows)] = (_Float16)KT::to_float(k0);
+    P.sk[pk_index(kvh, row, lane + 64, P.k_rows)] = (_Float16)KT::to_float(k1);
+    P.sk[pv_index(kvh, row, lane, P.k_rows)] = (_Float16)KT::to_float(v0);
+    P.sk[pv_index(kvh, row, lane + 64, P.k_rows)] = (_Float16)KT::to_float(v1);
+    if (pos >= P.cache_from) {
+        const int slot = pos & P.cache_mask;
+        P.cache_k[kt_index(kvh, slot, lane, P.n_slots)] = k0;
+        P.cache_k[kt_index(kvh, slot, lane + 64, P.n_slots)] = k1;
+        P.cache_v[vt_index(kvh, slot, lane, P.n_slots)] = v0;
+        P.cache_v[vt_index(kvh, slot, lane + 64, P.n_slots)] = v1;
     }
 }
 
@@ -196,6 +197,9 @@ __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const Pref
     }
 
     float m = P.sinks[hq] * LOG2E, l = hh == 0 ? 1.f : 0.f;
+    f32x16 negm;  // -m in every element: the C operand of each tile's first score MFMA
+#pragma unroll
+    for (int e = 0; e < 16; e++) negm[e] = -m;
     f32x16 acc[4];
 #pragma unroll
     for (int dt = 0; dt < 4; dt++) acc[dt] = f32x16{};
@@ -222,9 +226,10 @@ __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const Pref
 #pragma unroll
             for (int i = 0; i < 8; i++) vf[i] = stage[buf][h][8 + i][lane];
             __builtin_amdgcn_sched_barrier(0);
-            f32x16 s = {};
+            // scores relative to the running max: the first MFMA adds K Q^T to -m
+            f32x16 s = mfma32_f16(kf[0], qf[0], negm);
 #pragma unroll
-            for (int st = 0; st < 8; st++) s = mfma32_f16(kf[st], qf[st], s);
+            for (int st = 1; st < 8; st++) s = mfma32_f16(kf[st], qf[st], s);
             // wave-uniform: does any row of this block need masking in this tile?
             if (kp0 + 31 > q_first || (P.is_swa && q_last - kp0 >= P.window) || t0 + PF_BQ > P.T) {
                 // lane holds query row `col`, keys kp0 + 16(j>>1) + 8hh + 4(j&1) + r for element 4j + r
@@ -236,26 +241,30 @@ __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const Pref
                     s[e] = ok ? s[e] : -INFINITY;
                 }
             }
-            float mt = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
-            mt = fmaxf(mt, fmaxf(fmaxf(fmaxf(s[8], s[9]), fmaxf(s[10], s[11])), fmaxf(fmaxf(s[12], s[13]), fmaxf(s[14], s[15]))));
+            float mt = fmaxf(fmaxf(fmaxf(s[0], s[1]), s[2]), fmaxf(fmaxf(s[3], s[4]), s[5]));
+            mt = fmaxf(fmaxf(mt, fmaxf(s[6], s[7])), fmaxf(fmaxf(s[8], s[9]), s[10]));
+            mt = fmaxf(fmaxf(mt, fmaxf(s[11], s[12])), fmaxf(fmaxf(s[13], s[14]), s[15]));
             mt = xor32_max(mt);
-            if (__builtin_amdgcn_ballot_w64(mt > m + PF_RESCALE_LOG2) != 0) {  // wave-uniform, rare
-                const float m_new = fmaxf(m, mt);
-                const float corr = __builtin_amdgcn_exp2f(m - m_new);
-                m = m_new;
+            if (__builtin_amdgcn_ballot_w64(mt > PF_RESCALE_LOG2) != 0) {  // wave-uniform, rare
+                const float d = fmaxf(mt, 0.f);  // raise m by d
+                const float corr = __builtin_amdgcn_exp2f(-d);
+                m += d;
+#pragma unroll
+                for (int e = 0; e < 16; e++) negm[e] = -m;
                 l *= corr;
 #pragma unroll
                 for (int dt = 0; dt < 4; dt++) acc[dt] *= corr;
+#pragma unroll
+                for (int e = 0; e < 16; e++) s[e] -= d;
             }
-            float psum = 0.f;
+            // P in f16 (the MFMA operand); l sums the same rounded values
             f16x8 pf[2];
 #pragma unroll
-            for (int e = 0; e < 16; e++) {
-                const float p = __builtin_amdgcn_exp2f(s[e] - m);
-                psum += p;
-                pf[e >> 3][e & 7] = (_Float16)p;
-            }
-            l += psum;
+            for (int e = 0; e < 16; e++) pf[e >> 3][e & 7] = (_Float16)__builtin_amdgcn_exp2f(s[e]);
+            typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+            const h2 one2 = {(_Float16)1, (_Float16)1};
+#pragma unroll
+            for (int e = 0; e < 16; e += 2) l = __builtin_amdgcn_fdot2(h2{pf[e >> 3][e & 7], pf[e >> 3][(e & 7) + 1]}, one2, l, false);
 #pragma unroll
             for (int dt = 0; dt < 4; dt++)
 #pragma unroll
@@ -286,7 +295,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const Pref
 hipError_t launch_prefill(const PrefillParams &P, int dtype, hipStream_t stream) {
     const int n_pre = P.p0 - P.kbase;
     const int nqb = (P.T + PF_BQ - 1) / PF_BQ;
-    const dim3 gp((n_pre + 63) / 64, N_HEAD_KV), gk((P.T + 63) / 64, N_HEAD_KV);
+    const dim3 gp((n_pre + 63) / 64, N_HEAD_KV), gk((P.T + 3) / 4, N_HEAD_KV);
     if (dtype == DT_F16) {
         if (n_pre > 0) hipLaunchKernelGGL(prefix_kernel<DT_F16>, gp, dim3(256), 0, stream, P);
         hipLaunchKernelGGL(kv_prep_kernel<DT_F16>, gk, dim3(256), 0, stream, P);
