@@ -33,7 +33,8 @@
 namespace flint {
 
 constexpr int PF_BQ = 32;  // query positions per workgroup
-constexpr int PF_BK = 64;  // keys per LDS stage (two 32-key MFMA tiles)
+constexpr int PF_TILES = 2;              // 32-key MFMA tiles per LDS stage
+constexpr int PF_BK = 32 * PF_TILES;     // keys per LDS stage
 constexpr float PF_RESCALE_LOG2 = 8.f;  // lazy running-max margin (p stays below 2^8)
 
 // S^T row i (MFMA A row) holds key sigma(i) of its 32-key tile: bits 2 and 3 of i
@@ -77,36 +78,108 @@ __global__ __launch_bounds__(256) void prefix_kernel(const PrefillParams P) {
 }
 
 // ---------------------------------------------------------------------------
-// kv_prep: the new tokens' K and V. grid (T / 4, kv head), 256 threads: one token per
-// wave (its loads are the only memory round trip on the wave's path), lane = a NEOX pair
-// of dims (lane, lane + 64).
+// kv_prep: the new tokens' K and V. grid (32-position chunks, kv head), 256 threads.
+// Chunk c holds positions 32 c0 + 32 c .. +31 (32-aligned, so it is one tile of the
+// attention copy, whose kbase is 32-aligned, and one tile of the cache). Each wave
+// normalises (+ RoPE) 8 tokens' k (lane = a NEOX pair of dims) and rounds k and v to
+// the cache dtype into LDS; then every 16-byte unit of the four destination tiles is
+// written with one store. A V unit spans 8 positions: where some of them are not new
+// (or, for the ring, not kept) its elements are stored one by one, so no unit is
+// read back and no two workgroups write the same bytes.
 template <int DT>
 __global__ __launch_bounds__(256) void kv_prep_kernel(const PrefillParams P) {
     typedef KvType<DT> KT;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int kvh = blockIdx.y, t = blockIdx.x * 4 + wave;
-    if (t >= P.T) return;
-    const int pos = P.p0 + t, row = pos - P.kbase;
-    const float *kr = P.qkv + (size_t)t * P.q_stride + Q_DIM + kvh * HEAD_DIM;
-    const float *vr = kr + KV_DIM;
-    const float2 kx = make_float2(kr[lane], kr[lane + 64]), vx = make_float2(vr[lane], vr[lane + 64]);
+    __shared__ uint16_t kl[32][HEAD_DIM + 8], vl[32][HEAD_DIM + 8];  // rounded k and v
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, tid = threadIdx.x;
+    const int kvh = blockIdx.y;
+    const int c0 = (P.p0 >> 5) + blockIdx.x, pos0 = 32 * c0;  // first position of the chunk
+    const int lo = max(P.p0, pos0), hi = min(P.p0 + P.T, pos0 + 32);  // new positions [lo, hi)
     const float2 kw = make_float2(P.k_norm[lane], P.k_norm[lane + 64]);
     const float rf = P.rope_freq[lane];
-    float cs = 1.f, sn = 0.f;
-    if (P.has_rope) rope_sincos((float)pos * rf, &sn, &cs);
-    const float2 k2 = norm_rope_pair(kx, kw, P.rms_eps, P.has_rope, cs, sn);
-    const uint16_t k0 = KT::from_float(k2.x), k1 = KT::from_float(k2.y);
-    const uint16_t v0 = KT::from_float(vx.x), v1 = KT::from_float(vx.y);
-    P.sk[pk_index(kvh, row, lane, P.k_rows)] = (_Float16)KT::to_float(k0);
-    P.sk[pk_index(kvh, row, lane + 64, P.k_rows)] = (_Float16)KT::to_float(k1);
-    P.sk[pv_index(kvh, row, lane, P.k_rows)] = (_Float16)KT::to_float(v0);
-    P.sk[pv_index(kvh, row, lane + 64, P.k_rows)] = (_Float16)KT::to_float(v1);
-    if (pos >= P.cache_from) {
-        const int slot = pos & P.cache_mask;
-        P.cache_k[kt_index(kvh, slot, lane, P.n_slots)] = k0;
-        P.cache_k[kt_index(kvh, slot, lane + 64, P.n_slots)] = k1;
-        P.cache_v[vt_index(kvh, slot, lane, P.n_slots)] = v0;
-        P.cache_v[vt_index(kvh, slot, lane + 64, P.n_slots)] = v1;
+    // the wave's 8 tokens: all loads first (positions outside [lo, hi) read the chunk's
+    // first new token, in range, and are not stored), then the maths
+    float2 kx[8], vx[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int pos = pos0 + wave + 4 * i, t = (pos >= lo && pos < hi ? pos : lo) - P.p0;
+        const float *kr = P.qkv + (size_t)t * P.q_stride + Q_DIM + kvh * HEAD_DIM;
+        kx[i] = make_float2(kr[lane], kr[lane + 64]);
+        vx[i] = make_float2(kr[KV_DIM + lane], kr[KV_DIM + lane + 64]);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int r = wave + 4 * i, pos = pos0 + r;
+        float cs = 1.f, sn = 0.f;
+        if (P.has_rope) rope_sincos((float)pos * rf, &sn, &cs);
+        const float2 k2 = norm_rope_pair(kx[i], kw, P.rms_eps, P.has_rope, cs, sn);
+        kl[r][lane] = KT::from_float(k2.x);
+        kl[r][lane + 64] = KT::from_float(k2.y);
+        vl[r][lane] = KT::from_float(vx[i].x);
+        vl[r][lane + 64] = KT::from_float(vx[i].y);
+    }
+    __syncthreads();
+    const int row0 = pos0 - P.kbase;              // attention-copy row of the chunk's first position
+    const bool to_cache = hi > P.cache_from;       // some positions go to the cache
+    const int clo = max(lo, P.cache_from);         // cached positions [clo, hi)
+    const int ctile = (pos0 & P.cache_mask) >> 5;  // the cache tile (slot = pos & mask, 32-aligned)
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int u = tid + 256 * i;  // 16-byte unit of a 512-unit (8 KiB) tile
+        // K, attention copy: unit (st, hh, col) = key pf_sigma(col), dims 16 st + 8 hh .. +7
+        {
+            const int st = u >> 6, hh = (u >> 5) & 1, col = u & 31, r = pf_sigma(col);
+            if (pos0 + r >= lo && pos0 + r < hi) {
+                f16x8 v;
+#pragma unroll
+                for (int e = 0; e < 8; e++) v[e] = (_Float16)KT::to_float(kl[r][16 * st + 8 * hh + e]);
+                *(f16x8 *)(P.sk + pk_index(kvh, row0 + r, 16 * st + 8 * hh, P.k_rows)) = v;
+            }
+        }
+        // V, attention copy: unit (dt, kk, hh, d) = dim 32 dt + d, keys 16 kk + 8 hh .. +7
+        {
+            const int dt = u >> 7, kk = (u >> 6) & 1, hh = (u >> 5) & 1, d = 32 * dt + (u & 31);
+            const int r0 = 16 * kk + 8 * hh;
+            _Float16 *dst = P.sk + pv_index(kvh, row0 + r0, d, P.k_rows);
+            if (pos0 + r0 >= lo && pos0 + r0 + 8 <= hi) {
+                f16x8 v;
+#pragma unroll
+                for (int e = 0; e < 8; e++) v[e] = (_Float16)KT::to_float(vl[r0 + e][d]);
+                *(f16x8 *)dst = v;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; e++)
+                    if (pos0 + r0 + e >= lo && pos0 + r0 + e < hi) dst[e] = (_Float16)KT::to_float(vl[r0 + e][d]);
+            }
+        }
+        if (to_cache) {
+            // K, cache tile (kt_index order): unit (st, c, g, n) = key 8(n>>2) + 4st + (n&3),
+            // dims 32c + 8g .. +7
+            {
+                const int st = u >> 8, c = (u >> 6) & 3, g = (u >> 4) & 3, n = u & 15;
+                const int r = 8 * (n >> 2) + 4 * st + (n & 3), d = 32 * c + 8 * g;
+                if (pos0 + r >= clo && pos0 + r < hi) {
+                    u16x8 v;
+#pragma unroll
+                    for (int e = 0; e < 8; e++) v[e] = kl[r][d + e];
+                    *(u16x8 *)(P.cache_k + kt_index(kvh, 32 * ctile + r, d, P.n_slots)) = v;
+                }
+            }
+            // V, cache tile (vt_index order): unit (d, g) = dim d, slots 8g .. 8g+7 of the tile
+            {
+                const int d = u >> 2, r0 = 8 * (u & 3);
+                uint16_t *dst = P.cache_v + vt_index(kvh, 32 * ctile + r0, d, P.n_slots);
+                if (pos0 + r0 >= clo && pos0 + r0 + 8 <= hi) {
+                    u16x8 v;
+#pragma unroll
+                    for (int e = 0; e < 8; e++) v[e] = vl[r0 + e][d];
+                    *(u16x8 *)dst = v;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; e++)
+                        if (pos0 + r0 + e >= clo && pos0 + r0 + e < hi) dst[e] = vl[r0 + e][d];
+                }
+            }
+        }
     }
 }
 
@@ -114,11 +187,11 @@ __global__ __launch_bounds__(256) void kv_prep_kernel(const PrefillParams P) {
 // flash attention
 constexpr int PF_WAVES = 8;                  // one q head of the GQA group per wave
 constexpr int PF_THREADS = PF_WAVES * 64;
-constexpr int PF_STAGE_UNITS = 2 * 16 * 64;  // 16-byte units per 64-key stage (two tiles)
+constexpr int PF_STAGE_UNITS = PF_TILES * 16 * 64;  // 16-byte units per stage
 constexpr int PF_UNITS_PER_THREAD = PF_STAGE_UNITS / PF_THREADS;
 
-// One 64-key stage of the attention copy (two 16 KiB tiles) as 16-byte units, 4 per
-// thread: units tid + 512 i, read contiguously.
+// One stage of the attention copy (PF_TILES 16 KiB tiles) as 16-byte units, read
+// contiguously: units tid + 512 i.
 struct PfStage {
     u32x4 u[PF_UNITS_PER_THREAD];
 };
@@ -139,7 +212,7 @@ __device__ inline void pf_lstore(const PfStage &R, f16x8 (*dst)[16][64], int tid
 // other's MFMAs.
 __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const PrefillParams P, int n_qblocks) {
     // LDS: two stages (double buffer) of two tiles in the attention-copy order
-    __shared__ f16x8 stage[2][2][16][64];
+    __shared__ f16x8 stage[2][PF_TILES][16][64];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int col = lane & 31, hh = lane >> 5;
@@ -215,7 +288,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const Pref
     for (int sk = st_lo; sk <= st_hi; sk++) {
         const int buf = (sk - st_lo) & 1;
 #pragma unroll
-        for (int h = 0; h < 2; h++) {  // two 32-key MFMA tiles per stage
+        for (int h = 0; h < PF_TILES; h++) {  // the stage's 32-key MFMA tiles
             const int kp0 = P.kbase + sk * PF_BK + 32 * h;  // key position of the tile's first key
             if (kp0 > q_last) break;   // wave-uniform: past the block's last query
             // all 16 operand fragments of the tile requested at once: the K ones feed the
@@ -295,7 +368,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const Pref
 hipError_t launch_prefill(const PrefillParams &P, int dtype, hipStream_t stream) {
     const int n_pre = P.p0 - P.kbase;
     const int nqb = (P.T + PF_BQ - 1) / PF_BQ;
-    const dim3 gp((n_pre + 63) / 64, N_HEAD_KV), gk((P.T + 3) / 4, N_HEAD_KV);
+    const dim3 gp((n_pre + 63) / 64, N_HEAD_KV), gk(((P.p0 + P.T + 31) >> 5) - (P.p0 >> 5), N_HEAD_KV);
     if (dtype == DT_F16) {
         if (n_pre > 0) hipLaunchKernelGGL(prefix_kernel<DT_F16>, gp, dim3(256), 0, stream, P);
         hipLaunchKernelGGL(kv_prep_kernel<DT_F16>, gk, dim3(256), 0, stream, P);

@@ -211,13 +211,13 @@ void prefill_impl(const flint_attn_layer *L, const float *qkv, int q_stride, int
     if (L->is_swa) {
         P.cache_mask = L->n_slots - 1;
         P.cache_from = std::max(p0, p0 + T - L->n_slots);  // the ring keeps the last n_slots
-        P.kbase = std::max(0, p0 - (L->window - 1));
+        P.kbase = std::max(0, p0 - (L->window - 1)) & ~31;  // 32-aligned: chunks line up with tiles
     } else {
         P.cache_mask = -1;
         P.cache_from = p0;
         P.kbase = 0;
     }
-    P.k_rows = ((p0 + T - P.kbase) + 63) / 64 * 64;
+    P.k_rows = ((p0 + T - P.kbase) + PREFILL_ROW_ALIGN - 1) / PREFILL_ROW_ALIGN * PREFILL_ROW_ALIGN;
     DeviceScratch &ws = scratch();
     // zeroed when allocated: rows past the valid keys must hold finite values
     P.sk = (_Float16 *)ws.kv.get((size_t)N_HEAD_KV * P.k_rows * 2 * HEAD_DIM * sizeof(_Float16), true);

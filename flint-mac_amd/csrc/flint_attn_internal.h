@@ -8,6 +8,7 @@
 namespace flint {
 
 constexpr int MAX_SEQ = 64;  // sequences one batched decode launch can serve
+constexpr int PREFILL_ROW_ALIGN = 128;  // prefill attention-copy rows: a multiple of the LDS stage
 
 // Decode launch (fused.metal AttnDecArgs {pos, is_full, n_split, keys_per_split},
 // /root/reference/src/metal/fused_args.h:15-20, generalised to many sequences).
@@ -49,7 +50,7 @@ struct PrefillParams {
     uint16_t *cache_k, *cache_v;
     int n_slots, cache_mask, cache_from;
     // attention copy (f16, pk_index / pv_index layouts) of key positions
-    // kbase .. p0 + T - 1 at rows 0 .., k_rows rows per kv head (multiple of 64)
+    // kbase .. p0 + T - 1 at rows 0 .., k_rows rows per kv head (multiple of PREFILL_ROW_ALIGN)
     _Float16 *sk;
     int k_rows, kbase;
     float *att;           // [T][4096]
