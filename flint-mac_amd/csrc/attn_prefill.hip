@@ -213,6 +213,8 @@ __device__ inline void pf_lstore(const PfStage &R, f16x8 (*dst)[16][64], int tid
 __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const PrefillParams P, int n_qblocks) {
     // LDS: two stages (double buffer) of two tiles in the attention-copy order
     __shared__ f16x8 stage[2][PF_TILES][16][64];
+    // LDS: 8 KiB per wave that hands q over to the operand order, and later the output
+    __shared__ f16x8 q_lds[PF_WAVES][8][64];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int col = lane & 31, hh = lane >> 5;
@@ -227,46 +229,70 @@ __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const Pref
     const int st_lo = (k_lo - P.kbase) / PF_BK, st_hi = (q_last - P.kbase) / PF_BK;  // stages
     const _Float16 *__restrict__ skv = P.sk + (size_t)kvh * (P.k_rows >> 5) * (16 * 64 * 8);
 
-    // first stage in flight while Q is prepared
+    // ---- Q fragments (B operand of S^T = K Q^T): lane (col, hh) needs query row `col`,
+    //      dims 16s + 8hh + e, in f16, after RMSNorm, NEOX RoPE and the scale
+    //      log2(e)/sqrt(128) (the reference's half Q block, prefill.metal:158-161).
+    //      Loaded row-coalesced instead: lane (rr, q8) = (lane >> 3, lane & 7) reads rows
+    //      rr + 8g, dims 32k + 4q8 .. +3, so 8 lanes read one 128-byte line and an
+    //      instruction 1 KiB; a row's sum of squares is an 8-lane sum and each NEOX pair
+    //      (k, k + 2) sits in one lane. The f16 values go through this wave's LDS area
+    //      into the operand order. ----
+    // Loads in the order they are waited for (waits count loads in issue order): the
+    // norm gains and this lane's 8 RoPE frequencies (32k + 4q8 + j, k < 2), which every
+    // q value needs, then the q rows, then the first stage, needed only after q.
+    const int q8 = lane & 7, rr = lane >> 3;
+    float4 w[4], rf[2], x[4][4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) w[k] = *(const float4 *)(P.q_norm + 32 * k + 4 * q8);
+#pragma unroll
+    for (int k = 0; k < 2; k++) rf[k] = *(const float4 *)&P.rope_freq[32 * k + 4 * q8];
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+        const int t = t0 + rr + 8 * g;
+        const float *qp = P.qkv + (size_t)(t < P.T ? t : 0) * P.q_stride + hq * HEAD_DIM + 4 * q8;
+#pragma unroll
+        for (int k = 0; k < 4; k++) x[g][k] = *(const float4 *)(qp + 32 * k);
+    }
     PfStage R;
     pf_gload(R, skv + (size_t)st_lo * (PF_STAGE_UNITS * 8), tid);
 
-    // ---- Q fragments (B operand of S^T = K Q^T): column = query row `col`, k = dims
-    //      16s + 8hh + e. RMSNorm over the row (this lane's 64 dims + lane ^ 32's), NEOX
-    //      RoPE on the pairs (i, i + 64) = chunks (s, s + 4), scale log2(e)/sqrt(128), f16
-    //      (the reference's half Q block, prefill.metal:158-161) ----
     f16x8 qf[8];
     {
-        const float *qp = P.qkv + (size_t)(row_ok ? my_t : 0) * P.q_stride + hq * HEAD_DIM + 8 * hh;
-        float ss = 0.f;
-#pragma unroll
-        for (int s = 0; s < 8; s++) {
-            const float4 a = *(const float4 *)(qp + 16 * s), b = *(const float4 *)(qp + 16 * s + 4);
-            ss += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w + b.x * b.x + b.y * b.y + b.z * b.z + b.w * b.w;
-        }
-        ss = xor32_sum(ss);  // the row's other 64 dims are in lane ^ 32
-        const float scale = 1.0f / sqrtf(ss / HEAD_DIM + P.rms_eps);
         const float qs = LOG2E / sqrtf((float)HEAD_DIM);
+        uint2 *const qa = (uint2 *)&q_lds[wave][0][0];  // 8-byte halves of the f16x8 units
 #pragma unroll
-        for (int s = 0; s < 4; s++) {
-            float x0[8], x1[8], w0[8], w1[8];
-            *(float4 *)&x0[0] = *(const float4 *)(qp + 16 * s);
-            *(float4 *)&x0[4] = *(const float4 *)(qp + 16 * s + 4);
-            *(float4 *)&x1[0] = *(const float4 *)(qp + 16 * s + 64);
-            *(float4 *)&x1[4] = *(const float4 *)(qp + 16 * s + 68);
-            *(float4 *)&w0[0] = *(const float4 *)(P.q_norm + 16 * s + 8 * hh);
-            *(float4 *)&w0[4] = *(const float4 *)(P.q_norm + 16 * s + 8 * hh + 4);
-            *(float4 *)&w1[0] = *(const float4 *)(P.q_norm + 16 * s + 64 + 8 * hh);
-            *(float4 *)&w1[4] = *(const float4 *)(P.q_norm + 16 * s + 64 + 8 * hh + 4);
+        for (int g = 0; g < 4; g++) {
+            const int r = rr + 8 * g;
+            float ss = 0.f;
 #pragma unroll
-            for (int e = 0; e < 8; e++) {
-                float cs = 1.f, sn = 0.f;
-                if (P.has_rope) rope_sincos_fast((float)my_qp * P.rope_freq[16 * s + 8 * hh + e], &sn, &cs);
-                const float a = x0[e] * scale * w0[e], b = x1[e] * scale * w1[e];
-                qf[s][e] = row_ok ? (_Float16)((a * cs - b * sn) * qs) : (_Float16)0;
-                qf[s + 4][e] = row_ok ? (_Float16)((a * sn + b * cs) * qs) : (_Float16)0;
+            for (int k = 0; k < 4; k++)
+                ss += x[g][k].x * x[g][k].x + x[g][k].y * x[g][k].y + x[g][k].z * x[g][k].z + x[g][k].w * x[g][k].w;
+            ss = lane8_sum(ss);
+            const float scale = t0 + r < P.T ? qs / sqrtf(ss / HEAD_DIM + P.rms_eps) : 0.f;
+            const float pos = (float)(P.p0 + t0 + r);
+            _Float16 h[4][4];
+#pragma unroll
+            for (int k = 0; k < 2; k++) {
+                const float *x0 = &x[g][k].x, *x1 = &x[g][k + 2].x, *w0 = &w[k].x, *w1 = &w[k + 2].x, *f = &rf[k].x;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const float a0 = x0[j] * w0[j], a1 = x1[j] * w1[j];
+                    float cs = 1.f, sn = 0.f;
+                    if (P.has_rope) rope_sincos_fast(pos * f[j], &sn, &cs);
+                    h[k][j] = (_Float16)((a0 * cs - a1 * sn) * scale);
+                    h[k + 2][j] = (_Float16)((a0 * sn + a1 * cs) * scale);
+                }
+            }
+            // dims 32k + 4q8 + j: unit [s = 2k + (q8 >> 2)][r + 32((q8 >> 1) & 1)], half q8 & 1
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+                const h4 v = {h[k][0], h[k][1], h[k][2], h[k][3]};
+                qa[((2 * k + (q8 >> 2)) * 64 + r + 32 * ((q8 >> 1) & 1)) * 2 + (q8 & 1)] = __builtin_bit_cast(uint2, v);
             }
         }
+#pragma unroll
+        for (int st = 0; st < 8; st++) qf[st] = q_lds[wave][st][lane];
     }
 
     float m = P.sinks[hq] * LOG2E, l = hh == 0 ? 1.f : 0.f;
@@ -353,16 +379,29 @@ __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const Pref
         __syncthreads();
     }
 
-    if (!row_ok) return;
-    const float inv = 1.0f / xor32_sum(l);
-    float *o = P.att + (size_t)my_t * Q_DIM + hq * HEAD_DIM;
+    // ---- output rows, normalised, through this wave's LDS area (32 rows x 64 dims of
+    //      f32 at a time; float4 column c of row r at r * 16 + (c ^ (r & 15)), so both
+    //      sides are conflict-free) and stored row-coalesced: 16 lanes write one row's
+    //      256 bytes ----
+    const float inv = 1.0f / xor32_sum(l);  // rows past T: l = 1, acc = 0
+    float4 *const ob = (float4 *)&q_lds[wave][0][0];
 #pragma unroll
-    for (int dt = 0; dt < 4; dt++)
+    for (int half = 0; half < 2; half++) {
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            float4 v = {acc[dt][4 * j] * inv, acc[dt][4 * j + 1] * inv, acc[dt][4 * j + 2] * inv, acc[dt][4 * j + 3] * inv};
-            *(float4 *)(o + 32 * dt + 8 * j + 4 * hh) = v;
+        for (int d2 = 0; d2 < 2; d2++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const f32x16 &a = acc[2 * half + d2];
+                const int c = 8 * d2 + 2 * j + hh;  // dims 32 d2 + 8j + 4hh of the half
+                ob[col * 16 + (c ^ (col & 15))] = float4{a[4 * j] * inv, a[4 * j + 1] * inv, a[4 * j + 2] * inv, a[4 * j + 3] * inv};
+            }
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int r = 4 * i + (lane >> 4), c = lane & 15;
+            const float4 v = ob[r * 16 + (c ^ (r & 15))];
+            if (t0 + r < P.T) *(float4 *)(P.att + (size_t)(t0 + r) * Q_DIM + hq * HEAD_DIM + 64 * half + 4 * c) = v;
         }
+    }
 }
 
 hipError_t launch_prefill(const PrefillParams &P, int dtype, hipStream_t stream) {

@@ -117,6 +117,14 @@ constexpr int DPP_ROR1 = 0x121, DPP_ROR2 = 0x122, DPP_ROR4 = 0x124, DPP_ROR8 = 0
 // x of lane l ^ 8 (a rotation by 8 within the row of 16)
 __device__ inline float lane_xor8(float x) { return dpp<DPP_ROR8>(x); }
 
+constexpr int DPP_QUAD_XOR1 = 0xb1, DPP_QUAD_XOR2 = 0x4e, DPP_HALF_MIRROR = 0x141;
+// Sum over the aligned group of 8 lanes; all 8 get the same value.
+__device__ inline float lane8_sum(float x) {
+    x += dpp<DPP_QUAD_XOR1>(x);
+    x += dpp<DPP_QUAD_XOR2>(x);
+    return x + dpp<DPP_HALF_MIRROR>(x);
+}
+
 // f(x of lane l, x of lane l ^ 16): the swap leaves rows (0,0,2,2) in one register and
 // (1,1,3,3) in the other, so every lane combines the same pair in the same order.
 __device__ inline float xor16_sum(float x) {
@@ -177,11 +185,17 @@ __device__ inline float2 norm_rope_pair(float2 x, float2 w, float eps, bool rope
 }
 
 // The same angle's sin/cos on the hardware sine/cosine (v_sin_f32 / v_cos_f32, whose
-// argument is in turns) after the double-precision reduction: about 1e-6 absolute, for
-// operands that are rounded to f16 right after (prefill's q).
+// argument is in turns), for operands that are rounded to f16 right after (prefill's q).
+// The angle is reduced to [-1/2, 1/2] turns in float arithmetic: t + e = a * c_hi
+// exactly (e from an fma), t - rint(t) is exact, and a * c_lo carries the rest of
+// 1/(2 pi), so r is within ~3e-8 turns of the exact reduction for |a| up to ~1e7.
+// Contraction is off so that t stays the rounded product e was taken from.
 __device__ inline void rope_sincos_fast(float a, float *sn, float *cs) {
-    const double turns = (double)a * 0.15915494309189533576888376337251;  // 1 / (2 pi)
-    const float r = (float)(turns - rint(turns));
+#pragma clang fp contract(off)
+    const float c_hi = 0.15915494f, c_lo = 6.4206382e-09f;  // 1/(2 pi) = c_hi + c_lo
+    const float t = a * c_hi;
+    const float e = __builtin_fmaf(a, c_hi, -t);
+    const float r = (t - __builtin_rintf(t)) + __builtin_fmaf(a, c_lo, e);
     *sn = __builtin_amdgcn_sinf(r);
     *cs = __builtin_amdgcn_cosf(r);
 }
