@@ -340,12 +340,18 @@ __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const Pref
                     s[e] = ok ? s[e] : -INFINITY;
                 }
             }
-            float mt = fmaxf(fmaxf(fmaxf(s[0], s[1]), s[2]), fmaxf(fmaxf(s[3], s[4]), s[5]));
-            mt = fmaxf(fmaxf(mt, fmaxf(s[6], s[7])), fmaxf(fmaxf(s[8], s[9]), s[10]));
-            mt = fmaxf(fmaxf(mt, fmaxf(s[11], s[12])), fmaxf(fmaxf(s[13], s[14]), s[15]));
-            mt = xor32_max(mt);
-            if (__builtin_amdgcn_ballot_w64(mt > PF_RESCALE_LOG2) != 0) {  // wave-uniform, rare
-                const float d = fmaxf(mt, 0.f);  // raise m by d
+            // Does any score exceed the running max by more than the margin? Scores are
+            // finite or -inf, so compared as signed integers every float above the margin
+            // is above its bit pattern and every negative float below it: an integer max
+            // tree, with the row's float max only on the rare rescale path.
+            int mi = __float_as_int(s[0]);
+#pragma unroll
+            for (int e = 1; e < 16; e++) mi = max(mi, __float_as_int(s[e]));
+            if (__builtin_amdgcn_ballot_w64(mi > __float_as_int(PF_RESCALE_LOG2)) != 0) {  // wave-uniform, rare
+                float mt = s[0];
+#pragma unroll
+                for (int e = 1; e < 16; e++) mt = fmaxf(mt, s[e]);
+                const float d = fmaxf(xor32_max(mt), 0.f);  // raise the row's m by d
                 const float corr = __builtin_amdgcn_exp2f(-d);
                 m += d;
 #pragma unroll
