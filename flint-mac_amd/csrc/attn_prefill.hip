@@ -27,14 +27,14 @@
 // Any T in one call: the attention copy is a linear buffer of kbase..p0+T, so
 // the reference's 512-token chunking (ring room, flint_config.h:29-31) is not
 // needed.
+#include <climits>
+
 #include "common.h"
 #include "flint_attn_internal.h"
 
 namespace flint {
 
 constexpr int PF_BQ = 32;  // query positions per workgroup
-constexpr int PF_TILES = 2;              // 32-key MFMA tiles per LDS stage
-constexpr int PF_BK = 32 * PF_TILES;     // keys per LDS stage
 constexpr float PF_RESCALE_LOG2 = 8.f;  // lazy running-max margin (p stays below 2^8)
 
 // S^T row i (MFMA A row) holds key sigma(i) of its 32-key tile: bits 2 and 3 of i
@@ -187,32 +187,91 @@ __global__ __launch_bounds__(256) void kv_prep_kernel(const PrefillParams P) {
 // flash attention
 constexpr int PF_WAVES = 8;                  // one q head of the GQA group per wave
 constexpr int PF_THREADS = PF_WAVES * 64;
-constexpr int PF_STAGE_UNITS = PF_TILES * 16 * 64;  // 16-byte units per stage
-constexpr int PF_UNITS_PER_THREAD = PF_STAGE_UNITS / PF_THREADS;
+constexpr int PF_TILE_UNITS = 16 * 64;       // 16-byte units per 32-key tile (16 KiB)
+constexpr int PF_UNITS_PER_THREAD = PF_TILE_UNITS / PF_THREADS;
 
-// One stage of the attention copy (PF_TILES 16 KiB tiles) as 16-byte units, read
-// contiguously: units tid + 512 i.
-struct PfStage {
+// One tile of the attention copy as 16-byte units, read contiguously: units tid + 512 i.
+struct PfTile {
     u32x4 u[PF_UNITS_PER_THREAD];
 };
-__device__ inline void pf_gload(PfStage &R, const _Float16 *__restrict__ src, int tid) {
+__device__ inline void pf_gload(PfTile &R, const _Float16 *__restrict__ src, int tid) {
 #pragma unroll
     for (int i = 0; i < PF_UNITS_PER_THREAD; i++) R.u[i] = *(const u32x4 *)(src + 8 * (tid + PF_THREADS * i));
 }
-__device__ inline void pf_lstore(const PfStage &R, f16x8 (*dst)[16][64], int tid) {
+__device__ inline void pf_lstore(const PfTile &R, f16x8 (*dst)[64], int tid) {
 #pragma unroll
     for (int i = 0; i < PF_UNITS_PER_THREAD; i++) {
         const int u = tid + PF_THREADS * i;
-        dst[u >> 10][(u >> 6) & 15][u & 63] = __builtin_bit_cast(f16x8, R.u[i]);
+        dst[u >> 6][u & 63] = __builtin_bit_cast(f16x8, R.u[i]);
     }
+}
+
+// Scores S^T = K Q^T of one tile for this wave's head, relative to the running max (the
+// chain starts from -m): lane (col, hh) holds query row col, keys
+// kp0 + 16(j>>1) + 8hh + 4(j&1) + r in element 4j + r.
+__device__ __forceinline__ f32x16 pf_scores(const f16x8 (&kf)[8], const f16x8 (&qf)[8], const f32x16 &negm) {
+    f32x16 s = mfma32_f16(kf[0], qf[0], negm);
+#pragma unroll
+    for (int st = 1; st < 8; st++) s = mfma32_f16(kf[st], qf[st], s);
+    return s;
+}
+// Keys outside the row's [key_lo, key_hi] (causal, SWA window, rows past T) get -inf.
+__device__ __forceinline__ void pf_mask(f32x16 &s, int kp0, int hh, int key_lo, int key_hi) {
+#pragma unroll
+    for (int e = 0; e < 16; e++) {
+        const int j = e >> 2, r = e & 3;
+        const int kp = kp0 + 16 * (j >> 1) + 8 * hh + 4 * (j & 1) + r;
+        s[e] = (kp >= key_lo) & (kp <= key_hi) ? s[e] : -INFINITY;
+    }
+}
+// Does any score exceed the running max by more than the margin? Scores are finite or
+// -inf, so compared as signed integers every float above the margin is above its bit
+// pattern and every negative float below it: an integer max tree.
+__device__ __forceinline__ bool pf_over_margin(const f32x16 &s) {
+    int mi = __float_as_int(s[0]);
+#pragma unroll
+    for (int e = 1; e < 16; e++) mi = max(mi, __float_as_int(s[e]));
+    return __builtin_amdgcn_ballot_w64(mi > __float_as_int(PF_RESCALE_LOG2)) != 0;
+}
+// Raise the running max to cover s (wave-uniform call, rare): the row's m grows by d,
+// l and acc scale by 2^-d, s is re-expressed against the new m.
+__device__ __forceinline__ void pf_rescale(f32x16 &s, float &m, float &l, f32x16 &negm, f32x16 (&acc)[4]) {
+    float mt = s[0];
+#pragma unroll
+    for (int e = 1; e < 16; e++) mt = fmaxf(mt, s[e]);
+    const float d = fmaxf(xor32_max(mt), 0.f);
+    const float corr = __builtin_amdgcn_exp2f(-d);
+    m += d;
+#pragma unroll
+    for (int e = 0; e < 16; e++) negm[e] = -m;
+    l *= corr;
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++) acc[dt] *= corr;
+#pragma unroll
+    for (int e = 0; e < 16; e++) s[e] -= d;
+}
+// P = 2^s in f16 (the MFMA operand), l += the same rounded values.
+__device__ __forceinline__ void pf_softmax(const f32x16 &s, f16x8 (&pf)[2], float &l) {
+#pragma unroll
+    for (int e = 0; e < 16; e++) pf[e >> 3][e & 7] = (_Float16)__builtin_amdgcn_exp2f(s[e]);
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const h2 one2 = {(_Float16)1, (_Float16)1};
+#pragma unroll
+    for (int e = 0; e < 16; e += 2) l = __builtin_amdgcn_fdot2(h2{pf[e >> 3][e & 7], pf[e >> 3][(e & 7) + 1]}, one2, l, false);
+}
+__device__ __forceinline__ void pf_pv(f32x16 (&acc)[4], const f16x8 (&vf)[8], const f16x8 (&pf)[2]) {
+#pragma unroll
+    for (int kk = 0; kk < 2; kk++)
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++) acc[dt] = mfma32_f16(vf[2 * dt + kk], pf[kk], acc[dt]);
 }
 
 // Workgroup: 32 query positions x the 8 q heads of kv head kvh, wave w = head 8 kvh + w.
 // Two waves per SIMD (about 170 registers each), so one wave's softmax overlaps the
 // other's MFMAs.
 __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const PrefillParams P, int n_qblocks) {
-    // LDS: two stages (double buffer) of two tiles in the attention-copy order
-    __shared__ f16x8 stage[2][PF_TILES][16][64];
+    // LDS: three 32-key tiles in the attention-copy order (tile t in ring[(t - t_lo) % 3])
+    __shared__ f16x8 ring[3][16][64];
     // LDS: 8 KiB per wave that hands q over to the operand order, and later the output
     __shared__ f16x8 q_lds[PF_WAVES][8][64];
 
@@ -226,7 +285,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const Pref
     const bool row_ok = my_t < P.T;
 
     const int k_lo = P.is_swa ? max(P.kbase, q_first - (P.window - 1)) : 0;
-    const int st_lo = (k_lo - P.kbase) / PF_BK, st_hi = (q_last - P.kbase) / PF_BK;  // stages
+    const int t_lo = (k_lo - P.kbase) >> 5, t_hi = (q_last - P.kbase) >> 5;  // 32-key tiles
     const _Float16 *__restrict__ skv = P.sk + (size_t)kvh * (P.k_rows >> 5) * (16 * 64 * 8);
 
     // ---- Q fragments (B operand of S^T = K Q^T): lane (col, hh) needs query row `col`,
@@ -253,8 +312,10 @@ __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const Pref
 #pragma unroll
         for (int k = 0; k < 4; k++) x[g][k] = *(const float4 *)(qp + 32 * k);
     }
-    PfStage R;
-    pf_gload(R, skv + (size_t)st_lo * (PF_STAGE_UNITS * 8), tid);
+    PfTile R0, R1, R2;
+    pf_gload(R0, skv + (size_t)t_lo * (PF_TILE_UNITS * 8), tid);
+    if (t_lo + 1 <= t_hi) pf_gload(R1, skv + (size_t)(t_lo + 1) * (PF_TILE_UNITS * 8), tid);
+    if (t_lo + 2 <= t_hi) pf_gload(R2, skv + (size_t)(t_lo + 2) * (PF_TILE_UNITS * 8), tid);
 
     f16x8 qf[8];
     {
@@ -307,82 +368,101 @@ __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const Pref
     const int key_hi = row_ok ? my_qp : -1;
     const int key_lo = P.is_swa ? max(my_qp - (P.window - 1), 0) : 0;
 
-    pf_lstore(R, stage[0], tid);
-    if (st_lo + 1 <= st_hi) pf_gload(R, skv + (size_t)(st_lo + 1) * (PF_STAGE_UNITS * 8), tid);
+    // ---- software pipeline over the key tiles. Step t computes P of tile t and its P V
+    //      product while the score MFMAs of tile t + 1 run, in explicit slots with a
+    //      scheduling fence after each:
+    //       * slot g < 8 turns scores 2g, 2g+1 of tile t into P (exp, f16, row sum) and
+    //         issues score MFMA g of tile t + 1; slots 0-2 also store tile t + 3 into the
+    //         LDS slot tile t left and request tile t + 4;
+    //       * slot 8 + j issues P V MFMA j of tile t and reads the V fragment of tile t + 1
+    //         and the K fragment of tile t + 2 into the registers that MFMA and score MFMA j
+    //         freed, with a step of tile t + 1's rescale test.
+    //      Tiles t + 1 and t + 2 were stored in earlier steps, so no step waits on LDS
+    //      after its barrier; tile t's slot is free once the barrier ending step t - 1 is
+    //      passed (its last fragments were read in step t - 1). ----
+    pf_lstore(R0, ring[0], tid);
+    if (t_lo + 1 <= t_hi) pf_lstore(R1, ring[1], tid);
+    if (t_lo + 2 <= t_hi) pf_lstore(R2, ring[2], tid);
+    PfTile R;
+    if (t_lo + 3 <= t_hi) pf_gload(R, skv + (size_t)(t_lo + 3) * (PF_TILE_UNITS * 8), tid);
     __syncthreads();
 
-    for (int sk = st_lo; sk <= st_hi; sk++) {
-        const int buf = (sk - st_lo) & 1;
+    // wave-uniform: does any row of this block need masking in the tile at key kp0?
+    auto edge = [&](int kp0) { return kp0 + 31 > q_first || (P.is_swa && q_last - kp0 >= P.window) || t0 + PF_BQ > P.T; };
+    f16x8 kf[8], vf[8];
 #pragma unroll
-        for (int h = 0; h < PF_TILES; h++) {  // the stage's 32-key MFMA tiles
-            const int kp0 = P.kbase + sk * PF_BK + 32 * h;  // key position of the tile's first key
-            if (kp0 > q_last) break;   // wave-uniform: past the block's last query
-            // all 16 operand fragments of the tile requested at once: the K ones feed the
-            // score MFMAs back to back, the V ones land during the softmax
-            f16x8 kf[8], vf[8];
+    for (int st = 0; st < 8; st++) kf[st] = ring[0][st][lane];
 #pragma unroll
-            for (int st = 0; st < 8; st++) kf[st] = stage[buf][h][st][lane];
+    for (int i = 0; i < 8; i++) vf[i] = ring[0][8 + i][lane];
+    f32x16 s_cur = pf_scores(kf, qf, negm);
+    if (edge(P.kbase + 32 * t_lo)) pf_mask(s_cur, P.kbase + 32 * t_lo, hh, key_lo, key_hi);
+    if (pf_over_margin(s_cur)) pf_rescale(s_cur, m, l, negm, acc);
+    if (t_lo + 1 <= t_hi) {
 #pragma unroll
-            for (int i = 0; i < 8; i++) vf[i] = stage[buf][h][8 + i][lane];
+        for (int st = 0; st < 8; st++) kf[st] = ring[1][st][lane];
+    }
+
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const h2 one2 = {(_Float16)1, (_Float16)1};
+    // slots (in the ring) of tiles t, t + 1, t + 2
+    int sl0 = 0, sl1 = 1, sl2 = 2;
+    auto step = [&](const f32x16 &sc, f32x16 &sn, int t) {
+        const int kp1 = P.kbase + 32 * (t + 1);
+        const bool st3 = t + 3 <= t_hi, ld4 = t + 4 <= t_hi;
+        uint32_t pw[8];  // P of tile t as f16 pairs
+#pragma unroll
+        for (int g = 0; g < 8; g++) {
+            const h2 pp = {(_Float16)__builtin_amdgcn_exp2f(sc[2 * g]), (_Float16)__builtin_amdgcn_exp2f(sc[2 * g + 1])};
+            pw[g] = __builtin_bit_cast(uint32_t, pp);
+            l = __builtin_amdgcn_fdot2(pp, one2, l, false);
+            asm volatile("" : "+v"(l));  // keeps the row sum in this slot
+            sn = mfma32_f16(kf[g], qf[g], g == 0 ? negm : sn);
+            if (g < PF_UNITS_PER_THREAD && st3) {
+                const int u = tid + PF_THREADS * g;
+                ring[sl0][u >> 6][u & 63] = __builtin_bit_cast(f16x8, R.u[g]);
+            }
+            if (g == PF_UNITS_PER_THREAD && ld4) pf_gload(R, skv + (size_t)(t + 4) * (PF_TILE_UNITS * 8), tid);
             __builtin_amdgcn_sched_barrier(0);
-            // scores relative to the running max: the first MFMA adds K Q^T to -m
-            f32x16 s = mfma32_f16(kf[0], qf[0], negm);
-#pragma unroll
-            for (int st = 1; st < 8; st++) s = mfma32_f16(kf[st], qf[st], s);
-            // wave-uniform: does any row of this block need masking in this tile?
-            if (kp0 + 31 > q_first || (P.is_swa && q_last - kp0 >= P.window) || t0 + PF_BQ > P.T) {
-                // lane holds query row `col`, keys kp0 + 16(j>>1) + 8hh + 4(j&1) + r for element 4j + r
-#pragma unroll
-                for (int e = 0; e < 16; e++) {
-                    const int j = e >> 2, r = e & 3;
-                    const int kp = kp0 + 16 * (j >> 1) + 8 * hh + 4 * (j & 1) + r;
-                    const bool ok = (kp >= key_lo) & (kp <= key_hi);
-                    s[e] = ok ? s[e] : -INFINITY;
-                }
-            }
-            // Does any score exceed the running max by more than the margin? Scores are
-            // finite or -inf, so compared as signed integers every float above the margin
-            // is above its bit pattern and every negative float below it: an integer max
-            // tree, with the row's float max only on the rare rescale path.
-            int mi = __float_as_int(s[0]);
-#pragma unroll
-            for (int e = 1; e < 16; e++) mi = max(mi, __float_as_int(s[e]));
-            if (__builtin_amdgcn_ballot_w64(mi > __float_as_int(PF_RESCALE_LOG2)) != 0) {  // wave-uniform, rare
-                float mt = s[0];
-#pragma unroll
-                for (int e = 1; e < 16; e++) mt = fmaxf(mt, s[e]);
-                const float d = fmaxf(xor32_max(mt), 0.f);  // raise the row's m by d
-                const float corr = __builtin_amdgcn_exp2f(-d);
-                m += d;
-#pragma unroll
-                for (int e = 0; e < 16; e++) negm[e] = -m;
-                l *= corr;
-#pragma unroll
-                for (int dt = 0; dt < 4; dt++) acc[dt] *= corr;
-#pragma unroll
-                for (int e = 0; e < 16; e++) s[e] -= d;
-            }
-            // P in f16 (the MFMA operand); l sums the same rounded values
-            f16x8 pf[2];
-#pragma unroll
-            for (int e = 0; e < 16; e++) pf[e >> 3][e & 7] = (_Float16)__builtin_amdgcn_exp2f(s[e]);
-            typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-            const h2 one2 = {(_Float16)1, (_Float16)1};
-#pragma unroll
-            for (int e = 0; e < 16; e += 2) l = __builtin_amdgcn_fdot2(h2{pf[e >> 3][e & 7], pf[e >> 3][(e & 7) + 1]}, one2, l, false);
-#pragma unroll
-            for (int dt = 0; dt < 4; dt++)
-#pragma unroll
-                for (int kk = 0; kk < 2; kk++)
-                    acc[dt] = mfma32_f16(vf[2 * dt + kk], pf[kk], acc[dt]);
         }
-        if (sk + 1 <= st_hi) {
-            // stage sk + 1 into the other buffer (read by no wave since the last barrier)
-            // and request stage sk + 2
-            pf_lstore(R, stage[buf ^ 1], tid);
-            if (sk + 2 <= st_hi) pf_gload(R, skv + (size_t)(sk + 2) * (PF_STAGE_UNITS * 8), tid);
+        const f16x8 pf[2] = {__builtin_bit_cast(f16x8, u32x4{pw[0], pw[1], pw[2], pw[3]}),
+                             __builtin_bit_cast(f16x8, u32x4{pw[4], pw[5], pw[6], pw[7]})};
+        int mi = INT_MIN;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int kk = j >> 2, dt = j & 3;
+            acc[dt] = mfma32_f16(vf[2 * dt + kk], pf[kk], acc[dt]);
+            vf[2 * dt + kk] = ring[sl1][8 + 2 * dt + kk][lane];
+            kf[j] = ring[sl2][j][lane];  // unused after the last tile
+            mi = max(mi, max(__float_as_int(sn[2 * j]), __float_as_int(sn[2 * j + 1])));
+            __builtin_amdgcn_sched_barrier(0);
         }
+        const bool over = __builtin_amdgcn_ballot_w64(mi > __float_as_int(PF_RESCALE_LOG2)) != 0;
+        // The test ran before the mask: a masked score can only raise m needlessly, which
+        // the rescale handles exactly. Edge tiles are few, so they are masked outside the
+        // interleave.
+        if (edge(kp1)) pf_mask(sn, kp1, hh, key_lo, key_hi);
+        if (over) pf_rescale(sn, m, l, negm, acc);
         __syncthreads();
+        const int sl = sl0;
+        sl0 = sl1;
+        sl1 = sl2;
+        sl2 = sl;
+    };
+    // two steps per iteration, so the score buffers alternate without copies
+    f32x16 s_alt;
+    int t = t_lo;
+    for (; t + 2 <= t_hi; t += 2) {
+        step(s_cur, s_alt, t);
+        step(s_alt, s_cur, t + 1);
+    }
+    if (t < t_hi) {
+        step(s_cur, s_alt, t);
+        s_cur = s_alt;
+    }
+    {  // the last tile
+        f16x8 pf[2];
+        pf_softmax(s_cur, pf, l);
+        pf_pv(acc, vf, pf);
     }
 
     // ---- output rows, normalised, through this wave's LDS area (32 rows x 64 dims of
