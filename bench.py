@@ -29,7 +29,7 @@ N_FULL_FLINT, N_SWA_FLINT = 14, 35
 # HBM bytes per decode call (attn_decode_kernel + attn_combine_kernel) at 32k, from rocprofv3
 # --pmc FETCH_SIZE and WRITE_SIZE runs of `bench.py --only decode --no-cpu`, each scaled by the
 # counter's reading for the 64 MiB calibration copy (profiles/decode_32k_f16.md).
-DECODE_TRAFFIC_BYTES = 69927042
+DECODE_TRAFFIC_BYTES = 68985542
 
 
 def log(msg):
@@ -299,8 +299,9 @@ def main():
                          "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(d["bytes_per_launch"] / (t_full * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                          "traffic": DECODE_TRAFFIC_BYTES,
-                         "kernel": "one flint_attn_decode call = attn_decode_kernel<f16> (256 blocks) + "
-                                   "attn_combine_kernel (split merge); time per call from HIP events",
+                         "kernel": "one flint_attn_decode call = attn_decode_kernel<f16> (43 key splits x 4 kv "
+                                   "heads = 172 workgroups) + attn_combine_kernel (split merge); time per call "
+                                   "from HIP events",
                          "bytes_per_launch": d["bytes_per_launch"], "host_bound": d["host_bound"]},
         })
     if "prefill" in res:
