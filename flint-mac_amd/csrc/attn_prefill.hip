@@ -189,6 +189,7 @@ constexpr int PF_WAVES = 8;                  // one q head of the GQA group per 
 constexpr int PF_THREADS = PF_WAVES * 64;
 constexpr int PF_TILE_UNITS = 16 * 64;       // 16-byte units per 32-key tile (16 KiB)
 constexpr int PF_UNITS_PER_THREAD = PF_TILE_UNITS / PF_THREADS;
+constexpr int PF_RING = 5;                   // tiles held in LDS (a barrier every two tiles)
 
 // One tile of the attention copy as 16-byte units, read contiguously: units tid + 512 i.
 struct PfTile {
@@ -270,8 +271,8 @@ __device__ __forceinline__ void pf_pv(f32x16 (&acc)[4], const f16x8 (&vf)[8], co
 // Two waves per SIMD (about 170 registers each), so one wave's softmax overlaps the
 // other's MFMAs.
 __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const PrefillParams P, int n_qblocks) {
-    // LDS: three 32-key tiles in the attention-copy order (tile t in ring[(t - t_lo) % 3])
-    __shared__ f16x8 ring[3][16][64];
+    // LDS: five 32-key tiles in the attention-copy order (tile t in ring[(t - t_lo) % 5])
+    __shared__ f16x8 ring[PF_RING][16][64];
     // LDS: 8 KiB per wave that hands q over to the operand order, and later the output
     __shared__ f16x8 q_lds[PF_WAVES][8][64];
 
@@ -312,10 +313,11 @@ __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const Pref
 #pragma unroll
         for (int k = 0; k < 4; k++) x[g][k] = *(const float4 *)(qp + 32 * k);
     }
-    PfTile R0, R1, R2;
+    PfTile R0, R1, R2, R3;
     pf_gload(R0, skv + (size_t)t_lo * (PF_TILE_UNITS * 8), tid);
     if (t_lo + 1 <= t_hi) pf_gload(R1, skv + (size_t)(t_lo + 1) * (PF_TILE_UNITS * 8), tid);
     if (t_lo + 2 <= t_hi) pf_gload(R2, skv + (size_t)(t_lo + 2) * (PF_TILE_UNITS * 8), tid);
+    if (t_lo + 3 <= t_hi) pf_gload(R3, skv + (size_t)(t_lo + 3) * (PF_TILE_UNITS * 8), tid);
 
     f16x8 qf[8];
     {
@@ -372,19 +374,21 @@ __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const Pref
     //      product while the score MFMAs of tile t + 1 run, in explicit slots with a
     //      scheduling fence after each:
     //       * slot g < 8 turns scores 2g, 2g+1 of tile t into P (exp, f16, row sum) and
-    //         issues score MFMA g of tile t + 1; slots 0-2 also store tile t + 3 into the
-    //         LDS slot tile t left and request tile t + 4;
+    //         issues score MFMA g of tile t + 1; slots 0-2 also store tile t + 4 into the
+    //         LDS ring and request tile t + 5;
     //       * slot 8 + j issues P V MFMA j of tile t and reads the V fragment of tile t + 1
     //         and the K fragment of tile t + 2 into the registers that MFMA and score MFMA j
     //         freed, with a step of tile t + 1's rescale test.
-    //      Tiles t + 1 and t + 2 were stored in earlier steps, so no step waits on LDS
-    //      after its barrier; tile t's slot is free once the barrier ending step t - 1 is
-    //      passed (its last fragments were read in step t - 1). ----
+    //      Steps run in pairs (t_lo + 2j, t_lo + 2j + 1) with one barrier after each pair.
+    //      A pair reads tiles t + 1 .. t + 3 (stored before the previous barrier) and
+    //      writes tiles t + 4, t + 5 into the two ring slots whose tiles were last read in
+    //      the previous pair, so five slots never conflict. ----
     pf_lstore(R0, ring[0], tid);
     if (t_lo + 1 <= t_hi) pf_lstore(R1, ring[1], tid);
     if (t_lo + 2 <= t_hi) pf_lstore(R2, ring[2], tid);
+    if (t_lo + 3 <= t_hi) pf_lstore(R3, ring[3], tid);
     PfTile R;
-    if (t_lo + 3 <= t_hi) pf_gload(R, skv + (size_t)(t_lo + 3) * (PF_TILE_UNITS * 8), tid);
+    if (t_lo + 4 <= t_hi) pf_gload(R, skv + (size_t)(t_lo + 4) * (PF_TILE_UNITS * 8), tid);
     __syncthreads();
 
     // wave-uniform: does any row of this block need masking in the tile at key kp0?
@@ -401,14 +405,16 @@ __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const Pref
 #pragma unroll
         for (int st = 0; st < 8; st++) kf[st] = ring[1][st][lane];
     }
+    __syncthreads();  // tile t_lo's slot is rewritten in the first pair
 
     typedef _Float16 h2 __attribute__((ext_vector_type(2)));
     const h2 one2 = {(_Float16)1, (_Float16)1};
-    // slots (in the ring) of tiles t, t + 1, t + 2
-    int sl0 = 0, sl1 = 1, sl2 = 2;
-    auto step = [&](const f32x16 &sc, f32x16 &sn, int t) {
+    auto slot = [](int r) { return r >= PF_RING ? r - PF_RING : r; };
+    int sl0 = 0;  // ring slot of tile t
+    auto step = [&](const f32x16 &sc, f32x16 &sn, int t, bool bar) {
         const int kp1 = P.kbase + 32 * (t + 1);
-        const bool st3 = t + 3 <= t_hi, ld4 = t + 4 <= t_hi;
+        const int sl1 = slot(sl0 + 1), sl2 = slot(sl0 + 2), sl4 = slot(sl0 + 4);
+        const bool st4 = t + 4 <= t_hi, ld5 = t + 5 <= t_hi;
         uint32_t pw[8];  // P of tile t as f16 pairs
 #pragma unroll
         for (int g = 0; g < 8; g++) {
@@ -417,11 +423,11 @@ __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const Pref
             l = __builtin_amdgcn_fdot2(pp, one2, l, false);
             asm volatile("" : "+v"(l));  // keeps the row sum in this slot
             sn = mfma32_f16(kf[g], qf[g], g == 0 ? negm : sn);
-            if (g < PF_UNITS_PER_THREAD && st3) {
+            if (g < PF_UNITS_PER_THREAD && st4) {
                 const int u = tid + PF_THREADS * g;
-                ring[sl0][u >> 6][u & 63] = __builtin_bit_cast(f16x8, R.u[g]);
+                ring[sl4][u >> 6][u & 63] = __builtin_bit_cast(f16x8, R.u[g]);
             }
-            if (g == PF_UNITS_PER_THREAD && ld4) pf_gload(R, skv + (size_t)(t + 4) * (PF_TILE_UNITS * 8), tid);
+            if (g == PF_UNITS_PER_THREAD && ld5) pf_gload(R, skv + (size_t)(t + 5) * (PF_TILE_UNITS * 8), tid);
             __builtin_amdgcn_sched_barrier(0);
         }
         const f16x8 pf[2] = {__builtin_bit_cast(f16x8, u32x4{pw[0], pw[1], pw[2], pw[3]}),
@@ -442,21 +448,18 @@ __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const Pref
         // interleave.
         if (edge(kp1)) pf_mask(sn, kp1, hh, key_lo, key_hi);
         if (over) pf_rescale(sn, m, l, negm, acc);
-        __syncthreads();
-        const int sl = sl0;
+        if (bar) __syncthreads();
         sl0 = sl1;
-        sl1 = sl2;
-        sl2 = sl;
     };
     // two steps per iteration, so the score buffers alternate without copies
     f32x16 s_alt;
     int t = t_lo;
     for (; t + 2 <= t_hi; t += 2) {
-        step(s_cur, s_alt, t);
-        step(s_alt, s_cur, t + 1);
+        step(s_cur, s_alt, t, false);
+        step(s_alt, s_cur, t + 1, true);
     }
     if (t < t_hi) {
-        step(s_cur, s_alt, t);
+        step(s_cur, s_alt, t, false);
         s_cur = s_alt;
     }
     {  // the last tile
