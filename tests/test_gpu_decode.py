@@ -176,3 +176,31 @@ def test_decode_batch_matches_single(cuda, is_swa):
         kv1.decode(dq[s], one, p)
         torch.cuda.synchronize()
         np.testing.assert_allclose(got[s], one.cpu().numpy(), rtol=0, atol=1e-5)
+
+
+def test_decode_batch_long_contexts_auto_split(cuda):
+    """Config-5 shape: independent sequences at long, mixed contexts in one launch, with the
+    automatic split plan (one key-split size for the batch, so the sequences get different
+    split counts up to the grid's width; a sequence with one split is written directly by the
+    decode kernel). Every sequence equals the oracle."""
+    _say("decode batch, long mixed contexts, auto split")
+    rng = np.random.default_rng(44)
+    qn, kn, sk = layer_weights(rng)
+    positions = [4100, 17000, 40000, 65535, 700]
+    n_slots = 65536 + 32
+    kv = fa.KVLayer(is_swa=False, has_rope=False, n_slots=n_slots, kv_dtype="f16", q_norm=qn, k_norm=kn, sinks=sk,
+                    n_seq=len(positions))
+    L = oracle_layer(kv, qn, kn, sk, "f16")
+    qkv = rng.standard_normal((len(positions), QKV_DIM)).astype(np.float32)
+    wants = []
+    for s, p in enumerate(positions):
+        K, V = _history(rng, p + 1, "f16", outlier_frac=0.01)
+        _fill_cache(kv, K[:p], V[:p], np.arange(p), s)
+        wants.append(fo.decode_step(L, qkv[s], p, K.copy(), V.copy(), n_threads=8))
+    dq = torch.from_numpy(qkv).to(cuda)
+    att = torch.zeros((len(positions), Q_DIM), device=cuda)
+    kv.decode(dq, att, positions)
+    torch.cuda.synchronize()
+    got = att.cpu().numpy()
+    for s, p in enumerate(positions):
+        assert_close(got[s], wants[s], f"seq {s} pos {p}")
