@@ -1,7 +1,7 @@
 """Benchmark of the flint attention hot path on one MI355X.
 
 Primary line (`value`): fused decode attention at 32768 cached positions
-(full layer, f16 KV, 32 q / 4 kv heads, d=128, split-K +
+(benchmark config 3: full layer, f16 KV, 32 q / 4 kv heads, d=128, split-K +
 LSE merge + sink). One step = one decode token through 8 full-attention layers,
 each with its own 64 MiB KV cache, so a step streams 512 MiB and the 256 MB
 Infinity Cache cannot serve it. value = algorithmic KV bytes / step time (GB/s).
@@ -245,8 +245,9 @@ def main():
     ap.add_argument("--only", choices=["decode", "prefill", "config5"], default=None)
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py: this build runs on one GPU; the attention path shards by key range or sequence "
-              "(see DESIGN.md), but no multi-GPU figure is measured here. Use --gpus 1.", file=sys.stderr)
+        print("bench.py: this build runs on one GPU. The attention path would shard by key range (decode, "
+              "one LSE merge of per-GPU partials) or by sequence / kv head, but no multi-GPU figure is "
+              "measured here. Use --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     import torch

@@ -1,6 +1,6 @@
 """Shared input generators and comparison helpers for the attention tests.
 
-Inputs follow BASELINE.json's configs: raw q|k|v ~ N(0,1), RMSNorm gains
+Inputs follow the benchmark configs: raw q|k|v ~ N(0,1), RMSNorm gains
 ~ U(0.5, 1.5), per-head sink logits ~ N(0,1), seeded numpy generators.
 """
 import numpy as np

@@ -1,4 +1,4 @@
-"""Fused decode attention on the GPU against the CPU oracle (BASELINE configs 1-3
+"""Fused decode attention on the GPU against the CPU oracle (benchmark configs 1-3
 and the batched form of config 5), through the C ABI (flint_attn_decode,
 flint_attn_decode_batch). Tolerance: max-abs 2e-3 and mean-abs 2e-4 on the
 attention output; ring slot contents bit-exact for V (K within 1 ulp of the

@@ -1,4 +1,4 @@
-"""Batched prefill attention on the GPU against the CPU oracle (
+"""Batched prefill attention on the GPU against the CPU oracle (benchmark config 4,
 the reference's own `flint test-attn` probes, chunk invariance, prefill ==
 decode), through the C ABI (flint_attn_prefill, flint_attn_engine_debug_attn).
 Tolerance: max-abs 2e-3, mean-abs 2e-4; KV cache / ring slot contents
