@@ -251,14 +251,16 @@ __device__ __forceinline__ void pf_rescale(f32x16 &s, float &m, float &l, f32x16
 #pragma unroll
     for (int e = 0; e < 16; e++) s[e] -= d;
 }
-// P = 2^s in f16 (the MFMA operand), l += the same rounded values.
+// P = 2^s in f16 (the MFMA operand); l += P in fp32. (v_dot2 on the f16 pairs would sum
+// the rounded values, but it shares the matrix pipe's issue far worse than plain adds:
+// measured ~4x the cost of an fma between MFMAs.)
 __device__ __forceinline__ void pf_softmax(const f32x16 &s, f16x8 (&pf)[2], float &l) {
 #pragma unroll
-    for (int e = 0; e < 16; e++) pf[e >> 3][e & 7] = (_Float16)__builtin_amdgcn_exp2f(s[e]);
-    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-    const h2 one2 = {(_Float16)1, (_Float16)1};
-#pragma unroll
-    for (int e = 0; e < 16; e += 2) l = __builtin_amdgcn_fdot2(h2{pf[e >> 3][e & 7], pf[e >> 3][(e & 7) + 1]}, one2, l, false);
+    for (int e = 0; e < 16; e++) {
+        const float p = __builtin_amdgcn_exp2f(s[e]);
+        pf[e >> 3][e & 7] = (_Float16)p;
+        l += p;
+    }
 }
 __device__ __forceinline__ void pf_pv(f32x16 (&acc)[4], const f16x8 (&vf)[8], const f16x8 (&pf)[2]) {
 #pragma unroll
@@ -373,7 +375,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const Pref
     // ---- software pipeline over the key tiles. Step t computes P of tile t and its P V
     //      product while the score MFMAs of tile t + 1 run, in explicit slots with a
     //      scheduling fence after each:
-    //       * slot g < 8 turns scores 2g, 2g+1 of tile t into P (exp, f16, row sum) and
+    //       * slot g < 8 turns scores 2g, 2g+1 of tile t into P (exp, f16; fp32 row sum) and
     //         issues score MFMA g of tile t + 1; slots 0-2 also store tile t + 4 into the
     //         LDS ring and request tile t + 5;
     //       * slot 8 + j issues P V MFMA j of tile t and reads the V fragment of tile t + 1
@@ -408,7 +410,6 @@ __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const Pref
     __syncthreads();  // tile t_lo's slot is rewritten in the first pair
 
     typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-    const h2 one2 = {(_Float16)1, (_Float16)1};
     auto slot = [](int r) { return r >= PF_RING ? r - PF_RING : r; };
     int sl0 = 0;  // ring slot of tile t
     auto step = [&](const f32x16 &sc, f32x16 &sn, int t, bool bar) {
@@ -418,9 +419,10 @@ __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const Pref
         uint32_t pw[8];  // P of tile t as f16 pairs
 #pragma unroll
         for (int g = 0; g < 8; g++) {
-            const h2 pp = {(_Float16)__builtin_amdgcn_exp2f(sc[2 * g]), (_Float16)__builtin_amdgcn_exp2f(sc[2 * g + 1])};
+            const float e0 = __builtin_amdgcn_exp2f(sc[2 * g]), e1 = __builtin_amdgcn_exp2f(sc[2 * g + 1]);
+            const h2 pp = {(_Float16)e0, (_Float16)e1};
             pw[g] = __builtin_bit_cast(uint32_t, pp);
-            l = __builtin_amdgcn_fdot2(pp, one2, l, false);
+            l += e0 + e1;
             asm volatile("" : "+v"(l));  // keeps the row sum in this slot
             sn = mfma32_f16(kf[g], qf[g], g == 0 ? negm : sn);
             if (g < PF_UNITS_PER_THREAD && st4) {
