@@ -18,8 +18,9 @@
 //           a K/V tile is staged in LDS once per 256 rows. Q is normalised,
 //           rotated and scaled in the prologue (q never round-trips through HBM).
 //           Scores are S^T = K Q^T and O^T += V^T P^T on v_mfma_f32_32x32x16_f16
-//           with fp32 accumulation; K/V stream in 64-key stages, double-buffered
-//           in LDS with the next stage's loads in flight during the MFMAs; the
+//           with fp32 accumulation; K/V stream in 32-key tiles through a 5-tile
+//           LDS ring in a software pipeline (the next tile's score MFMAs between
+//           this tile's softmax instructions), one barrier per two tiles; the
 //           online softmax starts from m = sink, l = 1 (the sink is in the
 //           denominator only, prefill.metal:162), raises its running max lazily
 //           (only past a margin of 2^8) and masks kp <= qp and, on SWA layers,
@@ -270,8 +271,8 @@ __device__ __forceinline__ void pf_pv(f32x16 (&acc)[4], const f16x8 (&vf)[8], co
 }
 
 // Workgroup: 32 query positions x the 8 q heads of kv head kvh, wave w = head 8 kvh + w.
-// Two waves per SIMD (about 170 registers each), so one wave's softmax overlaps the
-// other's MFMAs.
+// Two waves per SIMD (about 250 registers each): while one wave runs softmax
+// instructions the other can issue MFMAs.
 __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const PrefillParams P, int n_qblocks) {
     // LDS: five 32-key tiles in the attention-copy order (tile t in ring[(t - t_lo) % 5])
     __shared__ f16x8 ring[PF_RING][16][64];
