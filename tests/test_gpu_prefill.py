@@ -172,3 +172,33 @@ def test_prefill_short_and_odd_shapes(cuda):
             torch.cuda.synchronize()
             want = _oracle_at(L, qkv, K, V, range(p0, p0 + T))
             assert_close(att.cpu().numpy(), np.stack([want[p] for p in range(p0, p0 + T)]), f"T={T} p0={p0}")
+
+
+@pytest.mark.parametrize("rollback", [300, 700])
+def test_prefill_after_rollback_swa_ring(cuda, rollback):
+    """Prefix reuse after a rollback (the reference's flint_truncate contract, capi.h:27-29,
+    and its caller's rule, server/src/main.rs:95-116): after positions 0..N-1, the sequence
+    is cut back to p = N - rollback and continues with new tokens. The 1024-slot SWA ring
+    still holds the window of p when the rollback is at most 511 tokens, so prefilling the
+    new tokens from p is exact; for a deeper rollback the caller re-prefills from
+    max(0, p - 512). Either way the outputs at p.. equal a fresh run of the new sequence."""
+    n, m = 1600, 1800
+    _say(f"prefill after rollback {rollback} (SWA ring)")
+    rng = np.random.default_rng(61)
+    qn, kn, sk = layer_weights(rng)
+    L = fo.Layer(qn, kn, sk, True, True, "f16", 1e4)
+    qkv_a = rng.standard_normal((n, QKV_DIM)).astype(np.float32)
+    p = n - rollback
+    qkv_b = np.concatenate([qkv_a[:p], rng.standard_normal((m - p, QKV_DIM)).astype(np.float32)])
+    kv = fa.KVLayer(is_swa=True, has_rope=True, n_slots=1024, kv_dtype="f16", q_norm=qn, k_norm=kn, sinks=sk,
+                    rope_theta=1e4)
+    att = torch.zeros((m, Q_DIM), device=cuda)
+    kv.prefill(torch.from_numpy(qkv_a).to(cuda), att[:n], 0)
+    start = p if rollback <= 511 else max(0, p - 512)
+    kv.prefill(torch.from_numpy(qkv_b[start:]).to(cuda), att[start:], start)
+    torch.cuda.synchronize()
+    got = att.cpu().numpy()
+    K, V = _oracle_history(L, qkv_b)
+    want = _oracle_at(L, qkv_b, K, V, [p, p + 1, p + 31, p + 300, m - 1])
+    for q, w in want.items():
+        assert_close(got[q], w, f"rollback {rollback} pos {q}")
