@@ -223,7 +223,7 @@ __device__ __forceinline__ void pf_mask(f32x16 &s, int kp0, int hh, int key_lo, 
     for (int e = 0; e < 16; e++) {
         const int j = e >> 2, r = e & 3;
         const int kp = kp0 + 16 * (j >> 1) + 8 * hh + 4 * (j & 1) + r;
-        s[e] = (kp >= key_lo) & (kp <= key_hi) ? s[e] : -INFINITY;
+        s[e] = ((kp >= key_lo) & (kp <= key_hi)) ? s[e] : -INFINITY;
     }
 }
 // Does any score exceed the running max by more than the margin? Scores are finite or

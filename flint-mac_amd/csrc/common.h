@@ -15,6 +15,7 @@ constexpr int GQA = N_HEAD / N_HEAD_KV;  // 8
 constexpr int Q_DIM = N_HEAD * HEAD_DIM;  // 4096
 constexpr int KV_DIM = N_HEAD_KV * HEAD_DIM;  // 512
 constexpr int QKV_DIM = Q_DIM + 2 * KV_DIM;  // 5120: one raw q|k|v row
+constexpr int N_EMBD = 2048;                  // hidden size (flint_config.h:12)
 constexpr float LOG2E = 1.4426950408889634f;
 
 // KV storage dtypes (values of flint_attn_layer.kv_dtype).

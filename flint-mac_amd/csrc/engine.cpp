@@ -19,6 +19,7 @@
 
 #include "../../include/capi.h"
 #include "../../include/flint_attn.h"
+#include "../../include/flint_proj.h"
 #include "common.h"
 #include "flint_attn_internal.h"
 
@@ -227,10 +228,107 @@ void prefill_impl(const flint_attn_layer *L, const float *qkv, int q_stride, int
     check(launch_prefill(P, L->kv_dtype, stream), "prefill launch");
 }
 
+// ---- attention projections (include/flint_proj.h) ----
+
+int64_t w_row_bytes(int type, int64_t k) {
+    int be = 0, bb = 0;
+    switch (type) {
+        case W_F32: be = 1, bb = 4; break;
+        case W_F16: case W_BF16: be = 1, bb = 2; break;
+        case W_Q8_0: be = 32, bb = 34; break;
+        case W_Q5_K: be = 256, bb = 176; break;
+        case W_Q6_K: be = 256, bb = 210; break;
+        case W_IQ4_XS: be = 256, bb = 136; break;
+        default: return -1;
+    }
+    if (k <= 0 || k % be || k % 32) return -1;
+    return k / be * bb;
+}
+
+bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
+
+void get_row_impl(int type, const void *w, int64_t k, int64_t row, float *out, hipStream_t stream) {
+    const int64_t rb = w_row_bytes(type, k);
+    if (rb < 0) throw Error("get_row: unsupported weight type or row length");
+    if (!w || !out) throw Error("get_row: NULL pointer");
+    if (row < 0) throw Error("get_row: negative row");
+    if (k > (int64_t)1 << 30) throw Error("get_row: row too long");
+    if (!aligned16(out)) throw Error("get_row: out must be 16-byte aligned");
+    if ((((uintptr_t)w + (uintptr_t)(row * rb)) & 1) != 0) throw Error("get_row: row data must be 2-byte aligned");
+    check(launch_get_row((const uint8_t *)w + row * rb, type, k, out, stream), "get_row launch");
+}
+
+// rows of k elements of one matvec tensor: 16-byte aligned rows are what the kernel reads
+void check_weight(const flint_weight *w, int64_t k, const char *name) {
+    if (!w || !w->data) throw Error(std::string(name) + ": NULL weight");
+    const int64_t rb = w_row_bytes(w->type, k);
+    if (rb < 0) throw Error(std::string(name) + ": unsupported weight type");
+    if (rb % 16 || !aligned16(w->data)) throw Error(std::string(name) + ": rows must be 16-byte aligned");
+}
+
+void qkv_proj_impl(const flint_weight *wq, const flint_weight *wk, const flint_weight *wv, const float *x,
+                   const float *attn_norm, float eps, float *qkv, hipStream_t stream) {
+    check_weight(wq, N_EMBD, "wq");
+    check_weight(wk, N_EMBD, "wk");
+    check_weight(wv, N_EMBD, "wv");
+    if (!x || !attn_norm || !qkv) throw Error("qkv_proj: NULL pointer");
+    if (!aligned16(x) || !aligned16(attn_norm)) throw Error("qkv_proj: x and attn_norm must be 16-byte aligned");
+    MatvecParams P{};
+    const flint_weight *ws[3] = {wq, wk, wv};
+    const int row0[3] = {0, Q_DIM, Q_DIM + KV_DIM};
+    for (int i = 0; i < 3; i++)
+        P.seg[i] = MatvecSeg{(const uint8_t *)ws[i]->data, ws[i]->type, row0[i], (int)w_row_bytes(ws[i]->type, N_EMBD)};
+    P.n_seg = 3;
+    P.n_rows = QKV_DIM;
+    P.x = x;
+    P.norm_w = attn_norm;
+    P.eps = eps;
+    P.y = qkv;
+    P.add = 0;
+    check(launch_matvec(P, N_EMBD, stream), "qkv_proj launch");
+}
+
+void o_proj_impl(const flint_weight *wo, const float *att, float *x, hipStream_t stream) {
+    check_weight(wo, Q_DIM, "wo");
+    if (!att || !x) throw Error("o_proj: NULL pointer");
+    if (!aligned16(att)) throw Error("o_proj: att must be 16-byte aligned");
+    MatvecParams P{};
+    P.seg[0] = MatvecSeg{(const uint8_t *)wo->data, wo->type, 0, (int)w_row_bytes(wo->type, Q_DIM)};
+    P.n_seg = 1;
+    P.n_rows = N_EMBD;
+    P.x = att;
+    P.y = x;
+    P.add = 1;
+    check(launch_matvec(P, Q_DIM, stream), "o_proj launch");
+}
+
 }  // namespace
 }  // namespace flint
 
 using namespace flint;
+
+extern "C" {
+
+int64_t flint_w_row_bytes(int32_t type, int64_t k) { return w_row_bytes(type, k); }
+
+int32_t flint_w_get_row(int32_t type, const void *w, int64_t k, int64_t row, float *out, void *stream, char *err,
+                        int32_t err_len) {
+    return guarded(err, err_len, [&] { get_row_impl(type, w, k, row, out, (hipStream_t)stream); });
+}
+
+int32_t flint_attn_qkv_proj(const flint_weight *wq, const flint_weight *wk, const flint_weight *wv, const float *x,
+                            const float *attn_norm, float rms_eps, float *qkv, void *stream, char *err,
+                            int32_t err_len) {
+    return guarded(err, err_len,
+                   [&] { qkv_proj_impl(wq, wk, wv, x, attn_norm, rms_eps, qkv, (hipStream_t)stream); });
+}
+
+int32_t flint_attn_o_proj(const flint_weight *wo, const float *att, float *x, void *stream, char *err,
+                          int32_t err_len) {
+    return guarded(err, err_len, [&] { o_proj_impl(wo, att, x, (hipStream_t)stream); });
+}
+
+}  // extern "C"
 
 // ---------------------------------------------------------------------------
 // engine object

@@ -58,4 +58,23 @@ struct PrefillParams {
 
 hipError_t launch_prefill(const PrefillParams &P, int dtype, hipStream_t stream);
 
+// Weight formats of the attention projections (ggml type ids, /root/reference/src/gguf.h:14-19)
+constexpr int W_F32 = 0, W_F16 = 1, W_Q8_0 = 8, W_Q5_K = 13, W_Q6_K = 14, W_IQ4_XS = 23, W_BF16 = 30;
+
+struct MatvecSeg {         // rows [row0, row0 + rows) of one launch come from one tensor
+    const uint8_t *w;      // its first row (16-byte aligned)
+    int type, row0, row_bytes;
+};
+struct MatvecParams {
+    MatvecSeg seg[3];
+    int n_seg, n_rows;
+    const float *x;        // [K] input
+    const float *norm_w;   // [K] RMSNorm gains applied to x first, or null
+    float eps;
+    float *y;              // [n_rows]: y = W x, or y += W x when add
+    int add;
+};
+hipError_t launch_get_row(const uint8_t *row, int type, int64_t k, float *out, hipStream_t stream);
+hipError_t launch_matvec(const MatvecParams &P, int k, hipStream_t stream);
+
 }  // namespace flint

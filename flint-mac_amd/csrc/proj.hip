@@ -1,0 +1,295 @@
+// Attention projections in the engine's GGUF weight formats, for gfx950:
+//   * get_row_kernel: one row dequantised to fp32 (Engine::debug_get_row,
+//     /root/reference/src/engine.mm:1370-1383; kernel k_get_row, fused.metal:589-600);
+//   * matvec_kernel: y = W x with 2048- or 4096-element rows, optionally on RMSNorm(x) * g
+//     (the q/k/v projections, engine.mm:728-732) or added to y (o_proj with the residual,
+//     engine.mm:811).
+//
+// Formats: ggml's block layouts (/root/reference/third_party/ggml/ggml-common.h), type ids
+// from /root/reference/src/gguf.h:14-19. Every row is cut into 32-element sub-blocks, the
+// unit all formats share: a q8_0 block, a half of a q5_K/iq4_xs 64-element pair, two q6_K
+// 16-element groups. Lane l of a wave owns sub-blocks l, l + 64, ..., so the 32 x values it
+// multiplies stay in its registers. Dequantisation repeats ggml's float operations in order
+// with contraction off, so get_row is bit-identical to dequantize_row_*
+// (/root/reference/src/ref/dequant_gen.c).
+//
+// Matvec layout (HBM-bound on the weight bytes): one wave per row. The wave reads its row
+// with 16-byte loads, coalesced, into an LDS area of its own; each lane then reads the bytes
+// of its sub-block from LDS at the alignment the format gives (q8_0 and q6_K blocks are only
+// 2-byte aligned), decodes 32 weights and accumulates their products with x in fp32; a
+// wave-wide sum gives y[row]. f32/f16/bf16 rows are read straight from HBM (64- or 128-byte
+// sub-blocks, aligned).
+#include <hip/hip_runtime.h>
+
+#include "common.h"
+#include "flint_attn_internal.h"
+
+namespace flint {
+
+__host__ __device__ constexpr int w_block_elems(int t) {
+    return t == W_F32 || t == W_F16 || t == W_BF16 ? 1 : t == W_Q8_0 ? 32
+         : t == W_Q5_K || t == W_Q6_K || t == W_IQ4_XS ? 256 : 0;
+}
+__host__ __device__ constexpr int w_block_bytes(int t) {
+    return t == W_F32 ? 4 : t == W_F16 || t == W_BF16 ? 2 : t == W_Q8_0 ? 34 : t == W_Q5_K ? 176
+         : t == W_Q6_K ? 210 : t == W_IQ4_XS ? 136 : 0;
+}
+
+__device__ inline float h2f(uint32_t h) { return (float)__builtin_bit_cast(_Float16, (uint16_t)h); }
+
+// iq4_nl code book (ggml-common.h:1120-1122) as int8 bytes, four to a word
+constexpr uint32_t IQ4_T0 = 0xbfad9881u, IQ4_T1 = 0xf6eaddcfu, IQ4_T2 = 0x26190d01u, IQ4_T3 = 0x71594535u;
+__device__ inline float iq4_value(uint32_t nib) {
+    const uint32_t sel = 0x0c0c0c00u | (nib & 7);  // byte nib&7 of the 8-byte half, upper bytes 0
+    const uint32_t b = nib & 8 ? __builtin_amdgcn_perm(IQ4_T3, IQ4_T2, sel) : __builtin_amdgcn_perm(IQ4_T1, IQ4_T0, sel);
+    return (float)(int8_t)b;
+}
+
+// byte i of a little-endian word array
+template <int N>
+__device__ inline uint32_t byte_of(const uint32_t (&w)[N], int i) { return (w[i >> 2] >> (8 * (i & 3))) & 0xff; }
+
+// The 32 weights of sub-block sb of a row whose bytes start at `row` (LDS or global; for
+// the quantised types the row start is 16-byte aligned). Float operations and their order
+// follow ggml's dequantize_row_* (dequant_gen.c:10-24, 50-106, 209-230); no contraction.
+__device__ inline void deq32(int type, const uint8_t *row, int sb, float (&w)[32]) {
+#pragma clang fp contract(off)
+    switch (type) {
+        case W_Q8_0: {  // y = q * d
+            const uint16_t *p = (const uint16_t *)(row + 34 * sb);
+            const float d = h2f(p[0]);
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const uint32_t v = p[1 + i];
+                w[2 * i] = (float)(int8_t)(v & 0xff) * d;
+                w[2 * i + 1] = (float)(int8_t)(v >> 8) * d;
+            }
+            break;
+        }
+        case W_Q5_K: {  // y = (d * sc) * (q4 + 16 h) - dmin * m
+            const uint8_t *blk = row + 176 * (sb >> 3);
+            const int j = sb & 7;
+            const uint32_t dm = *(const uint32_t *)blk;
+            const uint32_t s[3] = {((const uint32_t *)(blk + 4))[0], ((const uint32_t *)(blk + 4))[1],
+                                   ((const uint32_t *)(blk + 4))[2]};
+            // 6-bit scale and min of sub-block j (ggml's get_scale_min_k4, dequant_gen.c:1-8)
+            const uint32_t sc = j < 4 ? byte_of(s, j) & 63 : (byte_of(s, j + 4) & 15) | ((byte_of(s, j - 4) >> 6) << 4);
+            const uint32_t mn = j < 4 ? byte_of(s, j + 4) & 63 : (byte_of(s, j + 4) >> 4) | ((byte_of(s, j) >> 6) << 4);
+            const float d1 = h2f(dm & 0xffff) * (float)sc, m1 = h2f(dm >> 16) * (float)mn;
+            uint32_t qh[8], ql[8];
+            *(u32x4 *)&qh[0] = ((const u32x4 *)(blk + 16))[0];
+            *(u32x4 *)&qh[4] = ((const u32x4 *)(blk + 16))[1];
+            *(u32x4 *)&ql[0] = ((const u32x4 *)(blk + 48 + 32 * (j >> 1)))[0];
+            *(u32x4 *)&ql[4] = ((const u32x4 *)(blk + 48 + 32 * (j >> 1)))[1];
+            const int ls = 4 * (j & 1);
+#pragma unroll
+            for (int i = 0; i < 32; i++) {
+                const uint32_t q = ((byte_of(ql, i) >> ls) & 15) + (((byte_of(qh, i) >> j) & 1) << 4);
+                const float dq = d1 * (float)q;
+                w[i] = dq - m1;
+            }
+            break;
+        }
+        case W_Q6_K: {  // y = (d * sc) * (q6 - 32); the block is 2-byte aligned
+            const uint8_t *blk = row + 210 * (sb >> 3);
+            const int j = sb & 7, n = j >> 2, g = j & 3;
+            const uint16_t *ql = (const uint16_t *)(blk + 64 * n + 32 * (g & 1));
+            const uint16_t *qh = (const uint16_t *)(blk + 128 + 32 * n);
+            const uint32_t scw = *(const uint16_t *)(blk + 192 + 8 * n + 2 * g);  // scales 8n+2g, 8n+2g+1
+            const float d = h2f(*(const uint16_t *)(blk + 208));
+            const float ds0 = d * (float)(int8_t)(scw & 0xff), ds1 = d * (float)(int8_t)(scw >> 8);
+            const int lsh = 4 * (g >> 1), hsh = 2 * g;
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const uint32_t lo = ql[i], hi = qh[i];
+#pragma unroll
+                for (int b = 0; b < 2; b++) {
+                    const int e = 2 * i + b;
+                    const int q = (int)((((lo >> (8 * b)) >> lsh) & 15) | ((((hi >> (8 * b)) >> hsh) & 3) << 4)) - 32;
+                    w[e] = (e < 16 ? ds0 : ds1) * (float)q;
+                }
+            }
+            break;
+        }
+        case W_IQ4_XS: {  // y = (d * (ls - 32)) * table[nibble]; the block is 8-byte aligned
+            const uint8_t *blk = row + 136 * (sb >> 3);
+            const int ib = sb & 7;
+            const uint2 hdr = *(const uint2 *)blk;  // d | scales_h | scales_l[4]
+            const uint32_t ls = ((hdr.y >> (8 * (ib >> 1) + 4 * (ib & 1))) & 15) | (((hdr.x >> (16 + 2 * ib)) & 3) << 4);
+            const float dl = h2f(hdr.x & 0xffff) * (float)((int)ls - 32);
+            const uint2 q0 = *(const uint2 *)(blk + 8 + 16 * ib), q1 = *(const uint2 *)(blk + 16 + 16 * ib);
+            const uint32_t qs[4] = {q0.x, q0.y, q1.x, q1.y};
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const uint32_t v = byte_of(qs, i);
+                w[i] = dl * iq4_value(v & 15);
+                w[i + 16] = dl * iq4_value(v >> 4);
+            }
+            break;
+        }
+        case W_F16:
+        case W_BF16: {
+            uint32_t h[16];
+#pragma unroll
+            for (int k = 0; k < 4; k++) *(u32x4 *)&h[4 * k] = ((const u32x4 *)(row + 64 * sb))[k];
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                if (type == W_F16) {
+                    w[2 * i] = h2f(h[i] & 0xffff);
+                    w[2 * i + 1] = h2f(h[i] >> 16);
+                } else {
+                    w[2 * i] = __uint_as_float(h[i] << 16);
+                    w[2 * i + 1] = __uint_as_float(h[i] & 0xffff0000u);
+                }
+            }
+            break;
+        }
+        default: {  // W_F32
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const f32x4 v = ((const f32x4 *)(row + 128 * sb))[k];
+                w[4 * k] = v[0];
+                w[4 * k + 1] = v[1];
+                w[4 * k + 2] = v[2];
+                w[4 * k + 3] = v[3];
+            }
+        }
+    }
+}
+
+__device__ inline bool w_is_float(int t) { return t == W_F32 || t == W_F16 || t == W_BF16; }
+
+// ---------------------------------------------------------------------------
+// get_row: wave c dequantises sub-blocks 64c .. 64c+63 of the row. Its bytes start on a
+// block boundary; they are staged through LDS with 2-byte loads (any row alignment that
+// the block size allows).
+constexpr int GR_STAGE = 64 * 32 * 4;  // bytes of 64 f32 sub-blocks, the largest chunk
+__global__ __launch_bounds__(64) void get_row_kernel(const uint8_t *__restrict__ row, int type, int n_sub,
+                                                     float *__restrict__ out) {
+    __shared__ __align__(16) uint8_t stage[GR_STAGE];
+    const int lane = threadIdx.x, c = blockIdx.x;
+    const int sub0 = 64 * c, nsub = min(64, n_sub - sub0);
+    const int be = w_block_elems(type), bb = w_block_bytes(type);
+    const size_t off = (size_t)sub0 * 32 / be * bb;
+    const int nbytes = nsub * 32 / be * bb;  // chunks are whole blocks (64 is a multiple of 8)
+    const uint16_t *src = (const uint16_t *)(row + off);
+    uint16_t *dst = (uint16_t *)stage;
+    for (int i = lane; i < nbytes / 2; i += 64) dst[i] = src[i];
+    __syncthreads();
+    if (lane < nsub) {
+        float w[32];
+        deq32(type, stage, lane, w);
+        f32x4 *o = (f32x4 *)(out + 32 * (size_t)(sub0 + lane));
+#pragma unroll
+        for (int k = 0; k < 8; k++) o[k] = f32x4{w[4 * k], w[4 * k + 1], w[4 * k + 2], w[4 * k + 3]};
+    }
+}
+
+// ---------------------------------------------------------------------------
+// matvec
+constexpr int MV_WAVES = 4;  // rows (waves) per workgroup
+
+__device__ inline double wave_sum_f64(double v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+    return v;
+}
+
+template <int K>
+__global__ __launch_bounds__(64 * MV_WAVES) void matvec_kernel(const MatvecParams P) {
+    constexpr int SUBS = K / 32 / 64;              // sub-blocks per lane
+    constexpr int QBYTES = K / 32 * 34;            // largest quantised row (q8_0)
+    constexpr int UNITS = (QBYTES / 16 + 63) / 64;  // 16-byte loads per lane for it
+    __shared__ __align__(16) uint8_t stage[MV_WAVES][QBYTES];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int row = blockIdx.x * MV_WAVES + wave;
+    if (row >= P.n_rows) return;  // whole waves; no workgroup barrier below
+    int s = 0;
+    while (s + 1 < P.n_seg && row >= P.seg[s + 1].row0) s++;
+    const MatvecSeg S = P.seg[s];
+    const uint8_t *wrow = S.w + (size_t)(row - S.row0) * S.row_bytes;
+    const bool fl = w_is_float(S.type);
+
+    // x (and the norm gains) first: the norm waits for them, not for the row
+    float xv[SUBS][32];
+#pragma unroll
+    for (int i = 0; i < SUBS; i++)
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const f32x4 v = *(const f32x4 *)(P.x + 32 * (lane + 64 * i) + 4 * k);
+            xv[i][4 * k] = v[0], xv[i][4 * k + 1] = v[1], xv[i][4 * k + 2] = v[2], xv[i][4 * k + 3] = v[3];
+        }
+    float gv[SUBS][32];
+    if (P.norm_w) {
+#pragma unroll
+        for (int i = 0; i < SUBS; i++)
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const f32x4 v = *(const f32x4 *)(P.norm_w + 32 * (lane + 64 * i) + 4 * k);
+                gv[i][4 * k] = v[0], gv[i][4 * k + 1] = v[1], gv[i][4 * k + 2] = v[2], gv[i][4 * k + 3] = v[3];
+            }
+    }
+    u32x4 u[UNITS];
+    const int n_units = S.row_bytes >> 4;
+    if (!fl) {
+#pragma unroll
+        for (int k = 0; k < UNITS; k++) {
+            const int idx = lane + 64 * k;
+            if (idx < n_units) u[k] = ((const u32x4 *)wrow)[idx];
+        }
+    }
+    if (P.norm_w) {
+        // RMSNorm as the CPU reference (ref_model.cpp:45-50): double sum of squares, float
+        // scale, (x * scale) * g
+        double ss = 0;
+#pragma unroll
+        for (int i = 0; i < SUBS; i++)
+#pragma unroll
+            for (int e = 0; e < 32; e++) ss += (double)xv[i][e] * xv[i][e];
+        ss = wave_sum_f64(ss);
+        const float scale = 1.0f / sqrtf((float)(ss / K) + P.eps);
+#pragma unroll
+        for (int i = 0; i < SUBS; i++)
+#pragma unroll
+            for (int e = 0; e < 32; e++) xv[i][e] = xv[i][e] * scale * gv[i][e];
+    }
+    const uint8_t *src = wrow;
+    if (!fl) {
+#pragma unroll
+        for (int k = 0; k < UNITS; k++) {
+            const int idx = lane + 64 * k;
+            if (idx < n_units) ((u32x4 *)stage[wave])[idx] = u[k];
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        src = stage[wave];
+    }
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < SUBS; i++) {
+        float w[32];
+        deq32(S.type, src, lane + 64 * i, w);
+#pragma unroll
+        for (int e = 0; e < 32; e++) acc = fmaf(w[e], xv[i][e], acc);
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) P.y[row] = P.add ? P.y[row] + acc : acc;
+}
+
+hipError_t launch_get_row(const uint8_t *row, int type, int64_t k, float *out, hipStream_t stream) {
+    const int n_sub = (int)(k / 32);
+    hipLaunchKernelGGL(get_row_kernel, dim3((n_sub + 63) / 64), dim3(64), 0, stream, row, type, n_sub, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_matvec(const MatvecParams &P, int k, hipStream_t stream) {
+    const dim3 grid((P.n_rows + MV_WAVES - 1) / MV_WAVES), block(64 * MV_WAVES);
+    if (k == 2048)
+        hipLaunchKernelGGL(matvec_kernel<2048>, grid, block, 0, stream, P);
+    else
+        hipLaunchKernelGGL(matvec_kernel<4096>, grid, block, 0, stream, P);
+    return hipGetLastError();
+}
+
+}  // namespace flint

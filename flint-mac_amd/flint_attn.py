@@ -42,6 +42,15 @@ class LayerDesc(ctypes.Structure):
     ]
 
 
+class WeightDesc(ctypes.Structure):
+    """flint_weight (include/flint_proj.h)."""
+    _fields_ = [("data", ctypes.c_void_p), ("type", ctypes.c_int32)]
+
+
+# ggml type ids of the weight formats (include/flint_proj.h)
+W_TYPES = {"f32": 0, "f16": 1, "q8_0": 8, "q5_K": 13, "q6_K": 14, "iq4_xs": 23, "bf16": 30}
+N_EMBD = 2048
+
 _lib = None
 _vp, _i32, _i64, _f32 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_float
 _cp = ctypes.c_char_p
@@ -63,6 +72,10 @@ _SIGS = {
     "flint_attn_engine_decode": (_i32, [_vp, _i32, _vp, _vp, _i32, _vp, _cp, _i32]),
     "flint_attn_engine_prefill": (_i32, [_vp, _i32, _vp, _i32, _i32, _vp, _vp, _cp, _i32]),
     "flint_attn_engine_debug_attn": (_i32, [_vp, _i32, _f32p, _i32, _i32, _f32p, _cp, _i32]),
+    "flint_w_row_bytes": (_i64, [_i32, _i64]),
+    "flint_w_get_row": (_i32, [_i32, _vp, _i64, _i64, _vp, _vp, _cp, _i32]),
+    "flint_attn_qkv_proj": (_i32, [ctypes.POINTER(WeightDesc)] * 3 + [_vp, _vp, _f32, _vp, _vp, _cp, _i32]),
+    "flint_attn_o_proj": (_i32, [ctypes.POINTER(WeightDesc), _vp, _vp, _vp, _cp, _i32]),
     "flint_open": (_vp, [_vp, _cp, _i32]),
     "flint_close": (None, [_vp]),
     "flint_n_ctx": (_i32, [_vp]),
@@ -193,6 +206,34 @@ class KVLayer:
             T = qkv.shape[0]
         _call(lib().flint_attn_prefill, ctypes.byref(self.desc), _ptr(qkv), q_stride, p0, T, _ptr(att),
               _stream(stream))
+
+
+def row_bytes(wtype, k):
+    """Bytes of a row of k elements of a weight format, or -1 (flint_w_row_bytes)."""
+    return int(lib().flint_w_row_bytes(W_TYPES[wtype], k))
+
+
+def get_row(wtype, w, k, row, out, stream=None):
+    """Dequantise row `row` of the weight bytes `w` (a uint8 device tensor) into out [k] fp32
+    (flint_w_get_row; the reference's Engine::debug_get_row)."""
+    _call(lib().flint_w_get_row, W_TYPES[wtype], _ptr(w), k, row, _ptr(out), _vp(_stream(stream)))
+
+
+def _wdesc(w):
+    data, wtype = w
+    return ctypes.byref(WeightDesc(data.data_ptr(), W_TYPES[wtype]))
+
+
+def qkv_proj(wq, wk, wv, x, attn_norm, qkv, rms_eps=1e-6, stream=None):
+    """qkv [5120] = [Wq; Wk; Wv] RMSNorm(x) * attn_norm (flint_attn_qkv_proj). Each weight is a
+    (uint8 device tensor, type name) pair."""
+    _call(lib().flint_attn_qkv_proj, _wdesc(wq), _wdesc(wk), _wdesc(wv), _ptr(x), _ptr(attn_norm), rms_eps,
+          _ptr(qkv), _vp(_stream(stream)))
+
+
+def o_proj(wo, att, x, stream=None):
+    """x [2048] += Wo att (flint_attn_o_proj); wo is a (uint8 device tensor, type name) pair."""
+    _call(lib().flint_attn_o_proj, _wdesc(wo), _ptr(att), _ptr(x), _vp(_stream(stream)))
 
 
 def sync():

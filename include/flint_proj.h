@@ -1,0 +1,80 @@
+/*
+ * flint attention projections on MI355X (gfx950): the attention block's matvecs in the
+ * engine's GGUF weight formats, and the row dequantisation the reference tests them with.
+ * Same conventions as flint_attn.h: device pointers, `stream` a hipStream_t as void*
+ * (NULL = null stream), 0 / -1 with a NUL-terminated message in err[err_len].
+ *
+ * Weights are GGUF tensors as stored on disk: row-major, ggml block layouts
+ * (/root/reference/third_party/ggml/ggml-common.h: block_q8_0 :251-256, block_q5_K
+ * :343-356, block_q6_K :362-368, block_iq4_xs :454-460), rows of K elements in
+ * K / block_elems blocks. The type ids are ggml's (/root/reference/src/gguf.h:14-19).
+ * The quantised types are the ones the reference builds its attention kernels for
+ * (/root/reference/src/metal/fused.metal:641); f32, f16 and bf16 rows are accepted too.
+ */
+#ifndef FLINT_PROJ_H
+#define FLINT_PROJ_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FLINT_W_F32 0
+#define FLINT_W_F16 1
+#define FLINT_W_Q8_0 8
+#define FLINT_W_Q5_K 13
+#define FLINT_W_Q6_K 14
+#define FLINT_W_IQ4_XS 23
+#define FLINT_W_BF16 30
+
+#define FLINT_N_EMBD 2048 /* hidden size (/root/reference/src/metal/flint_config.h:12) */
+
+/* One weight tensor: device data (16-byte aligned) and its ggml type id. */
+typedef struct {
+    const void *data;
+    int32_t type;
+} flint_weight;
+
+/* Bytes of one row of k elements, or -1 if the type is unsupported or k is not a whole
+ * number of blocks (the reference's Tensor::row_bytes, /root/reference/src/gguf.h:38). */
+int64_t flint_w_row_bytes(int32_t type, int64_t k);
+
+/*
+ * Row `row` of a weight tensor with rows of k elements, dequantised to fp32 into out[k]
+ * (device, 16-byte aligned). Bit-identical to ggml's CPU dequantize_row_* (the reference's
+ * check-deq compares its GPU rows with those: /root/reference/src/main.mm:27-48).
+ * Replaces Engine::debug_get_row (/root/reference/src/engine.h:37, engine.mm:1370-1383;
+ * kernel k_get_row, /root/reference/src/metal/fused.metal:589-600).
+ */
+int32_t flint_w_get_row(int32_t type, const void *w, int64_t k, int64_t row, float *out, void *stream,
+                        char *err, int32_t err_len);
+
+/*
+ * The attention block's input side for one token: xn = RMSNorm(x) * attn_norm, then
+ * qkv[0:4096] = Wq xn, qkv[4096:4608] = Wk xn, qkv[4608:5120] = Wv xn.
+ *   x: device [2048], attn_norm: device [2048] gains, qkv: device [5120] (the raw q|k|v
+ *   row flint_attn_decode takes). Wq/Wk/Wv rows have 2048 elements (4096 / 512 / 512 rows);
+ *   each may have its own type; data 16-byte aligned.
+ * Replaces enc_rmsnorm + three enc_mv at /root/reference/src/engine.mm:728-732 (kernels
+ * k_rmsnorm / k_mv, /root/reference/src/metal/flint.metal:48-72, 217-240; the fused
+ * variant k_qkv, fused.metal:215-232); CPU reference ref_model.cpp:107-110.
+ */
+int32_t flint_attn_qkv_proj(const flint_weight *wq, const flint_weight *wk, const flint_weight *wv, const float *x,
+                            const float *attn_norm, float rms_eps, float *qkv, void *stream, char *err,
+                            int32_t err_len);
+
+/*
+ * The attention block's output side: x[r] += sum_i Wo[r][i] * att[i] for r < 2048
+ * (the residual add).  att: device [4096]; x: device [2048], updated in place.
+ * Replaces enc_mv(L.o, att, x, add = true) at /root/reference/src/engine.mm:811 (k_mv with
+ * add, flint.metal:48-72; fused variant k_mv_res, fused.metal:357-378); CPU reference
+ * ref_model.cpp:150-151.
+ */
+int32_t flint_attn_o_proj(const flint_weight *wo, const float *att, float *x, void *stream, char *err,
+                          int32_t err_len);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

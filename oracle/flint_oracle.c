@@ -261,3 +261,168 @@ void fo_prefill(const fo_layer *L, const float *qkv, int q_stride, int p0, int T
     for (int t = 0; t < T; t++)
         fo_decode_step(L, qkv + (size_t)t * q_stride, p0 + t, K, V, att + (size_t)t * FO_Q_DIM, n_threads);
 }
+
+/* ---- weight formats of the attention projections ----
+ * Restated from ggml's published block formats and dequantisation (the reference
+ * vendors them: /root/reference/third_party/ggml/ggml-common.h block_q8_0 :251-256,
+ * block_q5_K :343-356, block_q6_K :362-368, block_iq4_xs :454-460, kvalues_iq4nl
+ * :1120-1122; dequantize_row_* in /root/reference/src/ref/dequant_gen.c:10-24, 50-106,
+ * 209-230), with each float operation in the reference's order and no contraction, so
+ * the values are bit-identical. Row dispatch as /root/reference/src/ref/dequant_row.cpp:19-43. */
+
+static float half_bits_to_float(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h >> 15) << 31;
+    const int exp = (h >> 10) & 0x1f;
+    uint32_t mant = h & 0x3ff, bits;
+    if (exp == 0x1f) {
+        bits = sign | 0x7f800000u | (mant << 13); /* inf / nan */
+    } else if (exp != 0) {
+        bits = sign | ((uint32_t)(exp - 15 + 127) << 23) | (mant << 13);
+    } else if (mant == 0) {
+        bits = sign;
+    } else { /* subnormal: mant * 2^-24, exact in float */
+        int e = -14;
+        while (!(mant & 0x400)) {
+            mant <<= 1;
+            e--;
+        }
+        bits = sign | ((uint32_t)(e + 127) << 23) | ((mant & 0x3ff) << 13);
+    }
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+static uint16_t rd16(const unsigned char *p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+
+static const signed char iq4nl_values[16] = {-127, -104, -83, -65, -49, -35, -22, -10,
+                                             1,    13,   25,  38,  53,  69,  89,  113};
+
+long fo_block_elems(int type) {
+    switch (type) {
+        case FO_W_F32: case FO_W_F16: case FO_W_BF16: return 1;
+        case FO_W_Q8_0: return 32;
+        case FO_W_Q5_K: case FO_W_Q6_K: case FO_W_IQ4_XS: return 256;
+        default: return -1;
+    }
+}
+
+long fo_block_bytes(int type) {
+    switch (type) {
+        case FO_W_F32: return 4;
+        case FO_W_F16: case FO_W_BF16: return 2;
+        case FO_W_Q8_0: return 34;
+        case FO_W_Q5_K: return 176;
+        case FO_W_Q6_K: return 210;
+        case FO_W_IQ4_XS: return 136;
+        default: return -1;
+    }
+}
+
+long fo_row_bytes(int type, long k) {
+    const long be = fo_block_elems(type);
+    if (be <= 0 || k <= 0 || k % be) return -1;
+    return k / be * fo_block_bytes(type);
+}
+
+/* the 6-bit scale and min of sub-block j (0..7) of a K-quant super-block's 12 scale bytes */
+static void kquant_scale_min(const unsigned char *s, int j, int *sc, int *m) {
+    if (j < 4) {
+        *sc = s[j] & 63;
+        *m = s[j + 4] & 63;
+    } else {
+        *sc = (s[j + 4] & 0xf) | ((s[j - 4] >> 6) << 4);
+        *m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
+    }
+}
+
+int fo_dequant_row(int type, const void *row_, long k, float *y) {
+    const unsigned char *row = (const unsigned char *)row_;
+    if (fo_row_bytes(type, k) < 0) return -1;
+    switch (type) {
+        case FO_W_F32: memcpy(y, row, (size_t)k * 4); return 0;
+        case FO_W_F16:
+            for (long i = 0; i < k; i++) y[i] = half_bits_to_float(rd16(row + 2 * i));
+            return 0;
+        case FO_W_BF16:
+            for (long i = 0; i < k; i++) {
+                const uint32_t u = (uint32_t)rd16(row + 2 * i) << 16;
+                memcpy(&y[i], &u, 4);
+            }
+            return 0;
+        case FO_W_Q8_0: /* y = q * d */
+            for (long b = 0; b < k / 32; b++) {
+                const unsigned char *blk = row + 34 * b;
+                const float d = half_bits_to_float(rd16(blk));
+                for (int i = 0; i < 32; i++) y[32 * b + i] = (float)(signed char)blk[2 + i] * d;
+            }
+            return 0;
+        case FO_W_Q5_K: /* 8 sub-blocks of 32: y = (d * sc) * q5 - dmin * m */
+            for (long b = 0; b < k / 256; b++) {
+                const unsigned char *blk = row + 176 * b;
+                const float d = half_bits_to_float(rd16(blk)), dmin = half_bits_to_float(rd16(blk + 2));
+                const unsigned char *sc = blk + 4, *qh = blk + 16, *qs = blk + 48;
+                for (int j = 0; j < 8; j++) {
+                    int s, m;
+                    kquant_scale_min(sc, j, &s, &m);
+                    const float d1 = d * (float)s, m1 = dmin * (float)m;
+                    const unsigned char *ql = qs + 32 * (j / 2);
+                    for (int i = 0; i < 32; i++) {
+                        const int q = ((j & 1) ? ql[i] >> 4 : ql[i] & 0xf) + (((qh[i] >> j) & 1) ? 16 : 0);
+                        const float dq = d1 * (float)q;
+                        y[256 * b + 32 * j + i] = dq - m1;
+                    }
+                }
+            }
+            return 0;
+        case FO_W_Q6_K: /* 16 sub-blocks of 16: y = (d * sc) * (q6 - 32) */
+            for (long b = 0; b < k / 256; b++) {
+                const unsigned char *blk = row + 210 * b;
+                const unsigned char *ql = blk, *qh = blk + 128;
+                const signed char *sc = (const signed char *)(blk + 192);
+                const float d = half_bits_to_float(rd16(blk + 208));
+                for (int e = 0; e < 256; e++) {
+                    const int n = e / 128, g = (e % 128) / 32, l = e % 32;
+                    const unsigned char lo = ql[64 * n + l + 32 * (g & 1)];
+                    const int q = (((g < 2) ? lo & 0xf : lo >> 4) | (((qh[32 * n + l] >> (2 * g)) & 3) << 4)) - 32;
+                    const float ds = d * (float)sc[8 * n + l / 16 + 2 * g];
+                    y[256 * b + e] = ds * (float)q;
+                }
+            }
+            return 0;
+        case FO_W_IQ4_XS: /* 8 sub-blocks of 32: y = (d * (ls - 32)) * table[nibble] */
+            for (long b = 0; b < k / 256; b++) {
+                const unsigned char *blk = row + 136 * b;
+                const float d = half_bits_to_float(rd16(blk));
+                const uint16_t sh = rd16(blk + 2);
+                const unsigned char *sl = blk + 4, *qs = blk + 8;
+                for (int ib = 0; ib < 8; ib++) {
+                    const int ls = ((sl[ib / 2] >> (4 * (ib % 2))) & 0xf) | (((sh >> (2 * ib)) & 3) << 4);
+                    const float dl = d * (float)(ls - 32);
+                    for (int j = 0; j < 16; j++) {
+                        y[256 * b + 32 * ib + j] = dl * (float)iq4nl_values[qs[16 * ib + j] & 0xf];
+                        y[256 * b + 32 * ib + j + 16] = dl * (float)iq4nl_values[qs[16 * ib + j] >> 4];
+                    }
+                }
+            }
+            return 0;
+    }
+    return -1;
+}
+
+/* y[r] = sum_i W[r][i] * x[i] with a double accumulator over the dequantised row
+ * (RefModel::matvec, /root/reference/src/ref/ref_model.cpp:74-93) */
+int fo_matvec(int type, const void *w, long k, long n_rows, const float *x, float *y) {
+    const long rb = fo_row_bytes(type, k);
+    if (rb < 0) return -1;
+    float *row = (float *)malloc((size_t)k * sizeof(float));
+    if (!row) return -1;
+    for (long r = 0; r < n_rows; r++) {
+        fo_dequant_row(type, (const unsigned char *)w + r * rb, k, row);
+        double acc = 0;
+        for (long i = 0; i < k; i++) acc += (double)row[i] * x[i];
+        y[r] = (float)acc;
+    }
+    free(row);
+    return 0;
+}

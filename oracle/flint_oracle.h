@@ -31,6 +31,13 @@
  *                       reference RefModel (bit-exact, fp32 storage)
  *   fo_attend_split     equals fo_attend for n_split in {1, 2, 16, 32, 64}
  *   fo_slot/fo_first_key brute force over pos in [0, 4096) against a linear history
+ *   fo_dequant_row      bit-exact against ggml's dequantize_row_* compiled from the reference's
+ *                       vendored sources (oracle/_ref) on random blocks, and against the
+ *                       committed fixtures tests/golden/weight_rows.npz made from it; f16/bf16
+ *                       against numpy / bit shifts; closed forms (all-zero scales give 0,
+ *                       q8_0 with d = 1 gives the int8 values)
+ *   fo_matvec           one-hot rows select x exactly; equals a float64 numpy product of
+ *                       fo_dequant_row's rows; linearity in x
  */
 #ifndef FLINT_ORACLE_H
 #define FLINT_ORACLE_H
@@ -87,6 +94,18 @@ void fo_decode_step(const fo_layer *L, const float *qkv, int pos, float *K, floa
  * identical to T decode steps. att is [T][4096]. */
 void fo_prefill(const fo_layer *L, const float *qkv, int q_stride, int p0, int T, float *K, float *V,
                 float *att, int n_threads);
+
+/* Weight formats of the attention projections: ggml type ids
+ * (/root/reference/src/gguf.h:14-19). fo_row_bytes is -1 for an unsupported type or
+ * a k that is not a whole number of blocks. */
+enum { FO_W_F32 = 0, FO_W_F16 = 1, FO_W_Q8_0 = 8, FO_W_Q5_K = 13, FO_W_Q6_K = 14, FO_W_IQ4_XS = 23, FO_W_BF16 = 30 };
+long fo_block_elems(int type);
+long fo_block_bytes(int type);
+long fo_row_bytes(int type, long k);
+/* One row of k elements to fp32 (0 / -1), bit-identical to ggml's dequantize_row_*. */
+int fo_dequant_row(int type, const void *row, long k, float *out);
+/* y = W x over n_rows rows, double accumulation per row (0 / -1). */
+int fo_matvec(int type, const void *w, long k, long n_rows, const float *x, float *y);
 
 #ifdef __cplusplus
 }

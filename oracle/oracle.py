@@ -72,6 +72,13 @@ def lib():
         L.fo_decode_step.argtypes = [lp, _f32p, ctypes.c_int, _f32p, _f32p, _f32p, ctypes.c_int]
         L.fo_prefill.argtypes = [lp, _f32p, ctypes.c_int, ctypes.c_int, ctypes.c_int, _f32p, _f32p, _f32p,
                                  ctypes.c_int]
+        for f in ("fo_block_elems", "fo_block_bytes"):
+            getattr(L, f).restype = ctypes.c_long
+            getattr(L, f).argtypes = [ctypes.c_int]
+        L.fo_row_bytes.restype = ctypes.c_long
+        L.fo_row_bytes.argtypes = [ctypes.c_int, ctypes.c_long]
+        L.fo_dequant_row.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_long, _f32p]
+        L.fo_matvec.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_long, ctypes.c_long, _f32p, _f32p]
         _lib = L
     return _lib
 
@@ -177,3 +184,86 @@ def prefill(layer, qkv, p0, K, V, n_threads=1):
     att = np.empty((T, Q_DIM), np.float32)
     lib().fo_prefill(layer.ref, _p(qkv), QKV_DIM, int(p0), int(T), _p(K), _p(V), _p(att), int(n_threads))
     return att
+
+
+# ---- weight formats (ggml type ids) ----
+W_TYPES = {"f32": 0, "f16": 1, "q8_0": 8, "q5_K": 13, "q6_K": 14, "iq4_xs": 23, "bf16": 30}
+
+
+def row_bytes(wtype, k):
+    return int(lib().fo_row_bytes(W_TYPES[wtype], k))
+
+
+def dequant_rows(wtype, data, k):
+    """All rows of a [n_rows][row_bytes] uint8 array as float32 [n_rows][k]."""
+    rb = row_bytes(wtype, k)
+    assert rb > 0 and data.dtype == np.uint8 and data.size % rb == 0
+    data = np.ascontiguousarray(data).reshape(-1, rb)
+    out = np.empty((data.shape[0], k), np.float32)
+    for r in range(data.shape[0]):
+        assert lib().fo_dequant_row(W_TYPES[wtype], data[r].ctypes.data, k, _p(out[r])) == 0
+    return out
+
+
+def matvec(wtype, data, k, x):
+    rb = row_bytes(wtype, k)
+    data = np.ascontiguousarray(data)
+    n = data.size // rb
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty(n, np.float32)
+    assert lib().fo_matvec(W_TYPES[wtype], data.ctypes.data, k, n, _p(x), _p(y)) == 0
+    return y
+
+
+REF_DEQUANT = os.path.join(HERE, "_ref", "libref_dequant.so")
+_ref_deq = None
+
+
+def ref_dequant_rows(wtype, data, k):
+    """The reference's own ggml dequantize_row_* (oracle/_ref, built from /root/reference);
+    None when that build is absent. Only the quantised types (f32/f16/bf16 are plain casts
+    in the reference, dequant_row.cpp:23-33)."""
+    global _ref_deq
+    if not os.path.exists(REF_DEQUANT):
+        return None
+    if _ref_deq is None:
+        _ref_deq = ctypes.CDLL(REF_DEQUANT)
+        for t in ("q8_0", "q5_K", "q6_K", "iq4_xs"):
+            getattr(_ref_deq, "dequantize_row_" + t).argtypes = [ctypes.c_void_p, _f32p, ctypes.c_int64]
+    rb = row_bytes(wtype, k)
+    data = np.ascontiguousarray(data).reshape(-1, rb)
+    out = np.empty((data.shape[0], k), np.float32)
+    fn = getattr(_ref_deq, "dequantize_row_" + wtype)
+    for r in range(data.shape[0]):
+        fn(data[r].ctypes.data, _p(out[r]), k)
+    return out
+
+
+def random_blocks(wtype, n_rows, k, rng):
+    """Random rows of a block format: every byte random except the fp16 scales, which are
+    finite halves of moderate size (as quantisers write them)."""
+    rb = row_bytes(wtype, k)
+    data = rng.integers(0, 256, size=(n_rows, rb), dtype=np.uint8)
+    nb = k // int(lib().fo_block_elems(W_TYPES[wtype]))
+    bb = int(lib().fo_block_bytes(W_TYPES[wtype]))
+    def put_half(off, scale):
+        h = (rng.standard_normal((n_rows, nb)) * scale).astype(np.float16).view(np.uint8).reshape(n_rows, nb, 2)
+        blocks = data.reshape(n_rows, nb, bb)
+        blocks[:, :, off:off + 2] = h
+    if wtype == "q8_0":
+        put_half(0, 0.01)
+    elif wtype == "q5_K":
+        put_half(0, 0.002)
+        put_half(2, 0.002)
+    elif wtype == "q6_K":
+        put_half(208, 0.002)
+    elif wtype == "iq4_xs":
+        put_half(0, 0.001)
+    elif wtype in ("f16", "bf16"):
+        v = (rng.standard_normal((n_rows, k)) * 0.05).astype(np.float32)
+        if wtype == "f16":
+            return v.astype(np.float16).view(np.uint8).reshape(n_rows, rb)
+        return (v.view(np.uint32) >> 16).astype(np.uint16).view(np.uint8).reshape(n_rows, rb)
+    elif wtype == "f32":
+        return (rng.standard_normal((n_rows, k)) * 0.05).astype(np.float32).view(np.uint8).reshape(n_rows, rb)
+    return data

@@ -1,0 +1,142 @@
+"""GPU parity of the attention projections in the engine's weight formats
+(include/flint_proj.h, flint-mac_amd/csrc/proj.hip) against the CPU oracle:
+  * get_row bit-identical to fo_dequant_row (itself bit-identical to the reference's ggml
+    dequantize_row_*), the reference's check-deq contract (/root/reference/src/main.mm:27-48,
+    which allows 1e-5);
+  * the q/k/v projection with the attention RMSNorm, and o_proj with the residual add, within
+    fp32 reassociation of the oracle's double-accumulated matvec (ref_model.cpp:74-93, 107-110,
+    150-151).
+"""
+import numpy as np
+import pytest
+
+import flint_attn as fa
+import oracle
+
+pytestmark = pytest.mark.gpu
+QUANT = ("q8_0", "q5_K", "q6_K", "iq4_xs")
+ALL = QUANT + ("f32", "f16", "bf16")
+
+
+def _dev(a, cuda):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).to(cuda)
+
+
+@pytest.mark.parametrize("wtype", ALL)
+@pytest.mark.parametrize("k", [2048, 4096, 768])
+def test_get_row_bit_exact(cuda, wtype, k):
+    import torch
+    if oracle.row_bytes(wtype, k) < 0:
+        pytest.skip("k is not a whole number of blocks")
+    rng = np.random.default_rng(k * 7 + len(wtype))
+    rows = oracle.random_blocks(wtype, 5, k, rng)
+    want = oracle.dequant_rows(wtype, rows, k)
+    w = _dev(rows, cuda)
+    out = torch.empty(k, dtype=torch.float32, device=cuda)
+    for r in range(5):
+        out.fill_(float("nan"))
+        fa.get_row(wtype, w, k, r, out)
+        torch.cuda.synchronize()
+        got = out.cpu().numpy()
+        assert np.array_equal(got.view(np.uint32), want[r].view(np.uint32)), (wtype, k, r)
+
+
+def test_get_row_golden_rows(cuda):
+    """The committed reference rows (tests/golden/weight_rows.npz, 512 elements: one wave with
+    16 sub-blocks), straight against the reference's float bits."""
+    import os
+    import torch
+    z = np.load(os.path.join(os.path.dirname(__file__), "golden", "weight_rows.npz"))
+    out = torch.empty(512, dtype=torch.float32, device=cuda)
+    for t in QUANT:
+        w = _dev(z[t + "_rows"], cuda)
+        for r in range(z[t + "_rows"].shape[0]):
+            fa.get_row(t, w, 512, r, out)
+            torch.cuda.synchronize()
+            assert np.array_equal(out.cpu().numpy().view(np.uint32), z[t + "_bits"][r]), (t, r)
+
+
+def _rows_bound(dense, x):
+    """Per-row bound on fp32 reassociation: 2e-6 of the sum of |w x| (a single wrong weight
+    moves a 2048-term row by about 5e-4 of it)."""
+    return 2e-6 * np.abs(dense.astype(np.float64)) @ np.abs(x.astype(np.float64)) + 1e-7
+
+
+@pytest.mark.parametrize("types", [("q8_0",) * 3, ("q5_K",) * 3, ("q6_K",) * 3, ("iq4_xs",) * 3,
+                                   ("q5_K", "q6_K", "iq4_xs"), ("bf16", "f16", "f32")])
+def test_qkv_proj_matches_oracle(cuda, types):
+    import torch
+    rng = np.random.default_rng(11)
+    E = fa.N_EMBD
+    x = (rng.standard_normal(E) * 2).astype(np.float32)
+    g = rng.uniform(0.5, 1.5, E).astype(np.float32)
+    xn = np.empty(E, np.float32)
+    oracle.lib().fo_rmsnorm(oracle._p(x), oracle._p(g), oracle._p(xn), E, 1e-6)
+    ws, want, bound = [], [], []
+    for t, n in zip(types, (4096, 512, 512)):
+        rows = oracle.random_blocks(t, n, E, rng)
+        ws.append((_dev(rows, cuda), t))
+        want.append(oracle.matvec(t, rows, E, xn))
+        bound.append(_rows_bound(oracle.dequant_rows(t, rows, E), xn))
+    want, bound = np.concatenate(want), np.concatenate(bound)
+    qkv = torch.full((5120,), float("nan"), dtype=torch.float32, device=cuda)
+    fa.qkv_proj(ws[0], ws[1], ws[2], _dev(x, cuda), _dev(g, cuda), qkv, rms_eps=1e-6)
+    torch.cuda.synchronize()
+    got = qkv.cpu().numpy()
+    err = np.abs(got.astype(np.float64) - want)
+    assert np.all(err <= bound), (types, float((err / bound).max()), int(np.argmax(err / bound)))
+
+
+@pytest.mark.parametrize("wtype", ALL)
+def test_o_proj_residual_matches_oracle(cuda, wtype):
+    import torch
+    rng = np.random.default_rng(12)
+    att = rng.standard_normal(4096).astype(np.float32)
+    x0 = rng.standard_normal(fa.N_EMBD).astype(np.float32)
+    rows = oracle.random_blocks(wtype, fa.N_EMBD, 4096, rng)
+    o = oracle.matvec(wtype, rows, 4096, att)
+    want = x0 + o  # ref_model.cpp:150-151: x[i] += o[i] in float
+    bound = _rows_bound(oracle.dequant_rows(wtype, rows, 4096), att) + 1e-7 * np.abs(x0)
+    x = _dev(x0, cuda)
+    fa.o_proj((_dev(rows, cuda), wtype), _dev(att, cuda), x)
+    torch.cuda.synchronize()
+    err = np.abs(x.cpu().numpy().astype(np.float64) - want)
+    assert np.all(err <= bound), (wtype, float((err / bound).max()))
+
+
+def test_projection_block_round_trip(cuda):
+    """qkv_proj -> decode attention -> o_proj on one layer, against the oracle's attention
+    block (ref_model.cpp:107-151 with the cache in f16): the three stages compose."""
+    import torch
+    rng = np.random.default_rng(13)
+    E, pos = fa.N_EMBD, 40
+    g = rng.uniform(0.5, 1.5, E).astype(np.float32)
+    qn, kn = rng.uniform(0.5, 1.5, 128).astype(np.float32), rng.uniform(0.5, 1.5, 128).astype(np.float32)
+    sinks = rng.standard_normal(32).astype(np.float32)
+    wq, wk, wv = (oracle.random_blocks("q8_0", n, E, rng) for n in (4096, 512, 512))
+    wo = oracle.random_blocks("q6_K", E, 4096, rng)
+    layer = oracle.Layer(qn, kn, sinks, is_swa=False, has_rope=True, store="f16", rope_theta=1e6)
+    kv = fa.KVLayer(is_swa=False, has_rope=True, n_slots=64, kv_dtype="f16", q_norm=qn, k_norm=kn, sinks=sinks,
+                    rope_theta=1e6, device=cuda)
+    K = np.zeros((pos + 1, 512), np.float32)
+    V = np.zeros((pos + 1, 512), np.float32)
+    dq = (_dev(wq, cuda), "q8_0"), (_dev(wk, cuda), "q8_0"), (_dev(wv, cuda), "q8_0")
+    do = (_dev(wo, cuda), "q6_K")
+    qkv = torch.empty(5120, dtype=torch.float32, device=cuda)
+    att = torch.empty(4096, dtype=torch.float32, device=cuda)
+    for p in range(pos + 1):
+        x0 = rng.standard_normal(E).astype(np.float32)
+        xn = np.empty(E, np.float32)
+        oracle.lib().fo_rmsnorm(oracle._p(x0), oracle._p(g), oracle._p(xn), E, 1e-6)
+        qkv_ref = np.concatenate([oracle.matvec("q8_0", w, E, xn) for w in (wq, wk, wv)])
+        att_ref = oracle.decode_step(layer, qkv_ref, p, K, V)
+        x_ref = x0 + oracle.matvec("q6_K", wo, 4096, att_ref)
+        x = _dev(x0, cuda)
+        fa.qkv_proj(*dq, x, _dev(g, cuda), qkv)
+        kv.decode(qkv, att, pos=p)
+        fa.o_proj(do, att, x)
+        torch.cuda.synchronize()
+        got = x.cpu().numpy()
+        scale = np.abs(oracle.dequant_rows("q6_K", wo, 4096)).sum(1) * 2e-3 + 1e-5
+        assert np.all(np.abs(got - x_ref) <= scale), (p, float(np.abs(got - x_ref).max()))
