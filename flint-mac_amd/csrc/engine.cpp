@@ -1,6 +1,7 @@
 // Host side of the flint attention hot path: argument checks, launch plans,
-// device workspaces, the per-layer KV-cache engine and the C ABI
-// (include/flint_attn.h, include/capi.h). Compiled by hipcc as host C++.
+// device workspaces, the per-layer KV-cache engine and the C ABI of the attention
+// stage and the projections (include/flint_attn.h, include/flint_proj.h). Compiled by
+// hipcc as host C++.
 //
 // Stage scheduling mirrors the reference engine's attention stages
 // (/root/reference/src/engine.mm:735-766 decode, 1077-1104 prefill): one
@@ -17,7 +18,6 @@
 #include <string>
 #include <vector>
 
-#include "../../include/capi.h"
 #include "../../include/flint_attn.h"
 #include "../../include/flint_proj.h"
 #include "common.h"
@@ -266,14 +266,23 @@ void check_weight(const flint_weight *w, int64_t k, const char *name) {
     if (rb % 16 || !aligned16(w->data)) throw Error(std::string(name) + ": rows must be 16-byte aligned");
 }
 
-void qkv_proj_impl(const flint_weight *wq, const flint_weight *wk, const flint_weight *wv, const float *x,
-                   const float *attn_norm, float eps, float *qkv, hipStream_t stream) {
+void check_tokens(int n_tok, const char *name) {
+    if (n_tok < 1 || n_tok > 1 << 20) throw Error(std::string(name) + ": n_tok must be in [1, 2^20]");
+}
+
+void qkv_proj_impl(const flint_weight *wq, const flint_weight *wk, const flint_weight *wv, const float *x, int n_tok,
+                   const float *attn_norm, float eps, float *qkv, int qkv_stride, hipStream_t stream) {
     check_weight(wq, N_EMBD, "wq");
     check_weight(wk, N_EMBD, "wk");
     check_weight(wv, N_EMBD, "wv");
+    check_tokens(n_tok, "qkv_proj");
     if (!x || !attn_norm || !qkv) throw Error("qkv_proj: NULL pointer");
     if (!aligned16(x) || !aligned16(attn_norm)) throw Error("qkv_proj: x and attn_norm must be 16-byte aligned");
+    if (qkv_stride < QKV_DIM) throw Error("qkv_proj: qkv_stride must be >= 5120");
     MatvecParams P{};
+    P.n_tok = n_tok;
+    P.x_stride = N_EMBD;
+    P.y_stride = qkv_stride;
     const flint_weight *ws[3] = {wq, wk, wv};
     const int row0[3] = {0, Q_DIM, Q_DIM + KV_DIM};
     for (int i = 0; i < 3; i++)
@@ -288,11 +297,15 @@ void qkv_proj_impl(const flint_weight *wq, const flint_weight *wk, const flint_w
     check(launch_matvec(P, N_EMBD, stream), "qkv_proj launch");
 }
 
-void o_proj_impl(const flint_weight *wo, const float *att, float *x, hipStream_t stream) {
+void o_proj_impl(const flint_weight *wo, const float *att, int n_tok, float *x, hipStream_t stream) {
     check_weight(wo, Q_DIM, "wo");
+    check_tokens(n_tok, "o_proj");
     if (!att || !x) throw Error("o_proj: NULL pointer");
     if (!aligned16(att)) throw Error("o_proj: att must be 16-byte aligned");
     MatvecParams P{};
+    P.n_tok = n_tok;
+    P.x_stride = Q_DIM;
+    P.y_stride = N_EMBD;
     P.seg[0] = MatvecSeg{(const uint8_t *)wo->data, wo->type, 0, (int)w_row_bytes(wo->type, Q_DIM)};
     P.n_seg = 1;
     P.n_rows = N_EMBD;
@@ -320,12 +333,25 @@ int32_t flint_attn_qkv_proj(const flint_weight *wq, const flint_weight *wk, cons
                             const float *attn_norm, float rms_eps, float *qkv, void *stream, char *err,
                             int32_t err_len) {
     return guarded(err, err_len,
-                   [&] { qkv_proj_impl(wq, wk, wv, x, attn_norm, rms_eps, qkv, (hipStream_t)stream); });
+                   [&] { qkv_proj_impl(wq, wk, wv, x, 1, attn_norm, rms_eps, qkv, QKV_DIM, (hipStream_t)stream); });
 }
 
 int32_t flint_attn_o_proj(const flint_weight *wo, const float *att, float *x, void *stream, char *err,
                           int32_t err_len) {
-    return guarded(err, err_len, [&] { o_proj_impl(wo, att, x, (hipStream_t)stream); });
+    return guarded(err, err_len, [&] { o_proj_impl(wo, att, 1, x, (hipStream_t)stream); });
+}
+
+int32_t flint_attn_qkv_proj_rows(const flint_weight *wq, const flint_weight *wk, const flint_weight *wv,
+                                 const float *x, int32_t n_tok, const float *attn_norm, float rms_eps, float *qkv,
+                                 int32_t qkv_stride, void *stream, char *err, int32_t err_len) {
+    return guarded(err, err_len, [&] {
+        qkv_proj_impl(wq, wk, wv, x, n_tok, attn_norm, rms_eps, qkv, qkv_stride, (hipStream_t)stream);
+    });
+}
+
+int32_t flint_attn_o_proj_rows(const flint_weight *wo, const float *att, int32_t n_tok, float *x, void *stream,
+                               char *err, int32_t err_len) {
+    return guarded(err, err_len, [&] { o_proj_impl(wo, att, n_tok, x, (hipStream_t)stream); });
 }
 
 }  // extern "C"
@@ -421,6 +447,18 @@ const flint_attn_layer *flint_attn_engine_layer(const flint_attn_engine *e, int3
     return &e->layers[il].desc;
 }
 
+}  // extern "C"
+
+void flint::engine_set_layer_params(flint_attn_engine *e, int il, int window, float rms_eps) {
+    if (!flint_attn_engine_layer(e, il)) throw Error("engine: bad layer index");
+    if (window < 1 || (e->layers[il].desc.is_swa && window > e->layers[il].desc.n_slots))
+        throw Error("engine: SWA window must be in [1, ring size]");
+    e->layers[il].desc.window = window;
+    e->layers[il].desc.rms_eps = rms_eps;
+}
+
+extern "C" {
+
 int32_t flint_attn_engine_set_weights(flint_attn_engine *e, int32_t il, const float *q_norm, const float *k_norm,
                                       const float *sinks, char *err, int32_t err_len) {
     return guarded(err, err_len, [&] {
@@ -475,75 +513,5 @@ int32_t flint_attn_engine_debug_attn(flint_attn_engine *e, int32_t il, const flo
         check(hipMemcpy(out, dout, (size_t)n_tok * Q_DIM * sizeof(float), hipMemcpyDeviceToHost), "hipMemcpy");
     });
 }
-
-// ---------------------------------------------------------------------------
-// The engine's C API (include/capi.h; /root/reference/src/capi.mm:1-78).
-
-}  // extern "C"
-
-struct flint_engine {
-    flint_attn_engine *attn = nullptr;
-    int32_t n_ctx = 0;
-    int32_t pos = 0;
-    std::vector<float> logits;
-    ~flint_engine() { flint_attn_engine_destroy(attn); }
-};
-
-extern "C" {
-
-flint_engine *flint_open(const flint_config *cfg, char *err, int32_t err_len) {
-    try {
-        if (!cfg || !cfg->model_path) throw Error("flint_open: no model path");
-        std::FILE *f = std::fopen(cfg->model_path, "rb");
-        if (!f) throw Error(std::string("cannot open ") + cfg->model_path);
-        uint32_t magic = 0;
-        const size_t got = std::fread(&magic, 1, 4, f);
-        std::fclose(f);
-        if (got != 4 || magic != 0x46554747u) throw Error(std::string("not a GGUF file: ") + cfg->model_path);
-        throw Error(
-            "flint_open: this library implements the attention hot path only; the GGUF weight loader, "
-            "projections and FFN are not part of this build");
-    } catch (const std::exception &ex) {
-        set_err(err, err_len, ex.what());
-        return nullptr;
-    }
-}
-
-void flint_close(flint_engine *e) { delete e; }
-
-int32_t flint_n_ctx(const flint_engine *e) { return e ? e->n_ctx : 0; }
-int32_t flint_n_vocab(void) { return 150144; }
-int32_t flint_pos(const flint_engine *e) { return e ? e->pos : 0; }
-
-int32_t flint_truncate(flint_engine *e, int32_t pos) {
-    if (!e || pos < 0 || pos > e->pos) return -1;
-    e->pos = pos;
-    return 0;
-}
-
-int32_t flint_prefill(flint_engine *e, const int32_t *tokens, int32_t n, char *err, int32_t err_len) {
-    if (!e) {
-        set_err(err, err_len, "flint_prefill: no engine");
-        return -1;
-    }
-    if (!tokens || n <= 0) {
-        set_err(err, err_len, "prefill: empty");
-        return -1;
-    }
-    set_err(err, err_len, "flint_prefill: weights are not part of this build");
-    return -1;
-}
-
-int32_t flint_decode(flint_engine *e, int32_t token, char *err, int32_t err_len) {
-    (void)token;
-    if (!e) {
-        set_err(err, err_len, "flint_decode: no engine");
-        return -1;
-    }
-    set_err(err, err_len, "flint_decode: weights are not part of this build");
-    return -1;
-}
-
-const float *flint_logits(const flint_engine *e) { return e && !e->logits.empty() ? e->logits.data() : nullptr; }
 
 }  // extern "C"

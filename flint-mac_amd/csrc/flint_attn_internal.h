@@ -68,13 +68,25 @@ struct MatvecSeg {         // rows [row0, row0 + rows) of one launch come from o
 struct MatvecParams {
     MatvecSeg seg[3];
     int n_seg, n_rows;
-    const float *x;        // [K] input
-    const float *norm_w;   // [K] RMSNorm gains applied to x first, or null
+    const float *x;        // [n_tok] rows of x_stride floats, K inputs each
+    const float *norm_w;   // [K] RMSNorm gains applied to each x row first, or null
     float eps;
-    float *y;              // [n_rows]: y = W x, or y += W x when add
+    float *y;              // [n_tok] rows of y_stride floats: y = W x, or y += W x when add
     int add;
+    int n_tok;             // tokens (grid x), >= 1
+    long long x_stride, y_stride;
 };
 hipError_t launch_get_row(const uint8_t *row, int type, int64_t k, float *out, hipStream_t stream);
 hipError_t launch_matvec(const MatvecParams &P, int k, hipStream_t stream);
+
+}  // namespace flint
+
+struct flint_attn_engine;
+
+namespace flint {
+
+// Sets layer il's SWA window and RMSNorm epsilon (the GGUF's attention.sliding_window and
+// attention.layer_norm_rms_epsilon); throws std::runtime_error on a bad index or window.
+void engine_set_layer_params(flint_attn_engine *e, int il, int window, float rms_eps);
 
 }  // namespace flint

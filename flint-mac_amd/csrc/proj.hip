@@ -202,8 +202,12 @@ __global__ __launch_bounds__(64 * MV_WAVES) void matvec_kernel(const MatvecParam
     constexpr int UNITS = (QBYTES / 16 + 63) / 64;  // 16-byte loads per lane for it
     __shared__ __align__(16) uint8_t stage[MV_WAVES][QBYTES];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int row = blockIdx.x * MV_WAVES + wave;
+    const int row = blockIdx.y * MV_WAVES + wave;
     if (row >= P.n_rows) return;  // whole waves; no workgroup barrier below
+    // token blockIdx.x: consecutive workgroups take the same rows for successive tokens,
+    // so a batch reads each weight row from HBM about once (the rest hit L2)
+    const float *__restrict__ xt = P.x + (size_t)blockIdx.x * P.x_stride;
+    float *__restrict__ yt = P.y + (size_t)blockIdx.x * P.y_stride;
     int s = 0;
     while (s + 1 < P.n_seg && row >= P.seg[s + 1].row0) s++;
     const MatvecSeg S = P.seg[s];
@@ -216,7 +220,7 @@ __global__ __launch_bounds__(64 * MV_WAVES) void matvec_kernel(const MatvecParam
     for (int i = 0; i < SUBS; i++)
 #pragma unroll
         for (int k = 0; k < 8; k++) {
-            const f32x4 v = *(const f32x4 *)(P.x + 32 * (lane + 64 * i) + 4 * k);
+            const f32x4 v = *(const f32x4 *)(xt + 32 * (lane + 64 * i) + 4 * k);
             xv[i][4 * k] = v[0], xv[i][4 * k + 1] = v[1], xv[i][4 * k + 2] = v[2], xv[i][4 * k + 3] = v[3];
         }
     float gv[SUBS][32];
@@ -274,7 +278,7 @@ __global__ __launch_bounds__(64 * MV_WAVES) void matvec_kernel(const MatvecParam
         for (int e = 0; e < 32; e++) acc = fmaf(w[e], xv[i][e], acc);
     }
     acc = wave_sum(acc);
-    if (lane == 0) P.y[row] = P.add ? P.y[row] + acc : acc;
+    if (lane == 0) yt[row] = P.add ? yt[row] + acc : acc;
 }
 
 hipError_t launch_get_row(const uint8_t *row, int type, int64_t k, float *out, hipStream_t stream) {
@@ -284,7 +288,7 @@ hipError_t launch_get_row(const uint8_t *row, int type, int64_t k, float *out, h
 }
 
 hipError_t launch_matvec(const MatvecParams &P, int k, hipStream_t stream) {
-    const dim3 grid((P.n_rows + MV_WAVES - 1) / MV_WAVES), block(64 * MV_WAVES);
+    const dim3 grid(P.n_tok, (P.n_rows + MV_WAVES - 1) / MV_WAVES), block(64 * MV_WAVES);
     if (k == 2048)
         hipLaunchKernelGGL(matvec_kernel<2048>, grid, block, 0, stream, P);
     else

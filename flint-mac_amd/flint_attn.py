@@ -47,6 +47,14 @@ class WeightDesc(ctypes.Structure):
     _fields_ = [("data", ctypes.c_void_p), ("type", ctypes.c_int32)]
 
 
+class HParams(ctypes.Structure):
+    """flint_attn_hparams (include/flint_model.h)."""
+    _fields_ = [(n, ctypes.c_int32) for n in ("n_layer", "n_embd", "n_head", "n_head_kv", "head_dim", "n_vocab",
+                                              "n_ff_dense", "n_ff_exp", "n_ff_shexp", "n_expert", "n_expert_used",
+                                              "n_dense_lead", "n_swa")] + [("rms_eps", ctypes.c_float),
+                                                                           ("rope_theta", ctypes.c_float)]
+
+
 # ggml type ids of the weight formats (include/flint_proj.h)
 W_TYPES = {"f32": 0, "f16": 1, "q8_0": 8, "q5_K": 13, "q6_K": 14, "iq4_xs": 23, "bf16": 30}
 N_EMBD = 2048
@@ -76,6 +84,16 @@ _SIGS = {
     "flint_w_get_row": (_i32, [_i32, _vp, _i64, _i64, _vp, _vp, _cp, _i32]),
     "flint_attn_qkv_proj": (_i32, [ctypes.POINTER(WeightDesc)] * 3 + [_vp, _vp, _f32, _vp, _vp, _cp, _i32]),
     "flint_attn_o_proj": (_i32, [ctypes.POINTER(WeightDesc), _vp, _vp, _vp, _cp, _i32]),
+    "flint_attn_qkv_proj_rows": (_i32, [ctypes.POINTER(WeightDesc)] * 3 + [_vp, _i32, _vp, _f32, _vp, _i32, _vp, _cp,
+                                                                            _i32]),
+    "flint_attn_o_proj_rows": (_i32, [ctypes.POINTER(WeightDesc), _vp, _i32, _vp, _vp, _cp, _i32]),
+    "flint_attn_model_open": (_vp, [_cp, _i32, _i32, _cp, _i32]),
+    "flint_attn_model_close": (None, [_vp]),
+    "flint_attn_model_hparams": (_i32, [_vp, ctypes.POINTER(HParams), _u8p, _u8p]),
+    "flint_attn_model_engine": (_vp, [_vp]),
+    "flint_attn_model_embed": (_i32, [_vp, _i32p, _i32, _vp, _vp, _cp, _i32]),
+    "flint_attn_model_block_decode": (_i32, [_vp, _i32, _vp, _i32, _vp, _vp, _cp, _i32]),
+    "flint_attn_model_block_prefill": (_i32, [_vp, _i32, _vp, _i32, _i32, _vp, _vp, _cp, _i32]),
     "flint_open": (_vp, [_vp, _cp, _i32]),
     "flint_close": (None, [_vp]),
     "flint_n_ctx": (_i32, [_vp]),
@@ -236,8 +254,66 @@ def o_proj(wo, att, x, stream=None):
     _call(lib().flint_attn_o_proj, _wdesc(wo), _ptr(att), _ptr(x), _vp(_stream(stream)))
 
 
+def qkv_proj_rows(wq, wk, wv, x, attn_norm, qkv, rms_eps=1e-6, stream=None):
+    """qkv [T][>=5120] rows = [Wq; Wk; Wv] RMSNorm(x[t]) * attn_norm for x [T][2048]
+    (flint_attn_qkv_proj_rows)."""
+    _call(lib().flint_attn_qkv_proj_rows, _wdesc(wq), _wdesc(wk), _wdesc(wv), _ptr(x), x.shape[0], _ptr(attn_norm),
+          rms_eps, _ptr(qkv), qkv.stride(0), _vp(_stream(stream)))
+
+
+def o_proj_rows(wo, att, x, stream=None):
+    """x [T][2048] += Wo att[t] for att [T][4096] (flint_attn_o_proj_rows)."""
+    _call(lib().flint_attn_o_proj_rows, _wdesc(wo), _ptr(att), att.shape[0], _ptr(x), _vp(_stream(stream)))
+
+
 def sync():
     _call(lib().flint_attn_sync)
+
+
+class Model:
+    """flint_attn_model: a Flint GGUF's attention blocks in HBM (include/flint_model.h)."""
+
+    def __init__(self, path, n_ctx, kv_dtype="f16"):
+        err = ctypes.create_string_buffer(512)
+        h = lib().flint_attn_model_open(path.encode(), n_ctx, KV_F16 if kv_dtype == "f16" else KV_BF16, err,
+                                        len(err))
+        if not h:
+            raise FlintAttnError(err.value.decode())
+        self.h = ctypes.c_void_p(h)
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().flint_attn_model_close(self.h)
+            self.h = None
+
+    __del__ = close
+
+    def hparams(self):
+        """(HParams, is_swa list, has_rope list)."""
+        hp = HParams()
+        assert lib().flint_attn_model_hparams(self.h, ctypes.byref(hp), None, None) == 0
+        a = (ctypes.c_uint8 * hp.n_layer)()
+        b = (ctypes.c_uint8 * hp.n_layer)()
+        assert lib().flint_attn_model_hparams(self.h, ctypes.byref(hp), a, b) == 0
+        return hp, list(a), list(b)
+
+    def layer(self, il):
+        p = lib().flint_attn_engine_layer(lib().flint_attn_model_engine(self.h), il)
+        if not p:
+            raise FlintAttnError(f"bad layer index {il}")
+        return p.contents
+
+    def embed(self, tokens, x, stream=None):
+        t = (ctypes.c_int32 * len(tokens))(*[int(v) for v in tokens])
+        _call(lib().flint_attn_model_embed, self.h, t, len(tokens), _ptr(x), _vp(_stream(stream)))
+
+    def block_decode(self, il, x, pos, att=None, stream=None):
+        _call(lib().flint_attn_model_block_decode, self.h, il, _ptr(x), pos, _ptr(att) if att is not None else None,
+              _vp(_stream(stream)))
+
+    def block_prefill(self, il, X, p0, att=None, stream=None):
+        _call(lib().flint_attn_model_block_prefill, self.h, il, _ptr(X), p0, X.shape[0],
+              _ptr(att) if att is not None else None, _vp(_stream(stream)))
 
 
 class Engine:

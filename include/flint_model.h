@@ -1,0 +1,93 @@
+/*
+ * flint attention blocks loaded from a GGUF model on MI355X (gfx950).
+ *
+ * The engine's decode step and layer-major prefill, restricted to the attention half
+ * of each layer: RMSNorm -> q/k/v projections -> attention (QK norm, RoPE, KV cache,
+ * sinks) -> o projection added to the residual. The FFN / MoE half and the output head
+ * are not part of this library; a caller that runs them interleaves its own stages
+ * between the blocks, as the reference's encode_token does
+ * (/root/reference/src/engine.mm:717-893) and its prefill layer loop
+ * (/root/reference/src/engine.mm:1077-1112).
+ *
+ * Same conventions as flint_attn.h: device pointers, `stream` a hipStream_t as void*
+ * (NULL = null stream), 0 / -1 with a NUL-terminated message in err[err_len]. A model
+ * is one session; calls on it must be serialised (/root/reference/src/capi.h:1).
+ */
+#ifndef FLINT_MODEL_H
+#define FLINT_MODEL_H
+
+#include <stdint.h>
+
+#include "flint_attn.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct flint_attn_model flint_attn_model;
+
+/* Hyper-parameters read from the GGUF, as HParams::from_gguf reads them
+ * (/root/reference/src/ref/ref_model.cpp:13-39). */
+typedef struct {
+    int32_t n_layer, n_embd, n_head, n_head_kv, head_dim, n_vocab;
+    int32_t n_ff_dense, n_ff_exp, n_ff_shexp, n_expert, n_expert_used, n_dense_lead;
+    int32_t n_swa;
+    float rms_eps, rope_theta;
+} flint_attn_hparams;
+
+/*
+ * Opens a Flint GGUF: maps the file, reads and validates the hyper-parameters with the
+ * reference's checks and messages (gguf.cpp:137-194, ref_model.cpp:13-39: "cannot open
+ * <path>", "not a GGUF file: <path>", "gguf: missing key <key>", "not a flint model: <arch>",
+ * "unexpected routing config (expect sigmoid + norm, scale 1)", "missing tensor <name>", ...),
+ * checks every attention tensor's type and shape, then copies the token embedding and each
+ * layer's attention tensors (attn_norm, attn_q/k/v/output, attn_q_norm/k_norm, attn_sinks)
+ * to HBM and allocates the KV caches: full layers n_ctx positions, SWA layers a
+ * FLINT_SWA_RING-slot ring (/root/reference/src/engine.mm:472-513).
+ * kv_dtype: FLINT_KV_F16 (the reference's cache type) or FLINT_KV_BF16.
+ * Everything up to the first device allocation runs on the host only.
+ */
+flint_attn_model *flint_attn_model_open(const char *gguf_path, int32_t n_ctx, int32_t kv_dtype, char *err,
+                                        int32_t err_len);
+void flint_attn_model_close(flint_attn_model *m);
+
+/* Copies the hyper-parameters into *hp and, when not NULL, the per-layer flags
+ * (attention.sliding_window_pattern / attention.rope_pattern) into is_swa[n_layer] and
+ * has_rope[n_layer]. 0 / -1. */
+int32_t flint_attn_model_hparams(const flint_attn_model *m, flint_attn_hparams *hp, uint8_t *is_swa,
+                                 uint8_t *has_rope);
+
+/* The model's attention engine (its KV caches and layer descriptors), or NULL. */
+flint_attn_engine *flint_attn_model_engine(flint_attn_model *m);
+
+/*
+ * Token embedding rows: x[i][0:n_embd] = token_embd row tokens[i], dequantised to fp32
+ * (k_get_row / k_embed_rows, /root/reference/src/engine.mm:719, 1068).
+ * tokens: host [n]; x: device [n][n_embd].
+ */
+int32_t flint_attn_model_embed(flint_attn_model *m, const int32_t *tokens, int32_t n, float *x, void *stream,
+                               char *err, int32_t err_len);
+
+/*
+ * Decode step of layer il's attention block for the token at position pos:
+ *   x += Wo . attention(Wq/Wk/Wv . (RMSNorm(x) * attn_norm), pos)
+ * x: device [n_embd], updated in place. att: device [4096] that receives the attention
+ * output, or NULL (an internal buffer). The token's K/V go into the layer's cache at
+ * slot(pos). Replaces the attention half of encode_token, /root/reference/src/engine.mm:726-812.
+ */
+int32_t flint_attn_model_block_decode(flint_attn_model *m, int32_t il, float *x, int32_t pos, float *att,
+                                      void *stream, char *err, int32_t err_len);
+
+/*
+ * Layer-major prefill of layer il's attention block for the T tokens at positions
+ * p0 .. p0+T-1: X[t] += Wo . attention_t(...), all tokens in one pass (any T; the
+ * reference runs 512-token chunks, engine.mm:1077-1112). X: device [T][n_embd], updated
+ * in place; att: device [T][4096] or NULL. The result equals T decode steps in order.
+ */
+int32_t flint_attn_model_block_prefill(flint_attn_model *m, int32_t il, float *X, int32_t p0, int32_t T,
+                                       float *att, void *stream, char *err, int32_t err_len);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

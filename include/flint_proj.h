@@ -74,6 +74,20 @@ int32_t flint_attn_qkv_proj(const flint_weight *wq, const flint_weight *wk, cons
 int32_t flint_attn_o_proj(const flint_weight *wo, const float *att, float *x, void *stream, char *err,
                           int32_t err_len);
 
+/*
+ * The same two projections for n_tok tokens in one launch each (the prefill side):
+ * x: device [n_tok][2048]; qkv: device [n_tok] rows of qkv_stride floats (>= 5120), the raw
+ * q|k|v at each row's start; att: device [n_tok][4096]. Each token's result equals the
+ * single-token call's.
+ * Replace the prefill's k_rmsnorm_rows + three mm (q, k, v), and mm(o) + k_add_rows, at
+ * /root/reference/src/engine.mm:1083-1086 and 1105-1111.
+ */
+int32_t flint_attn_qkv_proj_rows(const flint_weight *wq, const flint_weight *wk, const flint_weight *wv,
+                                 const float *x, int32_t n_tok, const float *attn_norm, float rms_eps, float *qkv,
+                                 int32_t qkv_stride, void *stream, char *err, int32_t err_len);
+int32_t flint_attn_o_proj_rows(const flint_weight *wo, const float *att, int32_t n_tok, float *x, void *stream,
+                               char *err, int32_t err_len);
+
 #ifdef __cplusplus
 }
 #endif

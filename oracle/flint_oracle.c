@@ -426,3 +426,43 @@ int fo_matvec(int type, const void *w, long k, long n_rows, const float *x, floa
     free(row);
     return 0;
 }
+
+/* RefModel::matvec (ref_model.cpp:74-93) over dequantised rows: per row, acc += (double)w * x
+ * in index order, then rounded to float; rows are independent, so threads change nothing. */
+typedef struct {
+    const float *w, *x;
+    float *y;
+    long k, r0, r1;
+} mv_job;
+
+static void *mv_thread(void *arg) {
+    const mv_job *j = (const mv_job *)arg;
+    for (long r = j->r0; r < j->r1; r++) {
+        const float *row = j->w + r * j->k;
+        double acc = 0;
+        for (long i = 0; i < j->k; i++) acc += (double)row[i] * j->x[i];
+        j->y[r] = (float)acc;
+    }
+    return NULL;
+}
+
+void fo_matvec_f32(const float *w, long k, long n_rows, const float *x, float *y, int n_threads) {
+    enum { MAXT = 64 };
+    if (n_threads < 1) n_threads = 1;
+    if (n_threads > MAXT) n_threads = MAXT;
+    mv_job jobs[MAXT];
+    pthread_t th[MAXT];
+    const long chunk = (n_rows + n_threads - 1) / n_threads;
+    int n = 0;
+    for (int t = 0; t < n_threads; t++) {
+        const long r0 = t * chunk, r1 = r0 + chunk < n_rows ? r0 + chunk : n_rows;
+        if (r0 >= r1) break;
+        jobs[n] = (mv_job){w, x, y, k, r0, r1};
+        if (pthread_create(&th[n], NULL, mv_thread, &jobs[n]) != 0) {
+            mv_thread(&jobs[n]);
+            continue;
+        }
+        n++;
+    }
+    for (int t = 0; t < n; t++) pthread_join(th[t], NULL);
+}

@@ -106,6 +106,10 @@ long fo_row_bytes(int type, long k);
 int fo_dequant_row(int type, const void *row, long k, float *out);
 /* y = W x over n_rows rows, double accumulation per row (0 / -1). */
 int fo_matvec(int type, const void *w, long k, long n_rows, const float *x, float *y);
+/* The same product for rows already dequantised to fp32 (w [n_rows][k]), rows split over
+ * n_threads threads; each row's sum runs in the same order as fo_matvec's, so the result
+ * is bit-identical. RefModel::matvec, /root/reference/src/ref/ref_model.cpp:74-93. */
+void fo_matvec_f32(const float *w, long k, long n_rows, const float *x, float *y, int n_threads);
 
 #ifdef __cplusplus
 }

@@ -79,6 +79,7 @@ def lib():
         L.fo_row_bytes.argtypes = [ctypes.c_int, ctypes.c_long]
         L.fo_dequant_row.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_long, _f32p]
         L.fo_matvec.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_long, ctypes.c_long, _f32p, _f32p]
+        L.fo_matvec_f32.argtypes = [_f32p, ctypes.c_long, ctypes.c_long, _f32p, _f32p, ctypes.c_int]
         _lib = L
     return _lib
 
@@ -267,3 +268,55 @@ def random_blocks(wtype, n_rows, k, rng):
     elif wtype == "f32":
         return (rng.standard_normal((n_rows, k)) * 0.05).astype(np.float32).view(np.uint8).reshape(n_rows, rb)
     return data
+
+
+def matvec_f32(W, x, n_threads=8):
+    """y = W x for dequantised rows W [n_rows][k], bit-identical to matvec on the packed rows."""
+    W = np.ascontiguousarray(W, np.float32)
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty(W.shape[0], np.float32)
+    lib().fo_matvec_f32(_p(W), W.shape[1], W.shape[0], _p(x), _p(y), int(n_threads))
+    return y
+
+
+class BlockLayer:
+    """One layer's attention block as the CPU reference runs it (ref_model.cpp:106-151):
+    attn_norm gains, the q/k/v/o weights dequantised to fp32 rows (as dequant_row gives them
+    to RefModel::matvec), and the attention parameters (a Layer)."""
+
+    def __init__(self, attn_norm, wq, wk, wv, wo, attn, rms_eps=1e-6):
+        self.attn_norm = np.ascontiguousarray(attn_norm, np.float32)
+        self.wqkv = np.ascontiguousarray(np.concatenate([wq, wk, wv]), np.float32)
+        self.wo = np.ascontiguousarray(wo, np.float32)
+        assert self.wqkv.shape == (QKV_DIM, 2048) and self.wo.shape == (2048, Q_DIM)
+        self.attn, self.rms_eps = attn, float(rms_eps)
+
+
+def block_step(blk, x, pos, K, V, n_threads=8):
+    """The attention half of RefModel::forward for one layer and one position
+    (ref_model.cpp:107-151): xn = rmsnorm(x) * attn_norm, qkv = W xn (double sums),
+    att = the sink attention over history rows K, V [cap][512] (row pos written here, in
+    the layer's storage type), x + Wo att. Returns (x_new, att)."""
+    xn = rmsnorm(x, blk.attn_norm, blk.rms_eps)
+    qkv = matvec_f32(blk.wqkv, xn, n_threads)
+    att = decode_step(blk.attn, qkv, pos, K, V, n_threads=n_threads)
+    o = matvec_f32(blk.wo, att, n_threads)
+    return (np.asarray(x, np.float32) + o).astype(np.float32), att
+
+
+def block_forward(blocks, embd_rows, store, n_threads=8):
+    """Hidden state after every position of a model whose layers are `blocks` and whose
+    FFN halves are zero (so each layer adds only its attention block): token p at position p,
+    embedding row embd_rows[p]. Returns (hidden [n][2048], att [n_layers][n][4096]); the K/V
+    history is kept in `store` ("f32": what RefModel keeps; "f16"/"bf16": a GPU cache)."""
+    n = embd_rows.shape[0]
+    hist = [(np.zeros((n, KV_DIM), np.float32), np.zeros((n, KV_DIM), np.float32)) for _ in blocks]
+    hidden = np.empty((n, 2048), np.float32)
+    atts = np.empty((len(blocks), n, Q_DIM), np.float32)
+    for p in range(n):
+        x = np.ascontiguousarray(embd_rows[p], np.float32)
+        for il, blk in enumerate(blocks):
+            assert blk.attn.store == store
+            x, atts[il, p] = block_step(blk, x, p, hist[il][0], hist[il][1], n_threads)
+        hidden[p] = x
+    return hidden, atts

@@ -16,6 +16,9 @@
 //
 // Usage: ref_driver <model.gguf> <n_positions> <out.f32>
 //   writes n_positions x 4096 float32 (att of each position, in order).
+// Usage: ref_driver <model.gguf> <n_positions> <out.f32> <n_layers>
+//   runs the first n_layers layers and writes n_positions x n_embd float32: the hidden
+//   state after them (RefModel::last_hidden) at each position, for models of any n_embd.
 #include <cstdio>
 #include <cstdlib>
 #include <exception>
@@ -25,14 +28,15 @@
 #include "ref/ref_model.h"
 
 int main(int argc, char **argv) {
-    if (argc != 4) {
-        std::fprintf(stderr, "usage: %s <model.gguf> <n_positions> <out.f32>\n", argv[0]);
+    if (argc != 4 && argc != 5) {
+        std::fprintf(stderr, "usage: %s <model.gguf> <n_positions> <out.f32> [n_layers]\n", argv[0]);
         return 2;
     }
     try {
         flint::GgufFile f(argv[1]);
         flint::ref::RefModel model(f, 8);
-        model.debug_n_layers = 1;
+        const bool hidden = argc == 5;
+        model.debug_n_layers = hidden ? std::atoi(argv[4]) : 1;
         const int n = std::atoi(argv[2]);
         std::FILE *out = std::fopen(argv[3], "wb");
         if (!out) {
@@ -42,6 +46,10 @@ int main(int argc, char **argv) {
         for (int p = 0; p < n; p++) {
             model.forward(p);  // token id p: the embedding row for position p
             const std::vector<float> &h = model.last_hidden();
+            if (hidden) {
+                std::fwrite(h.data(), sizeof(float), h.size(), out);
+                continue;
+            }
             if (h.size() != 9216) {
                 std::fprintf(stderr, "unexpected hidden size %zu\n", h.size());
                 return 1;

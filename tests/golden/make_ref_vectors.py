@@ -52,8 +52,9 @@ def _s(b):
 
 
 def write_gguf(path, meta, tensors):
-    """Minimal GGUF v3 writer: meta = [(key, type, value)], tensors = [(name, np.ndarray, ggml_type)],
-    array dims given in numpy order (outer first); ggml dims are reversed."""
+    """Minimal GGUF v3 writer: meta = [(key, type, value)], tensors = [(name, np.ndarray, ggml_type)]
+    with array dims in numpy order (outer first; ggml dims are reversed), or
+    (name, uint8 rows, ggml_type, ggml dims) for data already in its on-disk encoding."""
     out = bytearray()
     out += struct.pack("<IIQQ", 0x46554747, 3, len(tensors), len(meta))
     for key, t, v in meta:
@@ -71,9 +72,13 @@ def write_gguf(path, meta, tensors):
         else:
             raise ValueError(t)
     blobs, off = [], 0
-    for name, arr, gt in tensors:
-        data = arr.astype(np.float32 if gt == T_F32 else np.float16).tobytes()
-        dims = list(reversed(arr.shape))
+    for t in tensors:
+        name, arr, gt = t[:3]
+        if len(t) == 4:
+            data, dims = np.ascontiguousarray(arr, np.uint8).tobytes(), list(t[3])
+        else:
+            data = arr.astype(np.float32 if gt == T_F32 else np.float16).tobytes()
+            dims = list(reversed(arr.shape))
         out += _s(name) + struct.pack("<I", len(dims)) + b"".join(struct.pack("<Q", d) for d in dims)
         out += struct.pack("<IQ", gt, off)
         blobs.append(data)

@@ -140,3 +140,31 @@ def test_projection_block_round_trip(cuda):
         got = x.cpu().numpy()
         scale = np.abs(oracle.dequant_rows("q6_K", wo, 4096)).sum(1) * 2e-3 + 1e-5
         assert np.all(np.abs(got - x_ref) <= scale), (p, float(np.abs(got - x_ref).max()))
+
+
+def test_projection_rows_equal_single_token_calls(cuda):
+    """The batched projections (flint_attn_qkv_proj_rows / flint_attn_o_proj_rows) give each
+    token exactly the single-token call's bits, also into a strided qkv row (q_stride 5248)."""
+    import torch
+    rng = np.random.default_rng(41)
+    T = 37
+    wq = (_dev(oracle.random_blocks("q5_K", 4096, 2048, rng), cuda), "q5_K")
+    wk = (_dev(oracle.random_blocks("iq4_xs", 512, 2048, rng), cuda), "iq4_xs")
+    wv = (_dev(oracle.random_blocks("q8_0", 512, 2048, rng), cuda), "q8_0")
+    wo = (_dev(oracle.random_blocks("q6_K", 2048, 4096, rng), cuda), "q6_K")
+    g = _dev(rng.uniform(0.5, 1.5, 2048).astype(np.float32), cuda)
+    x = _dev(rng.standard_normal((T, 2048)).astype(np.float32), cuda)
+    att = _dev(rng.standard_normal((T, 4096)).astype(np.float32), cuda)
+    qkv_rows = torch.full((T, 5248), float("nan"), device=cuda)
+    fa.qkv_proj_rows(wq, wk, wv, x, g, qkv_rows)
+    y_rows = x.clone()
+    fa.o_proj_rows(wo, att, y_rows)
+    qkv_one = torch.empty((T, 5120), device=cuda)
+    y_one = x.clone()
+    for t in range(T):
+        fa.qkv_proj(wq, wk, wv, x[t], g, qkv_one[t])
+        fa.o_proj(wo, att[t], y_one[t])
+    torch.cuda.synchronize()
+    assert torch.equal(qkv_rows[:, :5120], qkv_one)
+    assert torch.isnan(qkv_rows[:, 5120:]).all()  # the row padding is left alone
+    assert torch.equal(y_rows, y_one)
