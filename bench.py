@@ -12,7 +12,11 @@ bf16 KV, full causal and SWA-513), the 16-sequence mixed-context decode
 (config 5), the decode kernel's roofline, and the CPU oracle's decode rate on
 this host (cpu_baseline; a reported baseline, not the target).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only decode|prefill|config5]
+Also on the line: the attention block of a decode step read from a GGUF model (q8_0 q/k/v/o
+projections + attention; full layer at 32k and SWA layer), per layer and as tok/s for Flint's
+layer mix.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only decode|prefill|config5|blocks]
 """
 import argparse
 import json
@@ -211,6 +215,63 @@ def bench_config5(torch, fa, steps=3):
                 bytes_per_step=nbytes)
 
 
+def bench_blocks(torch, fa, reps=96, ctx=32768):
+    """The attention block of a decode step read from a GGUF file (include/flint_model.h):
+    RMSNorm + q/k/v projections, attention, o projection + residual, with q8_0 weights in
+    Flint's shapes (random N(0, 1/k) rows, ggml's q8_0 rounding). One full layer at `ctx` cached
+    positions and one SWA layer (window 513). The caches hold zeros: the kernels read every byte
+    whatever the values. Each block and its attention stage alone are timed like the decode
+    line; the projections are the difference."""
+    import ctypes
+    import tempfile
+    import numpy as np
+    import gguf_writer as gw
+    dev = torch.device("cuda:0")
+    rng = np.random.default_rng(6)
+    E = 2048
+
+    def q8(n, k):
+        return gw.quantize_q8_0((rng.standard_normal((n, k)) / np.sqrt(k)).astype(np.float32))
+
+    tensors = [("token_embd.weight", rng.standard_normal((16, E)).astype(np.float32), gw.T_F16),
+               ("output_norm.weight", np.ones(E, np.float32), gw.T_F32),
+               ("output.weight", np.zeros((1, E), np.float32), gw.T_F16)]
+    wbytes = 0
+    for il in range(2):
+        b = f"blk.{il}."
+        tensors.append((b + "attn_norm.weight", rng.uniform(0.5, 1.5, E).astype(np.float32), gw.T_F32))
+        for name, n, k in (("attn_q", 4096, E), ("attn_k", 512, E), ("attn_v", 512, E), ("attn_output", E, 4096)):
+            rows = q8(n, k)
+            wbytes += rows.nbytes if il == 0 else 0
+            tensors.append((b + name + ".weight", rows, 8, (k, n)))
+        tensors += [(b + "attn_q_norm.weight", rng.uniform(0.5, 1.5, 128).astype(np.float32), gw.T_F32),
+                    (b + "attn_k_norm.weight", rng.uniform(0.5, 1.5, 128).astype(np.float32), gw.T_F32),
+                    (b + "attn_sinks.weight", rng.standard_normal(32).astype(np.float32), gw.T_F32)]
+        tensors += gw.flint_zero_ffn(il)
+    with tempfile.TemporaryDirectory() as tmp:
+        path = os.path.join(tmp, "blocks.gguf")
+        gw.write_gguf(path, gw.flint_meta([0, 1], [0, 1], 513, 1.0e4), tensors)
+        model = fa.Model(path, n_ctx=ctx + 32)
+    x = torch.randn(E, device=dev) * 0.1
+    qkv = torch.randn(5120, device=dev)
+    att = torch.empty(4096, device=dev)
+    out = {}
+    for il, name in ((0, "full"), (1, "swa")):
+        desc = model.layer(il)
+        t_block = queued_launch_ms(torch, lambda: model.block_decode(il, x, ctx, att), reps)[0]
+        t_attn = queued_launch_ms(
+            torch, lambda: fa._call(fa.lib().flint_attn_decode, ctypes.byref(desc), fa._ptr(qkv), fa._ptr(att), ctx,
+                                    0, ctypes.c_void_p(fa._stream(None))), reps)[0]
+        out[name] = dict(block_ms=t_block, attn_ms=t_attn, proj_ms=t_block - t_attn)
+    model.close()
+    t_proj = 0.5 * (out["full"]["proj_ms"] + out["swa"]["proj_ms"])
+    return dict(full_32k_block_ms=out["full"]["block_ms"], swa_block_ms=out["swa"]["block_ms"],
+                full_32k_attn_ms=out["full"]["attn_ms"], swa_attn_ms=out["swa"]["attn_ms"],
+                proj_ms=t_proj, proj_weight_bytes=wbytes, proj_gbs=wbytes / (t_proj * 1e-3) / 1e9,
+                tok_s_32k=1.0 / ((N_FULL_FLINT * out["full"]["block_ms"] + N_SWA_FLINT * out["swa"]["block_ms"])
+                                 * 1e-3))
+
+
 def cpu_baseline(target_s=10.0):
     """The CPU oracle (C restatement of the reference's CPU attention) on this host:
     config-3 decode steps (32768 cached positions, f16-rounded KV)."""
@@ -242,7 +303,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["decode", "prefill", "config5"], default=None)
+    ap.add_argument("--only", choices=["decode", "prefill", "config5", "blocks"], default=None)
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build runs on one GPU. The attention path would shard by key range (decode, "
@@ -271,6 +332,10 @@ def main():
         res["config5"] = bench_config5(torch, fa)
         log(f"config5: ms {res['config5']['ms_per_step']:.3f} tok/s {res['config5']['tok_s']:.1f} "
             f"GB/s {res['config5']['gbs']:.1f}")
+    if args.only in (None, "blocks"):
+        log("attention blocks from a GGUF model (q8_0 projections)")
+        res["blocks"] = bench_blocks(torch, fa)
+        log(f"blocks: {res['blocks']}")
     cpu = None
     if not args.no_cpu:
         log("cpu baseline")
@@ -312,6 +377,9 @@ def main():
         c = res["config5"]
         line["config5_16seq_48layers"] = {"ms_per_step": round(c["ms_per_step"], 4), "tok_s": round(c["tok_s"], 1),
                                           "gbs": round(c["gbs"], 1), "bytes_per_step": c["bytes_per_step"]}
+    if "blocks" in res:
+        line["attention_block_decode_q8_0"] = {k: (round(v, 5) if isinstance(v, float) else v)
+                                               for k, v in res["blocks"].items()}
     if cpu:
         line["cpu_baseline"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in cpu.items()}
     print(json.dumps(line), flush=True)

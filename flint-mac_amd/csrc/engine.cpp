@@ -289,6 +289,8 @@ void qkv_proj_impl(const flint_weight *wq, const flint_weight *wk, const flint_w
         P.seg[i] = MatvecSeg{(const uint8_t *)ws[i]->data, ws[i]->type, row0[i], (int)w_row_bytes(ws[i]->type, N_EMBD)};
     P.n_seg = 3;
     P.n_rows = QKV_DIM;
+    static_assert(Q_DIM % 16 == 0 && KV_DIM % 16 == 0, "segments must hold whole row groups");
+    if (QKV_DIM % matvec_row_multiple(N_EMBD)) throw Error("qkv_proj: row grouping");
     P.x = x;
     P.norm_w = attn_norm;
     P.eps = eps;
@@ -309,6 +311,7 @@ void o_proj_impl(const flint_weight *wo, const float *att, int n_tok, float *x, 
     P.seg[0] = MatvecSeg{(const uint8_t *)wo->data, wo->type, 0, (int)w_row_bytes(wo->type, Q_DIM)};
     P.n_seg = 1;
     P.n_rows = N_EMBD;
+    if (N_EMBD % matvec_row_multiple(Q_DIM)) throw Error("o_proj: row grouping");
     P.x = att;
     P.y = x;
     P.add = 1;

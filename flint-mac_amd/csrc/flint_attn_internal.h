@@ -78,6 +78,7 @@ struct MatvecParams {
 };
 hipError_t launch_get_row(const uint8_t *row, int type, int64_t k, float *out, hipStream_t stream);
 hipError_t launch_matvec(const MatvecParams &P, int k, hipStream_t stream);
+int matvec_row_multiple(int k);  // n_rows of a matvec launch must be a multiple of this
 
 }  // namespace flint
 

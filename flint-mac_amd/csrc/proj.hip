@@ -13,12 +13,13 @@
 // with contraction off, so get_row is bit-identical to dequantize_row_*
 // (/root/reference/src/ref/dequant_gen.c).
 //
-// Matvec layout (HBM-bound on the weight bytes): one wave per row. The wave reads its row
-// with 16-byte loads, coalesced, into an LDS area of its own; each lane then reads the bytes
-// of its sub-block from LDS at the alignment the format gives (q8_0 and q6_K blocks are only
-// 2-byte aligned), decodes 32 weights and accumulates their products with x in fp32; a
-// wave-wide sum gives y[row]. f32/f16/bf16 rows are read straight from HBM (64- or 128-byte
-// sub-blocks, aligned).
+// Matvec layout (HBM-bound on the weight bytes): a wave takes R consecutive rows. It requests
+// their bytes at kernel start (16-byte loads, coalesced) while the workgroup reads x once
+// into LDS (normalised there when the RMSNorm is fused). Row by row, the bytes go into an
+// LDS area of the wave's own; each lane then reads the bytes of its sub-block from LDS at the
+// alignment the format gives (q8_0 and q6_K blocks are only 2-byte aligned), decodes 32
+// weights and accumulates their products with x in fp32; a wave-wide sum gives y[row].
+// f32/f16/bf16 rows are read straight from HBM (64- or 128-byte sub-blocks, aligned).
 #include <hip/hip_runtime.h>
 
 #include "common.h"
@@ -186,8 +187,11 @@ __global__ __launch_bounds__(64) void get_row_kernel(const uint8_t *__restrict__
 }
 
 // ---------------------------------------------------------------------------
-// matvec
-constexpr int MV_WAVES = 4;  // rows (waves) per workgroup
+// matvec: a workgroup of MV_WAVES waves serves MV_WAVES * R consecutive rows of one token.
+// x (RMS-normalised and scaled by the gains first, when norm_w is given) is read from HBM
+// once per workgroup into LDS; each wave then takes R rows, whose bytes it requested at
+// kernel start, and reads its lanes' 32-element slices of x from LDS.
+constexpr int MV_WAVES = 4;
 
 __device__ inline double wave_sum_f64(double v) {
 #pragma unroll
@@ -195,90 +199,115 @@ __device__ inline double wave_sum_f64(double v) {
     return v;
 }
 
-template <int K>
+template <int K, int R>
 __global__ __launch_bounds__(64 * MV_WAVES) void matvec_kernel(const MatvecParams P) {
-    constexpr int SUBS = K / 32 / 64;              // sub-blocks per lane
-    constexpr int QBYTES = K / 32 * 34;            // largest quantised row (q8_0)
+    constexpr int SUBS = K / 32 / 64;               // sub-blocks per lane
+    constexpr int QBYTES = K / 32 * 34;             // largest quantised row (q8_0)
     constexpr int UNITS = (QBYTES / 16 + 63) / 64;  // 16-byte loads per lane for it
+    constexpr int XPT = K / (64 * MV_WAVES);        // x elements per thread in the shared pass
+    __shared__ __align__(16) float xs[K];           // the (normalised) x row
     __shared__ __align__(16) uint8_t stage[MV_WAVES][QBYTES];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int row = blockIdx.y * MV_WAVES + wave;
-    if (row >= P.n_rows) return;  // whole waves; no workgroup barrier below
+    __shared__ double part[MV_WAVES];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int row0 = (blockIdx.y * MV_WAVES + wave) * R;  // R rows, all in one segment
+    int s = 0;
+    while (s + 1 < P.n_seg && row0 >= P.seg[s + 1].row0) s++;
+    const MatvecSeg S = P.seg[s];
+    const uint8_t *wrow = S.w + (size_t)(row0 - S.row0) * S.row_bytes;
+    const bool fl = w_is_float(S.type);
     // token blockIdx.x: consecutive workgroups take the same rows for successive tokens,
     // so a batch reads each weight row from HBM about once (the rest hit L2)
     const float *__restrict__ xt = P.x + (size_t)blockIdx.x * P.x_stride;
     float *__restrict__ yt = P.y + (size_t)blockIdx.x * P.y_stride;
-    int s = 0;
-    while (s + 1 < P.n_seg && row >= P.seg[s + 1].row0) s++;
-    const MatvecSeg S = P.seg[s];
-    const uint8_t *wrow = S.w + (size_t)(row - S.row0) * S.row_bytes;
-    const bool fl = w_is_float(S.type);
 
-    // x (and the norm gains) first: the norm waits for them, not for the row
-    float xv[SUBS][32];
+    // x and the gains: XPT consecutive elements per thread, 16-byte loads
+    f32x4 xv[XPT / 4], gv[XPT / 4];
 #pragma unroll
-    for (int i = 0; i < SUBS; i++)
-#pragma unroll
-        for (int k = 0; k < 8; k++) {
-            const f32x4 v = *(const f32x4 *)(xt + 32 * (lane + 64 * i) + 4 * k);
-            xv[i][4 * k] = v[0], xv[i][4 * k + 1] = v[1], xv[i][4 * k + 2] = v[2], xv[i][4 * k + 3] = v[3];
-        }
-    float gv[SUBS][32];
+    for (int k = 0; k < XPT / 4; k++) xv[k] = *(const f32x4 *)(xt + XPT * tid + 4 * k);
     if (P.norm_w) {
 #pragma unroll
-        for (int i = 0; i < SUBS; i++)
-#pragma unroll
-            for (int k = 0; k < 8; k++) {
-                const f32x4 v = *(const f32x4 *)(P.norm_w + 32 * (lane + 64 * i) + 4 * k);
-                gv[i][4 * k] = v[0], gv[i][4 * k + 1] = v[1], gv[i][4 * k + 2] = v[2], gv[i][4 * k + 3] = v[3];
-            }
+        for (int k = 0; k < XPT / 4; k++) gv[k] = *(const f32x4 *)(P.norm_w + XPT * tid + 4 * k);
     }
-    u32x4 u[UNITS];
+    // this wave's rows (quantised types; float rows are read in the dot loop)
+    u32x4 u[R][UNITS];
     const int n_units = S.row_bytes >> 4;
     if (!fl) {
 #pragma unroll
-        for (int k = 0; k < UNITS; k++) {
-            const int idx = lane + 64 * k;
-            if (idx < n_units) u[k] = ((const u32x4 *)wrow)[idx];
-        }
+        for (int r = 0; r < R; r++)
+#pragma unroll
+            for (int k = 0; k < UNITS; k++) {
+                const int idx = lane + 64 * k;
+                if (idx < n_units) u[r][k] = ((const u32x4 *)(wrow + (size_t)r * S.row_bytes))[idx];
+            }
     }
     if (P.norm_w) {
         // RMSNorm as the CPU reference (ref_model.cpp:45-50): double sum of squares, float
         // scale, (x * scale) * g
         double ss = 0;
 #pragma unroll
-        for (int i = 0; i < SUBS; i++)
+        for (int k = 0; k < XPT / 4; k++)
 #pragma unroll
-            for (int e = 0; e < 32; e++) ss += (double)xv[i][e] * xv[i][e];
+            for (int e = 0; e < 4; e++) ss += (double)xv[k][e] * xv[k][e];
         ss = wave_sum_f64(ss);
+        if (lane == 0) part[wave] = ss;
+        __syncthreads();
+        ss = 0;
+#pragma unroll
+        for (int w = 0; w < MV_WAVES; w++) ss += part[w];
         const float scale = 1.0f / sqrtf((float)(ss / K) + P.eps);
 #pragma unroll
-        for (int i = 0; i < SUBS; i++)
+        for (int k = 0; k < XPT / 4; k++)
 #pragma unroll
-            for (int e = 0; e < 32; e++) xv[i][e] = xv[i][e] * scale * gv[i][e];
+            for (int e = 0; e < 4; e++) xv[k][e] = xv[k][e] * scale * gv[k][e];
     }
-    const uint8_t *src = wrow;
-    if (!fl) {
 #pragma unroll
-        for (int k = 0; k < UNITS; k++) {
-            const int idx = lane + 64 * k;
-            if (idx < n_units) ((u32x4 *)stage[wave])[idx] = u[k];
+    for (int k = 0; k < XPT / 4; k++) *(f32x4 *)&xs[XPT * tid + 4 * k] = xv[k];
+    __syncthreads();
+
+    // this lane's slices of x: sub-blocks lane + 64 i
+    float xl[SUBS][32];
+#pragma unroll
+    for (int i = 0; i < SUBS; i++)
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const f32x4 v = *(const f32x4 *)&xs[32 * (lane + 64 * i) + 4 * k];
+            xl[i][4 * k] = v[0], xl[i][4 * k + 1] = v[1], xl[i][4 * k + 2] = v[2], xl[i][4 * k + 3] = v[3];
         }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        src = stage[wave];
-    }
-    float acc = 0.f;
+    float acc[R];
 #pragma unroll
-    for (int i = 0; i < SUBS; i++) {
-        float w[32];
-        deq32(S.type, src, lane + 64 * i, w);
+    for (int r = 0; r < R; r++) {
+        const uint8_t *src = wrow + (size_t)r * S.row_bytes;
+        if (!fl) {
+            if (r > 0) __builtin_amdgcn_wave_barrier();  // every lane done with the previous row
 #pragma unroll
-        for (int e = 0; e < 32; e++) acc = fmaf(w[e], xv[i][e], acc);
+            for (int k = 0; k < UNITS; k++) {
+                const int idx = lane + 64 * k;
+                if (idx < n_units) ((u32x4 *)stage[wave])[idx] = u[r][k];
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            src = stage[wave];
+        }
+        float a = 0.f;
+#pragma unroll
+        for (int i = 0; i < SUBS; i++) {
+            float w[32];
+            deq32(S.type, src, lane + 64 * i, w);
+#pragma unroll
+            for (int e = 0; e < 32; e++) a = fmaf(w[e], xl[i][e], a);
+        }
+        acc[r] = a;
     }
-    acc = wave_sum(acc);
-    if (lane == 0) yt[row] = P.add ? yt[row] + acc : acc;
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = wave_sum(acc[r]);
+    if (lane < R) {
+        float a = acc[0];
+#pragma unroll
+        for (int r = 1; r < R; r++) a = lane == r ? acc[r] : a;
+        const int row = row0 + lane;
+        yt[row] = P.add ? yt[row] + a : a;
+    }
 }
 
 hipError_t launch_get_row(const uint8_t *row, int type, int64_t k, float *out, hipStream_t stream) {
@@ -287,12 +316,20 @@ hipError_t launch_get_row(const uint8_t *row, int type, int64_t k, float *out, h
     return hipGetLastError();
 }
 
+// Rows per wave: 4 for the 2048-element rows (q/k/v: 320 workgroups per token), 2 for the
+// 4096-element rows (o: 256 workgroups).
+constexpr int MV_ROWS_2048 = 4, MV_ROWS_4096 = 2;
+
+int matvec_row_multiple(int k) { return MV_WAVES * (k == 2048 ? MV_ROWS_2048 : MV_ROWS_4096); }
+
 hipError_t launch_matvec(const MatvecParams &P, int k, hipStream_t stream) {
-    const dim3 grid(P.n_tok, (P.n_rows + MV_WAVES - 1) / MV_WAVES), block(64 * MV_WAVES);
+    const dim3 block(64 * MV_WAVES);
     if (k == 2048)
-        hipLaunchKernelGGL(matvec_kernel<2048>, grid, block, 0, stream, P);
+        hipLaunchKernelGGL((matvec_kernel<2048, MV_ROWS_2048>), dim3(P.n_tok, P.n_rows / matvec_row_multiple(k)),
+                           block, 0, stream, P);
     else
-        hipLaunchKernelGGL(matvec_kernel<4096>, grid, block, 0, stream, P);
+        hipLaunchKernelGGL((matvec_kernel<4096, MV_ROWS_4096>), dim3(P.n_tok, P.n_rows / matvec_row_multiple(k)),
+                           block, 0, stream, P);
     return hipGetLastError();
 }
 

@@ -35,6 +35,7 @@ sys.path.insert(0, os.path.join(ROOT, "oracle"))
 sys.path.insert(0, HERE)
 import oracle as fo  # noqa: E402
 import make_ref_vectors as g  # noqa: E402
+import gguf_writer as gw  # noqa: E402  (flint-mac_amd/, on the path via make_ref_vectors)
 
 E = 2048
 SEED = 300
@@ -99,35 +100,12 @@ def model_sha(m):
 def write_model(path, m, meta_edit=None, tensor_edit=None):
     """Writes the model as a Flint GGUF. meta_edit {key: None (drop) | (type, value)} and
     tensor_edit (a function of the tensor list) make the defective files of the loader tests."""
-    a = "flint."
-    n_layer = len(m["layers"])
-    meta = [
-        ("general.architecture", g.GGUF_STRING, "flint"),
-        (a + "block_count", g.GGUF_U32, n_layer),
-        (a + "embedding_length", g.GGUF_U32, E),
-        (a + "attention.head_count", g.GGUF_U32, 32),
-        (a + "attention.head_count_kv", g.GGUF_U32, 4),
-        (a + "attention.key_length", g.GGUF_U32, 128),
-        (a + "feed_forward_length", g.GGUF_U32, 1),
-        (a + "expert_feed_forward_length", g.GGUF_U32, 1),
-        (a + "expert_shared_feed_forward_length", g.GGUF_U32, 1),
-        (a + "expert_count", g.GGUF_U32, 1),
-        (a + "expert_used_count", g.GGUF_U32, 1),
-        (a + "leading_dense_block_count", g.GGUF_U32, 1),
-        (a + "attention.sliding_window", g.GGUF_U32, N_SWA),
-        (a + "attention.layer_norm_rms_epsilon", g.GGUF_F32, RMS_EPS),
-        (a + "rope.freq_base", g.GGUF_F32, THETA),
-        (a + "attention.sliding_window_pattern", g.GGUF_ARRAY, [bool(L["is_swa"]) for L in m["layers"]]),
-        (a + "attention.rope_pattern", g.GGUF_ARRAY, [bool(L["has_rope"]) for L in m["layers"]]),
-        (a + "expert_gating_func", g.GGUF_U32, 2),
-        (a + "expert_weights_norm", g.GGUF_BOOL, True),
-        (a + "expert_weights_scale", g.GGUF_F32, 1.0),
-    ]
-    z16 = lambda *shape: np.zeros(shape, np.float32)  # noqa: E731 (written as f16 zeros)
+    meta = gw.flint_meta([L["is_swa"] for L in m["layers"]], [L["has_rope"] for L in m["layers"]], N_SWA, THETA,
+                         RMS_EPS)
     tensors = [
         ("token_embd.weight", m["embd"].astype(np.float32), T_F16),
         ("output_norm.weight", np.ones(E, np.float32), T_F32),
-        ("output.weight", z16(1, E), T_F16),
+        ("output.weight", np.zeros((1, E), np.float32), T_F16),
     ]
     for il, L in enumerate(m["layers"]):
         b = f"blk.{il}."
@@ -140,19 +118,7 @@ def write_model(path, m, meta_edit=None, tensor_edit=None):
             (b + "attn_q_norm.weight", L["q_norm"], T_F32),
             (b + "attn_k_norm.weight", L["k_norm"], T_F32),
             (b + "attn_sinks.weight", L["sinks"], T_F32),
-            (b + "ffn_norm.weight", np.ones(E, np.float32), T_F32),
-        ]
-        if il < 1:  # leading dense block
-            tensors += [(b + "ffn_gate.weight", z16(1, E), T_F16), (b + "ffn_up.weight", z16(1, E), T_F16),
-                        (b + "ffn_down.weight", z16(E, 1), T_F16)]
-        else:  # one zero expert and a zero shared expert
-            tensors += [(b + "ffn_gate_inp.weight", z16(1, E), T_F16),
-                        (b + "ffn_gate_exps.weight", z16(1, 1, E), T_F16),
-                        (b + "ffn_up_exps.weight", z16(1, 1, E), T_F16),
-                        (b + "ffn_down_exps.weight", z16(1, E, 1), T_F16),
-                        (b + "ffn_gate_shexp.weight", z16(1, E), T_F16),
-                        (b + "ffn_up_shexp.weight", z16(1, E), T_F16),
-                        (b + "ffn_down_shexp.weight", z16(E, 1), T_F16)]
+        ] + gw.flint_zero_ffn(il)
     for key, val in (meta_edit or {}).items():
         meta = [e for e in meta if e[0] != key] + ([(key,) + tuple(val)] if val is not None else [])
     if tensor_edit:

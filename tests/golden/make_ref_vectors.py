@@ -20,7 +20,6 @@ The raw q|k|v the attention sees is rmsnorm(x)[0:5120] with unit weights
 import hashlib
 import json
 import os
-import struct
 import subprocess
 import sys
 import tempfile
@@ -42,52 +41,9 @@ CASES = [
 ]
 PROBE_HEADS = [0, 7, 8, 31]
 
-GGUF_U32, GGUF_F32, GGUF_BOOL, GGUF_STRING, GGUF_ARRAY = 4, 6, 7, 8, 9
-T_F32, T_F16 = 0, 1
-
-
-def _s(b):
-    b = b.encode()
-    return struct.pack("<Q", len(b)) + b
-
-
-def write_gguf(path, meta, tensors):
-    """Minimal GGUF v3 writer: meta = [(key, type, value)], tensors = [(name, np.ndarray, ggml_type)]
-    with array dims in numpy order (outer first; ggml dims are reversed), or
-    (name, uint8 rows, ggml_type, ggml dims) for data already in its on-disk encoding."""
-    out = bytearray()
-    out += struct.pack("<IIQQ", 0x46554747, 3, len(tensors), len(meta))
-    for key, t, v in meta:
-        out += _s(key) + struct.pack("<I", t)
-        if t == GGUF_U32:
-            out += struct.pack("<I", v)
-        elif t == GGUF_F32:
-            out += struct.pack("<f", v)
-        elif t == GGUF_BOOL:
-            out += struct.pack("<B", 1 if v else 0)
-        elif t == GGUF_STRING:
-            out += _s(v)
-        elif t == GGUF_ARRAY:  # bool arrays only
-            out += struct.pack("<IQ", GGUF_BOOL, len(v)) + bytes(1 if x else 0 for x in v)
-        else:
-            raise ValueError(t)
-    blobs, off = [], 0
-    for t in tensors:
-        name, arr, gt = t[:3]
-        if len(t) == 4:
-            data, dims = np.ascontiguousarray(arr, np.uint8).tobytes(), list(t[3])
-        else:
-            data = arr.astype(np.float32 if gt == T_F32 else np.float16).tobytes()
-            dims = list(reversed(arr.shape))
-        out += _s(name) + struct.pack("<I", len(dims)) + b"".join(struct.pack("<Q", d) for d in dims)
-        out += struct.pack("<IQ", gt, off)
-        blobs.append(data)
-        off += (len(data) + 31) // 32 * 32
-    pad = (-len(out)) % 32
-    with open(path, "wb") as f:
-        f.write(out + b"\0" * pad)
-        for d in blobs:
-            f.write(d + b"\0" * ((-len(d)) % 32))
+# the GGUF writer lives with the library (flint-mac_amd/gguf_writer.py)
+sys.path.insert(0, os.path.join(ROOT, "flint-mac_amd"))
+from gguf_writer import GGUF_ARRAY, GGUF_BOOL, GGUF_F32, GGUF_STRING, GGUF_U32, T_F16, T_F32, write_gguf  # noqa: E402,F401
 
 
 def make_inputs(seed, n):
