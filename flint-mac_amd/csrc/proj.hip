@@ -210,23 +210,36 @@ __global__ __launch_bounds__(64 * MV_WAVES) void matvec_kernel(const MatvecParam
     __shared__ double part[MV_WAVES];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int row0 = (blockIdx.y * MV_WAVES + wave) * R;  // R rows, all in one segment
-    int s = 0;
-    while (s + 1 < P.n_seg && row0 >= P.seg[s + 1].row0) s++;
-    const MatvecSeg S = P.seg[s];
+    // the segment by selection among constant-index reads: the kernel arguments arrive in one
+    // batch of scalar loads (a search loop over P.seg costs a memory round trip per step)
+    const MatvecSeg s0 = P.seg[0], s1 = P.seg[1], s2 = P.seg[2];
+    const int n_seg = P.n_seg, add = P.add;
+    const long long x_stride = P.x_stride, y_stride = P.y_stride;
+    const float *const x = P.x, *const norm_w = P.norm_w;
+    float *const y = P.y;
+    const float eps = P.eps;
+    pin_sgpr(s0.w), pin_sgpr(s0.type), pin_sgpr(s0.row0), pin_sgpr(s0.row_bytes);
+    pin_sgpr(s1.w), pin_sgpr(s1.type), pin_sgpr(s1.row0), pin_sgpr(s1.row_bytes);
+    pin_sgpr(s2.w), pin_sgpr(s2.type), pin_sgpr(s2.row0), pin_sgpr(s2.row_bytes);
+    pin_sgpr(n_seg), pin_sgpr(add), pin_sgpr(x_stride), pin_sgpr(y_stride), pin_sgpr(x), pin_sgpr(norm_w);
+    pin_sgpr(y), pin_sgpr(eps);
+    __builtin_amdgcn_sched_barrier(0);
+    const bool in2 = n_seg > 2 && row0 >= s2.row0, in1 = !in2 && n_seg > 1 && row0 >= s1.row0;
+    const MatvecSeg S = in2 ? s2 : in1 ? s1 : s0;
     const uint8_t *wrow = S.w + (size_t)(row0 - S.row0) * S.row_bytes;
     const bool fl = w_is_float(S.type);
     // token blockIdx.x: consecutive workgroups take the same rows for successive tokens,
     // so a batch reads each weight row from HBM about once (the rest hit L2)
-    const float *__restrict__ xt = P.x + (size_t)blockIdx.x * P.x_stride;
-    float *__restrict__ yt = P.y + (size_t)blockIdx.x * P.y_stride;
+    const float *__restrict__ xt = x + (size_t)blockIdx.x * x_stride;
+    float *__restrict__ yt = y + (size_t)blockIdx.x * y_stride;
 
     // x and the gains: XPT consecutive elements per thread, 16-byte loads
     f32x4 xv[XPT / 4], gv[XPT / 4];
 #pragma unroll
     for (int k = 0; k < XPT / 4; k++) xv[k] = *(const f32x4 *)(xt + XPT * tid + 4 * k);
-    if (P.norm_w) {
+    if (norm_w) {
 #pragma unroll
-        for (int k = 0; k < XPT / 4; k++) gv[k] = *(const f32x4 *)(P.norm_w + XPT * tid + 4 * k);
+        for (int k = 0; k < XPT / 4; k++) gv[k] = *(const f32x4 *)(norm_w + XPT * tid + 4 * k);
     }
     // this wave's rows (quantised types; float rows are read in the dot loop)
     u32x4 u[R][UNITS];
@@ -240,7 +253,7 @@ __global__ __launch_bounds__(64 * MV_WAVES) void matvec_kernel(const MatvecParam
                 if (idx < n_units) u[r][k] = ((const u32x4 *)(wrow + (size_t)r * S.row_bytes))[idx];
             }
     }
-    if (P.norm_w) {
+    if (norm_w) {
         // RMSNorm as the CPU reference (ref_model.cpp:45-50): double sum of squares, float
         // scale, (x * scale) * g
         double ss = 0;
@@ -254,7 +267,7 @@ __global__ __launch_bounds__(64 * MV_WAVES) void matvec_kernel(const MatvecParam
         ss = 0;
 #pragma unroll
         for (int w = 0; w < MV_WAVES; w++) ss += part[w];
-        const float scale = 1.0f / sqrtf((float)(ss / K) + P.eps);
+        const float scale = 1.0f / sqrtf((float)(ss / K) + eps);
 #pragma unroll
         for (int k = 0; k < XPT / 4; k++)
 #pragma unroll
@@ -306,7 +319,7 @@ __global__ __launch_bounds__(64 * MV_WAVES) void matvec_kernel(const MatvecParam
 #pragma unroll
         for (int r = 1; r < R; r++) a = lane == r ? acc[r] : a;
         const int row = row0 + lane;
-        yt[row] = P.add ? yt[row] + a : a;
+        yt[row] = add ? yt[row] + a : a;
     }
 }
 
