@@ -33,10 +33,12 @@
 //    last-block merge inside the streaming kernel needs an agent-scope
 //    release/acquire per block and funnels every partial through one CU, which
 //    measured slower than the kernel boundary.)
-//  * Batched entry: grid (max split, kv head, sequence), so one launch serves many
-//    independent sequences (one token each); blocks past a sequence's split count
-//    exit at once. Every kernel argument the block needs is read at wave start, so
-//    the kernel-argument fetch costs one memory round trip.
+//  * Batched entry: one launch serves many independent sequences (one token each).
+//    The grid is flat: sequence s owns 4 x n_split[s] consecutive workgroups (kv head
+//    fastest), so no workgroup is idle and the XCDs, dealt workgroups in id order, get
+//    equal shares of the stream. Every kernel argument the block needs is read at wave
+//    start (the per-sequence tables one entry per lane), so the kernel-argument fetch
+//    costs one memory round trip.
 #include "common.h"
 #include "flint_attn_internal.h"
 
@@ -173,25 +175,38 @@ __global__ __launch_bounds__(DEC_THREADS) void attn_decode_kernel(const DecodePa
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n = lane & 15, g = lane >> 4;   // MFMA column (q head x hi/lo) and k-group
     const int hloc = n & 7, hl = n >> 3;      // head within the GQA group, 0 = hi half, 1 = lo half
-    const int split = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
+    static_assert(MAX_SEQ == 64, "one per-sequence table entry per lane");
 
-    // ---- every kernel argument is read here, in one batch of scalar loads at wave start
-    //      (left to itself the compiler sinks each load to its first use, and each sunk
-    //      load is one more memory round trip on the critical path) ----
-    const int n_split = P.n_split[seq], pos = P.pos[seq];
-    const int is_swa = P.is_swa, has_rope = P.has_rope, window = P.window, tps = P.tiles_per_split;
+    // ---- every kernel argument is read here, in one batch of loads at wave start (left to
+    //      itself the compiler sinks each load to its first use, and each sunk load is one
+    //      more memory round trip on the critical path). The per-sequence tables arrive one
+    //      entry per lane, so finding this workgroup's sequence costs no second round trip ----
+    const int t_base = P.wg_base[lane], t_pos = P.pos[lane], t_tps = P.tps[lane], t_ns = P.n_split[lane];
+    const int n_seq = P.n_seq;
+    const int is_swa = P.is_swa, has_rope = P.has_rope, window = P.window;
     const int n_slots = P.n_slots, slot_mask = P.slot_mask, max_split = P.max_split;
     const float rms_eps = P.rms_eps;
     const long long seq_stride = P.seq_stride;
     const float *const qkv = P.qkv, *const q_norm = P.q_norm, *const k_norm = P.k_norm, *const sinks = P.sinks;
     uint16_t *const k_cache = P.k_cache, *const v_cache = P.v_cache;
     float *const att = P.att, *const partial = P.partial;
-    pin_sgpr(n_split), pin_sgpr(pos), pin_sgpr(is_swa), pin_sgpr(has_rope), pin_sgpr(window), pin_sgpr(tps);
+    pin_sgpr(n_seq), pin_sgpr(is_swa), pin_sgpr(has_rope), pin_sgpr(window);
     pin_sgpr(n_slots), pin_sgpr(slot_mask), pin_sgpr(max_split), pin_sgpr(rms_eps), pin_sgpr(seq_stride);
     pin_sgpr(qkv), pin_sgpr(q_norm), pin_sgpr(k_norm), pin_sgpr(sinks), pin_sgpr(k_cache), pin_sgpr(v_cache);
     pin_sgpr(att), pin_sgpr(partial);
+    asm volatile("" ::"v"(t_base), "v"(t_pos), "v"(t_tps), "v"(t_ns));
 
-    if (split >= n_split) return;  // grid x covers the longest sequence's splits
+    // The grid is flat and holds exactly the launch's work units: sequence s owns workgroups
+    // wg_base[s] .. wg_base[s] + 4 n_split[s] - 1, kv head fastest. The hardware deals
+    // workgroups to the XCDs in id order, so equal-sized units spread every XCD's share of
+    // the stream evenly (a grid with idle slots skews it, and one XCD moves ~1.2 TB/s at most).
+    const int wid = blockIdx.x;
+    const int seq = __builtin_popcountll(__builtin_amdgcn_ballot_w64(lane < n_seq && wid >= t_base)) - 1;
+    const int n_split = __builtin_amdgcn_readlane(t_ns, seq), pos = __builtin_amdgcn_readlane(t_pos, seq);
+    const int tps = __builtin_amdgcn_readlane(t_tps, seq);
+    const int local = wid - __builtin_amdgcn_readlane(t_base, seq);
+    const int kvh = local & (N_HEAD_KV - 1), split = local / N_HEAD_KV;
+    if (seq < 0 || split >= n_split) return;  // not reached: the host sizes the grid exactly
     const bool last_split = split == n_split - 1;
     const int k_begin = is_swa ? max(pos - (window - 1), 0) : 0;
     const int tile_lo = k_begin >> 5, tile_hi = (pos + 31) >> 5;  // tiles holding keys [k_begin, pos)
@@ -450,7 +465,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const DecodeParams P)
 }
 
 hipError_t launch_decode(const DecodeParams &P, int dtype, hipStream_t stream) {
-    dim3 grid(P.max_split, N_HEAD_KV, P.n_seq), block(DEC_THREADS);
+    dim3 grid(P.wg_base[P.n_seq]), block(DEC_THREADS);
     if (dtype == DT_F16)
         hipLaunchKernelGGL(attn_decode_kernel<DT_F16>, grid, block, 0, stream, P);
     else

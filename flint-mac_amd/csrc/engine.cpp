@@ -103,23 +103,36 @@ void validate_layer(const flint_attn_layer *L) {
     }
 }
 
-// Split plan: 32-key tiles per split, the same for every sequence of a launch.
-// An 8-wave block is one CU's share; the plan keeps the 4 x (total splits)
-// blocks within one round of the 256 CUs, with at least two tiles per wave.
-// Small launches (a few blocks, latency-bound) take one split per sequence
-// when that stays within 8 tiles per wave: the split merge costs more than
-// the extra tiles.
-int plan_tiles_per_split(int total_tiles, int max_tiles, int keys_per_split) {
-    if (keys_per_split > 0) return std::max(1, keys_per_split / 32);
-    // one split (no merge kernel) while a workgroup's 8 waves need at most 3 tiles each;
-    // otherwise spread the key tiles of all sequences over about 192 workgroups (a multiple
-    // of 4 tiles each, 8 at least). Measured on MI355X at 16k-64k keys: ~170-210
-    // workgroups of longer streams beat one workgroup per CU (256), e.g. 15.6 vs 17.2 us
-    // per call at 32k, 25.1 vs 27.5 at 64k.
-    if (max_tiles <= 3 * 8 && total_tiles * N_HEAD_KV <= 256) return std::max(max_tiles, 1);
-    const int target_blocks = 192;
-    const int tps = (total_tiles * N_HEAD_KV + target_blocks - 1) / target_blocks;
-    return std::max(8, (tps + 3) / 4 * 4);
+// Split plan: 32-key tiles per split, per sequence. An 8-wave block is one CU's share.
+// Small launches (a few blocks, latency-bound) take one split per sequence while a
+// workgroup's 8 waves need at most 3 tiles each: the split merge costs more than the extra
+// tiles. Otherwise the key tiles of all sequences are spread over about 192 workgroups
+// (measured on MI355X at 16k-64k keys: ~170-210 workgroups of longer streams beat one per
+// CU, e.g. 15.6 vs 17.2 us per call at 32k, 25.1 vs 27.5 at 64k), each sequence's range cut
+// into equal splits (a multiple of 4 tiles, 8 at least): the launch lasts as long as its
+// longest split, and with one split length for every sequence the short remainders of the
+// others left HBM idle at the end (16 sequences at 4k-65k: 221 vs 262 us per layer).
+// keys_per_split > 0 overrides the plan with that split length for every sequence.
+void plan_splits(int n_seq, const int *tiles, int keys_per_split, int *n_split, int *tps) {
+    int total = 0, max_tiles = 0;
+    for (int s = 0; s < n_seq; s++) total += tiles[s], max_tiles = std::max(max_tiles, tiles[s]);
+    for (int s = 0; s < n_seq; s++) {
+        int t;
+        if (keys_per_split > 0) {
+            t = std::max(1, keys_per_split / 32);
+        } else if (max_tiles <= 3 * 8 && total * N_HEAD_KV <= 256) {
+            t = std::max(max_tiles, 1);
+        } else {
+            const int target_blocks = 192;
+            // this sequence's share of the workgroups, then equal splits of its range
+            const int64_t want = ((int64_t)tiles[s] * target_blocks + (int64_t)total * N_HEAD_KV - 1) /
+                                 ((int64_t)total * N_HEAD_KV);
+            const int ns = std::max<int64_t>(1, want);
+            t = std::max(8, ((tiles[s] + ns - 1) / ns + 3) / 4 * 4);
+        }
+        tps[s] = t;
+        n_split[s] = std::max(1, (tiles[s] + t - 1) / t);
+    }
 }
 
 // theta^(-2i/128) table, cached for the last theta
@@ -159,24 +172,23 @@ void decode_impl(const flint_attn_layer *L, int n_seq, int64_t seq_stride, const
     P.rms_eps = L->rms_eps;
     rope_freqs_cached(L->rope_theta, P.rope_freq);
     P.n_seq = n_seq;
-    int tiles[MAX_SEQ], total_tiles = 0, max_tiles = 0;
+    int tiles[MAX_SEQ];
     for (int s = 0; s < n_seq; s++) {
         const int p = pos[s];
         if (p < 0) throw Error("position must be >= 0");
         if (!L->is_swa && p >= L->n_slots) throw Error("context full: position beyond the layer's KV capacity");
         const int k_begin = L->is_swa ? std::max(p - (L->window - 1), 0) : 0;
         tiles[s] = p > 0 ? (p + 31) / 32 - k_begin / 32 : 0;
-        total_tiles += tiles[s];
-        max_tiles = std::max(max_tiles, tiles[s]);
     }
-    const int tps = plan_tiles_per_split(total_tiles, max_tiles, keys_per_split);
+    plan_splits(n_seq, tiles, keys_per_split, P.n_split, P.tps);
     int max_split = 1;
+    P.wg_base[0] = 0;
     for (int s = 0; s < n_seq; s++) {
         P.pos[s] = pos[s];
-        P.n_split[s] = std::max(1, (tiles[s] + tps - 1) / tps);
         max_split = std::max(max_split, P.n_split[s]);
+        P.wg_base[s + 1] = P.wg_base[s] + N_HEAD_KV * P.n_split[s];
     }
-    P.tiles_per_split = tps;
+    for (int s = n_seq + 1; s <= MAX_SEQ; s++) P.wg_base[s] = P.wg_base[n_seq];
     P.max_split = max_split;
     if (max_split > 1024) throw Error("too many key splits (max 1024): raise keys_per_split");
     DeviceScratch &ws = scratch();

@@ -25,12 +25,13 @@ struct DecodeParams {
     int n_slots;                // slots per kv head
     int slot_mask;              // SWA: n_slots - 1 (power of two); full: all ones
     int is_swa, has_rope, window, max_split;
-    int tiles_per_split;        // 32-key tiles per split (all sequences)
     float rms_eps;
     int n_seq;
     float rope_freq[64];        // theta^(-2i/128), computed on the host like ref_model.cpp:55
     int pos[MAX_SEQ];           // sequence s decodes the token at pos[s]
     int n_split[MAX_SEQ];       // key splits of sequence s (grid x covers max_split)
+    int tps[MAX_SEQ];           // 32-key tiles per split of sequence s
+    int wg_base[MAX_SEQ + 1];   // first workgroup of sequence s (4 per split); [n_seq] = grid size
 };
 
 hipError_t launch_decode(const DecodeParams &P, int dtype, hipStream_t stream);

@@ -180,9 +180,10 @@ def test_decode_batch_matches_single(cuda, is_swa):
 
 def test_decode_batch_long_contexts_auto_split(cuda):
     """Config-5 shape: independent sequences at long, mixed contexts in one launch, with the
-    automatic split plan (one key-split size for the batch, so the sequences get different
-    split counts up to the grid's width; a sequence with one split is written directly by the
-    decode kernel). Every sequence equals the oracle."""
+    automatic split plan (each sequence's key range cut into its own number of equal splits,
+    so the sequences differ in split count and split length up to the grid's width; a
+    sequence with one split is written directly by the decode kernel). Every sequence equals
+    the oracle."""
     _say("decode batch, long mixed contexts, auto split")
     rng = np.random.default_rng(44)
     qn, kn, sk = layer_weights(rng)
