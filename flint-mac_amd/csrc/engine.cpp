@@ -104,9 +104,9 @@ void validate_layer(const flint_attn_layer *L) {
 }
 
 // Split plan: 32-key tiles per split, per sequence. An 8-wave block is one CU's share.
-// Small launches (a few blocks, latency-bound) take one split per sequence while a
-// workgroup's 8 waves need at most 3 tiles each: the split merge costs more than the extra
-// tiles. Otherwise the key tiles of all sequences are spread over about 192 workgroups
+// Every sequence takes one split while a workgroup's 8 waves need at most 3 tiles each
+// (a grid of at most 4 x 64 workgroups, one round of the CUs): the split merge kernel costs
+// more than streaming those tiles through one CU. Otherwise the key tiles of all sequences are spread over about 192 workgroups
 // (measured on MI355X at 16k-64k keys: ~170-210 workgroups of longer streams beat one per
 // CU, e.g. 15.6 vs 17.2 us per call at 32k, 25.1 vs 27.5 at 64k), each sequence's range cut
 // into equal splits (a multiple of 4 tiles, 8 at least): the launch lasts as long as its
@@ -120,7 +120,7 @@ void plan_splits(int n_seq, const int *tiles, int keys_per_split, int *n_split, 
         int t;
         if (keys_per_split > 0) {
             t = std::max(1, keys_per_split / 32);
-        } else if (max_tiles <= 3 * 8 && total * N_HEAD_KV <= 256) {
+        } else if (max_tiles <= 3 * 8) {
             t = std::max(max_tiles, 1);
         } else {
             const int target_blocks = 192;
