@@ -3,8 +3,8 @@ the library's tests, the benchmark and users who want a small model file to try 
 attention blocks with (include/flint_model.h). Host-side tooling; no GPU work.
 
 File layout written: header (magic "GGUF", version 3, tensor count, key/value count), the
-key/value section, the tensor infos, then the tensor data, each tensor 32-byte aligned
-(general.alignment's default), as /root/reference/src/gguf.cpp:137-194 reads it.
+key/value section, the tensor infos, then the tensor data, each tensor aligned to
+general.alignment (32 unless given), as /root/reference/src/gguf.cpp:137-194 reads it.
 """
 import struct
 
@@ -19,26 +19,39 @@ def _s(b):
     return struct.pack("<Q", len(b)) + b
 
 
-def write_gguf(path, meta, tensors):
+# metadata value types of the format and their scalar encodings
+GGUF_U8, GGUF_I8, GGUF_U16, GGUF_I16, GGUF_I32, GGUF_U64, GGUF_I64, GGUF_F64 = 0, 1, 2, 3, 5, 10, 11, 12
+_SCALAR = {GGUF_U8: "<B", GGUF_I8: "<b", GGUF_U16: "<H", GGUF_I16: "<h", GGUF_U32: "<I", GGUF_I32: "<i",
+           GGUF_F32: "<f", GGUF_U64: "<Q", GGUF_I64: "<q", GGUF_F64: "<d"}
+
+
+def _value(t, v):
+    if t in _SCALAR:
+        return struct.pack(_SCALAR[t], v)
+    if t == GGUF_BOOL:
+        return struct.pack("<B", 1 if v else 0)
+    if t == GGUF_STRING:
+        return _s(v)
+    raise ValueError(t)
+
+
+def write_gguf(path, meta, tensors, alignment=32):
     """Minimal GGUF v3 writer: meta = [(key, type, value)], tensors = [(name, np.ndarray, ggml_type)]
     with array dims in numpy order (outer first; ggml dims are reversed), or
-    (name, uint8 rows, ggml_type, ggml dims) for data already in its on-disk encoding."""
+    (name, uint8 rows, ggml_type, ggml dims) for data already in its on-disk encoding.
+    An array value is (element type, list); a bare list is a bool array. A non-default
+    alignment is also written as general.alignment."""
+    if alignment != 32:
+        meta = list(meta) + [("general.alignment", GGUF_U32, alignment)]
     out = bytearray()
     out += struct.pack("<IIQQ", 0x46554747, 3, len(tensors), len(meta))
     for key, t, v in meta:
         out += _s(key) + struct.pack("<I", t)
-        if t == GGUF_U32:
-            out += struct.pack("<I", v)
-        elif t == GGUF_F32:
-            out += struct.pack("<f", v)
-        elif t == GGUF_BOOL:
-            out += struct.pack("<B", 1 if v else 0)
-        elif t == GGUF_STRING:
-            out += _s(v)
-        elif t == GGUF_ARRAY:  # bool arrays only
-            out += struct.pack("<IQ", GGUF_BOOL, len(v)) + bytes(1 if x else 0 for x in v)
+        if t == GGUF_ARRAY:
+            et, items = v if isinstance(v, tuple) else (GGUF_BOOL, v)
+            out += struct.pack("<IQ", et, len(items)) + b"".join(_value(et, x) for x in items)
         else:
-            raise ValueError(t)
+            out += _value(t, v)
     blobs, off = [], 0
     for t in tensors:
         name, arr, gt = t[:3]
@@ -50,12 +63,12 @@ def write_gguf(path, meta, tensors):
         out += _s(name) + struct.pack("<I", len(dims)) + b"".join(struct.pack("<Q", d) for d in dims)
         out += struct.pack("<IQ", gt, off)
         blobs.append(data)
-        off += (len(data) + 31) // 32 * 32
-    pad = (-len(out)) % 32
+        off += (len(data) + alignment - 1) // alignment * alignment
+    pad = (-len(out)) % alignment
     with open(path, "wb") as f:
         f.write(out + b"\0" * pad)
         for d in blobs:
-            f.write(d + b"\0" * ((-len(d)) % 32))
+            f.write(d + b"\0" * ((-len(d)) % alignment))
 
 
 def quantize_q8_0(w):

@@ -207,3 +207,72 @@ def test_loader_argument_checks(model_file):
 def test_capi_open_valid_model_names_the_scope(model_file):
     msg = capi_open_error(model_file)
     assert "attention blocks only" in msg and "2-layer model" in msg
+
+
+def _raw_meta_model(model, tmp_path, name, extra_meta=(), alignment=32, retype=None):
+    """The block model with extra metadata entries (raw: any value type) and its tensors at the
+    given data alignment; retype = {key: (type, value)} replaces a hyper-parameter's encoding."""
+    import gguf_writer as gw
+    meta = gw.flint_meta([L["is_swa"] for L in model["layers"]], [L["has_rope"] for L in model["layers"]], mb.N_SWA,
+                         mb.THETA, mb.RMS_EPS)
+    for key, (t, v) in (retype or {}).items():
+        meta = [(k, t, v) if k == key else (k, tt, vv) for k, tt, vv in meta]
+    path = str(tmp_path / f"{name}.gguf")
+    captured = {}
+
+    def grab(ts):
+        captured["t"] = ts
+        return ts
+    mb.write_model(path, model, tensor_edit=grab)
+    gw.write_gguf(path, meta + list(extra_meta), captured["t"], alignment=alignment)
+    return path
+
+
+def test_loader_reads_every_metadata_type(model, tmp_path):
+    """Metadata of every GGUF value type, integer hyper-parameters in other integer widths, a
+    float one in f64, and a 64-byte data alignment: the file parses and validates (the
+    reference's get_int / get_float accept any integer / float width, gguf.cpp:206-213)."""
+    import gguf_writer as gw
+    extra = [("x.u8", gw.GGUF_U8, 200), ("x.i8", gw.GGUF_I8, -5), ("x.u16", gw.GGUF_U16, 60000),
+             ("x.i16", gw.GGUF_I16, -300), ("x.i32", gw.GGUF_I32, -70000), ("x.u64", gw.GGUF_U64, 1 << 40),
+             ("x.i64", gw.GGUF_I64, -(1 << 40)), ("x.f64", gw.GGUF_F64, 0.125), ("x.s", gw.GGUF_STRING, "tokens"),
+             ("x.ai", gw.GGUF_ARRAY, (gw.GGUF_I32, [1, -2, 3])), ("x.af", gw.GGUF_ARRAY, (gw.GGUF_F32, [0.5, 1.5])),
+             ("x.as", gw.GGUF_ARRAY, (gw.GGUF_STRING, ["a", "bc", ""])), ("x.ab", gw.GGUF_ARRAY, [True, False])]
+    retype = {"flint.block_count": (gw.GGUF_U64, 2), "flint.attention.head_count": (gw.GGUF_I16, 32),
+              "flint.rope.freq_base": (gw.GGUF_F64, mb.THETA)}
+    path = _raw_meta_model(model, tmp_path, "types", extra, alignment=64, retype=retype)
+    assert "attention blocks only" in capi_open_error(path) and "2-layer model" in capi_open_error(path)
+    err = _err()
+    h = fa.lib().flint_attn_model_open(path.encode(), 256, fa.KV_F16, err, len(err))
+    if h:  # a GPU is present: the model loaded
+        hp = fa.HParams()
+        assert fa.lib().flint_attn_model_hparams(h, ctypes.byref(hp), None, None) == 0
+        assert hp.n_layer == 2 and hp.n_head == 32 and hp.rope_theta == mb.THETA
+        fa.lib().flint_attn_model_close(h)
+    else:  # no GPU: every host-side check passed and the first device allocation failed
+        assert err.value.decode().startswith("hipMalloc"), err.value.decode()
+
+
+def test_loader_rejects_bad_encodings(model, tmp_path):
+    import gguf_writer as gw
+    # a metadata value type the format does not have
+    path = str(tmp_path / "badtype.gguf")
+    blob = bytearray(open(_raw_meta_model(model, tmp_path, "ok", [("x.z", gw.GGUF_U32, 7)]), "rb").read())
+    i = blob.index(b"x.z") + 3
+    blob[i:i + 4] = struct.pack("<I", 13)
+    open(path, "wb").write(bytes(blob))
+    assert model_open_error(path) == "gguf: unknown metadata type 13"
+    # an array of arrays
+    i = blob.index(b"x.z") + 3
+    blob[i:i + 4] = struct.pack("<I", gw.GGUF_ARRAY)
+    blob[i + 4:i + 8] = struct.pack("<I", gw.GGUF_ARRAY)  # element type (the u32 value's bytes)
+    open(path, "wb").write(bytes(blob))
+    assert model_open_error(path) == "gguf: unsupported array element type"
+    # a tensor type id ggml does not define
+    p2 = str(tmp_path / "tensortype.gguf")
+    mb.write_model(p2, model, tensor_edit=lambda ts: [(t[0], t[1], 99, (2048, 1)) if t[0] == "output.weight"
+                                                      else t for t in ts])
+    assert model_open_error(p2) == "unsupported ggml type 99"
+    # general.alignment 0
+    p3 = _raw_meta_model(model, tmp_path, "align0", [("general.alignment", gw.GGUF_U32, 0)])
+    assert model_open_error(p3) == "gguf: general.alignment is 0"
