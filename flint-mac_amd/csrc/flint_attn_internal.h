@@ -29,7 +29,7 @@ struct DecodeParams {
     int n_seq;
     float rope_freq[64];        // theta^(-2i/128), computed on the host like ref_model.cpp:55
     int pos[MAX_SEQ];           // sequence s decodes the token at pos[s]
-    int n_split[MAX_SEQ];       // key splits of sequence s (grid x covers max_split)
+    int n_split[MAX_SEQ];       // key splits of sequence s
     int tps[MAX_SEQ];           // 32-key tiles per split of sequence s
     int wg_base[MAX_SEQ + 1];   // first workgroup of sequence s (4 per split); [n_seq] = grid size
 };
