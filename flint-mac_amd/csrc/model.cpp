@@ -152,6 +152,7 @@ struct flint_attn_model {
     // scratch: raw q|k|v rows and attention outputs for up to `cap` tokens
     float *qkv = nullptr, *att = nullptr;
     int cap = 0;
+    int32_t n_ctx = 0, pos = 0;  // the session: context length and tokens processed
 
     ~flint_attn_model() {
         flint_attn_engine_destroy(eng);
@@ -185,6 +186,7 @@ flint_attn_model *flint_attn_model_open(const char *gguf_path, int32_t n_ctx, in
         if (kv_dtype != FLINT_KV_F16 && kv_dtype != FLINT_KV_BF16)
             throw std::runtime_error("flint_attn_model_open: kv_dtype must be F16 or BF16");
         auto m = std::make_unique<flint_attn_model>();
+        m->n_ctx = n_ctx;
         m->file = std::make_unique<gguf::File>(gguf_path);
         const gguf::File &f = *m->file;
         m->hp = read_hparams(f);
@@ -313,6 +315,44 @@ int32_t flint_attn_model_block_prefill(flint_attn_model *m, int32_t il, float *X
              e2);
         call(flint_attn_engine_prefill(m->eng, il, m->qkv, p0, T, a, stream, e2, sizeof(e2)), e2);
         call(flint_attn_o_proj_rows(&L.o, a, T, X, stream, e2, sizeof(e2)), e2);
+    });
+}
+
+int32_t flint_attn_model_pos(const flint_attn_model *m) { return m ? m->pos : 0; }
+int32_t flint_attn_model_n_ctx(const flint_attn_model *m) { return m ? m->n_ctx : 0; }
+
+int32_t flint_attn_model_truncate(flint_attn_model *m, int32_t pos) {
+    if (!m || pos < 0 || pos > m->pos) return -1;
+    m->pos = pos;
+    return 0;
+}
+
+int32_t flint_attn_model_step(flint_attn_model *m, int32_t token, float *x, void *stream, char *err,
+                              int32_t err_len) {
+    return guarded(err, err_len, [&] {
+        if (!m) throw std::runtime_error("step: no model");
+        if (!x) throw std::runtime_error("step: x is NULL");
+        if (m->pos >= m->n_ctx) throw std::runtime_error("context full");
+        char e2[512] = {0};
+        call(flint_attn_model_embed(m, &token, 1, x, stream, e2, sizeof(e2)), e2);
+        for (int il = 0; il < (int)m->layers.size(); il++)
+            call(flint_attn_model_block_decode(m, il, x, m->pos, nullptr, stream, e2, sizeof(e2)), e2);
+        m->pos++;
+    });
+}
+
+int32_t flint_attn_model_prefill(flint_attn_model *m, const int32_t *tokens, int32_t n, float *X, void *stream,
+                                 char *err, int32_t err_len) {
+    return guarded(err, err_len, [&] {
+        if (!m) throw std::runtime_error("prefill: no model");
+        if (!tokens || n <= 0) throw std::runtime_error("prefill: empty");
+        if (!X) throw std::runtime_error("prefill: X is NULL");
+        if ((int64_t)m->pos + n > m->n_ctx) throw std::runtime_error("prefill: context full");
+        char e2[512] = {0};
+        call(flint_attn_model_embed(m, tokens, n, X, stream, e2, sizeof(e2)), e2);
+        for (int il = 0; il < (int)m->layers.size(); il++)
+            call(flint_attn_model_block_prefill(m, il, X, m->pos, n, nullptr, stream, e2, sizeof(e2)), e2);
+        m->pos += n;
     });
 }
 

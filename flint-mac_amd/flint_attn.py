@@ -94,6 +94,11 @@ _SIGS = {
     "flint_attn_model_embed": (_i32, [_vp, _i32p, _i32, _vp, _vp, _cp, _i32]),
     "flint_attn_model_block_decode": (_i32, [_vp, _i32, _vp, _i32, _vp, _vp, _cp, _i32]),
     "flint_attn_model_block_prefill": (_i32, [_vp, _i32, _vp, _i32, _i32, _vp, _vp, _cp, _i32]),
+    "flint_attn_model_pos": (_i32, [_vp]),
+    "flint_attn_model_n_ctx": (_i32, [_vp]),
+    "flint_attn_model_truncate": (_i32, [_vp, _i32]),
+    "flint_attn_model_step": (_i32, [_vp, _i32, _vp, _vp, _cp, _i32]),
+    "flint_attn_model_prefill": (_i32, [_vp, _i32p, _i32, _vp, _vp, _cp, _i32]),
     "flint_open": (_vp, [_vp, _cp, _i32]),
     "flint_close": (None, [_vp]),
     "flint_n_ctx": (_i32, [_vp]),
@@ -310,6 +315,29 @@ class Model:
     def block_decode(self, il, x, pos, att=None, stream=None):
         _call(lib().flint_attn_model_block_decode, self.h, il, _ptr(x), pos, _ptr(att) if att is not None else None,
               _vp(_stream(stream)))
+
+    @property
+    def pos(self):
+        return lib().flint_attn_model_pos(self.h)
+
+    @property
+    def n_ctx(self):
+        return lib().flint_attn_model_n_ctx(self.h)
+
+    def truncate(self, pos):
+        """0 on success, -1 if pos is outside [0, pos] (flint_attn_model_truncate)."""
+        return lib().flint_attn_model_truncate(self.h, pos)
+
+    def step(self, token, x, stream=None):
+        """The token through every layer's attention block at the current position; x [2048]
+        receives the hidden state (flint_attn_model_step)."""
+        _call(lib().flint_attn_model_step, self.h, int(token), _ptr(x), _vp(_stream(stream)))
+
+    def prefill(self, tokens, X, stream=None):
+        """tokens at the current position, layer-major; X [n][2048] receives the hidden states
+        (flint_attn_model_prefill)."""
+        t = (ctypes.c_int32 * len(tokens))(*[int(v) for v in tokens])
+        _call(lib().flint_attn_model_prefill, self.h, t, len(tokens), _ptr(X), _vp(_stream(stream)))
 
     def block_prefill(self, il, X, p0, att=None, stream=None):
         _call(lib().flint_attn_model_block_prefill, self.h, il, _ptr(X), p0, X.shape[0],

@@ -87,6 +87,43 @@ int32_t flint_attn_model_block_decode(flint_attn_model *m, int32_t il, float *x,
 int32_t flint_attn_model_block_prefill(flint_attn_model *m, int32_t il, float *X, int32_t p0, int32_t T,
                                        float *att, void *stream, char *err, int32_t err_len);
 
+/*
+ * The model as one session over its attention blocks, as the reference's Engine drives its
+ * layers (/root/reference/src/engine.h:24-79). The position is the number of tokens processed.
+ * With the FFN half outside this library, the hidden state these calls return is that of the
+ * attention blocks alone: for a model whose FFN weights are zero it is RefModel::last_hidden()
+ * (/root/reference/src/ref/ref_model.cpp:95-187).
+ */
+int32_t flint_attn_model_pos(const flint_attn_model *m);   /* Engine::pos, engine.h:57 */
+int32_t flint_attn_model_n_ctx(const flint_attn_model *m); /* Engine::n_ctx, engine.h:60 */
+
+/*
+ * Rolls the session back to position pos, 0 <= pos <= the current position (0 / -1), as
+ * flint_truncate (/root/reference/src/capi.mm:52-56): the caches keep their contents and the
+ * next token goes to position pos. SWA layers keep only their last FLINT_SWA_RING positions,
+ * so after a rollback of more than FLINT_SWA_RING - window tokens (511 for Flint) the caller
+ * re-prefills from max(0, pos - (window - 1)), the rule of /root/reference/src/capi.h:27-28.
+ */
+int32_t flint_attn_model_truncate(flint_attn_model *m, int32_t pos);
+
+/*
+ * Engine::step (engine.mm:902-940) over the attention blocks: the token's embedding row
+ * through every layer's block at the current position, which then advances by one.
+ * x: device [n_embd] receives the hidden state after the last layer.
+ * Fails with "context full" when the position has reached n_ctx (engine.mm:904).
+ */
+int32_t flint_attn_model_step(flint_attn_model *m, int32_t token, float *x, void *stream, char *err,
+                              int32_t err_len);
+
+/*
+ * Engine::prefill (engine.mm:971-1255) over the attention blocks, layer-major: tokens[n]
+ * (host) at the current position, every token through layer 0, then layer 1, ...; the
+ * position advances by n. X: device [n][n_embd] receives the hidden states.
+ * Fails with "prefill: empty" or "prefill: context full" (engine.mm:975-976).
+ */
+int32_t flint_attn_model_prefill(flint_attn_model *m, const int32_t *tokens, int32_t n, float *X, void *stream,
+                                 char *err, int32_t err_len);
+
 #ifdef __cplusplus
 }
 #endif

@@ -155,3 +155,61 @@ def test_block_errors(setup, cuda):
     model.block_decode(1, x, 500)  # SWA layer: the ring has no n_ctx limit
     torch.cuda.synchronize()
     model.close()
+
+
+def test_session_step_prefill_truncate(setup, cuda):
+    """The model as one session (flint_attn_model_step / _prefill / _truncate, the reference's
+    Engine::step / prefill / truncate): token by token, prefill + steps + prefill, and after a
+    rollback the same tokens again give the same hidden states bit for bit (full layer: the
+    slots are rewritten with the same values; SWA ring: a 60-token rollback keeps its window)."""
+    import torch
+    path, embd, hidden, att, blocks = setup
+    n = embd.shape[0]
+    m = fa.Model(path, n_ctx=256)
+    assert (m.pos, m.n_ctx) == (0, 256)
+    xs = torch.zeros((n, 2048), device=cuda)
+    for p in range(n):
+        m.step(p, xs[p])
+    torch.cuda.synchronize()
+    assert m.pos == n
+    first = xs.cpu().numpy()
+    _close(first, hidden, "session steps, end to end")
+    assert m.truncate(n + 1) == -1 and m.truncate(-1) == -1 and m.pos == n
+    assert m.truncate(100) == 0 and m.pos == 100
+    again = torch.zeros((n - 100, 2048), device=cuda)
+    for i, p in enumerate(range(100, n)):
+        m.step(p, again[i])
+    torch.cuda.synchronize()
+    assert np.array_equal(again.cpu().numpy(), first[100:]), "replay after truncate differs"
+    m.close()
+
+    m2 = fa.Model(path, n_ctx=256)
+    X = torch.zeros((n, 2048), device=cuda)
+    m2.prefill(list(range(70)), X[:70])
+    for p in range(70, 80):
+        m2.step(p, X[p])
+    m2.prefill(list(range(80, n)), X[80:])
+    torch.cuda.synchronize()
+    assert m2.pos == n
+    _close(X.cpu().numpy(), hidden, "session prefill/step/prefill, end to end")
+    m2.close()
+
+
+def test_session_errors(setup, cuda):
+    import torch
+    m = fa.Model(setup[0], n_ctx=64)
+    X = torch.zeros((65, 2048), device=cuda)
+    with pytest.raises(fa.FlintAttnError, match="prefill: empty"):
+        m.prefill([], X)
+    with pytest.raises(fa.FlintAttnError, match="prefill: context full"):
+        m.prefill(list(range(65)), X)
+    assert m.pos == 0
+    m.prefill(list(range(64)), X[:64])
+    with pytest.raises(fa.FlintAttnError, match="context full"):
+        m.step(0, X[64])
+    assert m.pos == 64
+    assert m.truncate(10) == 0
+    m.step(10, X[10])
+    torch.cuda.synchronize()
+    assert m.pos == 11
+    m.close()

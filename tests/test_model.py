@@ -202,6 +202,10 @@ def test_loader_argument_checks(model_file):
     assert L.flint_attn_model_block_decode(None, 0, None, 0, None, None, err, len(err)) == -1
     assert L.flint_attn_model_block_prefill(None, 0, None, 0, 1, None, None, err, len(err)) == -1
     assert L.flint_attn_model_embed(None, None, 0, None, None, err, len(err)) == -1
+    assert L.flint_attn_model_pos(None) == 0 and L.flint_attn_model_n_ctx(None) == 0
+    assert L.flint_attn_model_truncate(None, 0) == -1
+    assert L.flint_attn_model_step(None, 0, None, None, err, len(err)) == -1
+    assert L.flint_attn_model_prefill(None, None, 0, None, None, err, len(err)) == -1
 
 
 def test_capi_open_valid_model_names_the_scope(model_file):
