@@ -20,8 +20,8 @@
  *   split-K partials + LSE merge           /root/reference/src/metal/fused.metal:319-350
  *   SWA window / ring slot                 /root/reference/src/metal/flint_config.h:25,29-31
  *
- * Parity pinning (what checks each function; all in tests/test_oracle.py and
- * tests/test_ref_parity.py):
+ * Parity pinning (what checks each function; in tests/test_oracle.py, tests/test_ref_parity.py,
+ * tests/test_weights.py and tests/test_model.py):
  *   fo_round            numpy float16 / torch bfloat16 casts, bit-exact, all finite inputs of a sweep
  *   fo_rmsnorm          closed form for constant vectors; reference RefModel (bit-exact)
  *   fo_rope_neox        pos 0 identity, pair-norm preservation, relative-position invariance
@@ -38,6 +38,12 @@
  *                       q8_0 with d = 1 gives the int8 values)
  *   fo_matvec           one-hot rows select x exactly; equals a float64 numpy product of
  *                       fo_dequant_row's rows; linearity in x
+ *   fo_matvec_f32       with oracle.py's block forward (rmsnorm, q/k/v and o matvecs over
+ *                       dequantised rows, the attention above, the residual add): the hidden
+ *                       states of a two-layer quantised model with zero FFN weights equal the
+ *                       reference's RefModel::forward bit for bit (tests/test_model.py against
+ *                       tests/golden/block_vectors.json, written from oracle/_ref); a zero
+ *                       o-projection leaves x unchanged; position 0 matches the one-key closed form
  */
 #ifndef FLINT_ORACLE_H
 #define FLINT_ORACLE_H
