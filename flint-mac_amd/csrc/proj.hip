@@ -208,7 +208,9 @@ __global__ __launch_bounds__(64 * MV_WAVES) void matvec_kernel(const MatvecParam
     __shared__ __align__(16) float xs[K];           // the (normalised) x row
     __shared__ __align__(16) uint8_t stage[MV_WAVES][QBYTES];
     __shared__ double part[MV_WAVES];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // wave index made scalar: the row segment, its type and its row pointer are then known
+    // to be wave-uniform (scalar branches for the format, scalar load bases)
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int row0 = (blockIdx.y * MV_WAVES + wave) * R;  // R rows, all in one segment
     // the segment by selection among constant-index reads: the kernel arguments arrive in one
     // batch of scalar loads (a search loop over P.seg costs a memory round trip per step)
@@ -286,11 +288,13 @@ __global__ __launch_bounds__(64 * MV_WAVES) void matvec_kernel(const MatvecParam
             const f32x4 v = *(const f32x4 *)&xs[32 * (lane + 64 * i) + 4 * k];
             xl[i][4 * k] = v[0], xl[i][4 * k + 1] = v[1], xl[i][4 * k + 2] = v[2], xl[i][4 * k + 3] = v[3];
         }
+    // The two row sources take separate code paths, so that each dequantiser's reads have a
+    // known address space: LDS reads for the staged quantised rows, global reads for float
+    // rows (one pointer that may be either compiles to generic flat loads, several times slower).
     float acc[R];
+    if (!fl) {
 #pragma unroll
-    for (int r = 0; r < R; r++) {
-        const uint8_t *src = wrow + (size_t)r * S.row_bytes;
-        if (!fl) {
+        for (int r = 0; r < R; r++) {
             if (r > 0) __builtin_amdgcn_wave_barrier();  // every lane done with the previous row
 #pragma unroll
             for (int k = 0; k < UNITS; k++) {
@@ -300,17 +304,30 @@ __global__ __launch_bounds__(64 * MV_WAVES) void matvec_kernel(const MatvecParam
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            src = stage[wave];
-        }
-        float a = 0.f;
+            float a = 0.f;
 #pragma unroll
-        for (int i = 0; i < SUBS; i++) {
-            float w[32];
-            deq32(S.type, src, lane + 64 * i, w);
+            for (int i = 0; i < SUBS; i++) {
+                float w[32];
+                deq32(S.type, stage[wave], lane + 64 * i, w);
 #pragma unroll
-            for (int e = 0; e < 32; e++) a = fmaf(w[e], xl[i][e], a);
+                for (int e = 0; e < 32; e++) a = fmaf(w[e], xl[i][e], a);
+            }
+            acc[r] = a;
         }
-        acc[r] = a;
+    } else {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint8_t *__restrict__ src = wrow + (size_t)r * S.row_bytes;
+            float a = 0.f;
+#pragma unroll
+            for (int i = 0; i < SUBS; i++) {
+                float w[32];
+                deq32(S.type, src, lane + 64 * i, w);
+#pragma unroll
+                for (int e = 0; e < 32; e++) a = fmaf(w[e], xl[i][e], a);
+            }
+            acc[r] = a;
+        }
     }
 #pragma unroll
     for (int r = 0; r < R; r++) acc[r] = wave_sum(acc[r]);
