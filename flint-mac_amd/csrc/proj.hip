@@ -346,9 +346,9 @@ hipError_t launch_get_row(const uint8_t *row, int type, int64_t k, float *out, h
     return hipGetLastError();
 }
 
-// Rows per wave: 4 for the 2048-element rows (q/k/v: 320 workgroups per token), 2 for the
-// 4096-element rows (o: 256 workgroups).
-constexpr int MV_ROWS_2048 = 4, MV_ROWS_4096 = 2;
+// Rows per wave: 2 for the 2048-element rows (q/k/v: 640 workgroups per token) and for the
+// 4096-element rows (o: 256 workgroups); measured best of 1, 2, 4 and 8.
+constexpr int MV_ROWS_2048 = 2, MV_ROWS_4096 = 2;
 
 int matvec_row_multiple(int k) { return MV_WAVES * (k == 2048 ? MV_ROWS_2048 : MV_ROWS_4096); }
 
