@@ -205,3 +205,34 @@ def test_decode_batch_long_contexts_auto_split(cuda):
     got = att.cpu().numpy()
     for s, p in enumerate(positions):
         assert_close(got[s], wants[s], f"seq {s} pos {p}")
+
+
+@pytest.mark.parametrize("store", ["f16", "bf16"])
+def test_decode_batch_64_sequences(cuda, store):
+    """The largest batch (64 sequences, every entry of the per-sequence tables the decode
+    kernel reads one per lane), full layer, positions from 0 to 4000 (one split each, or
+    several with the merge), the first and last sequences the longest; every sequence
+    equals the oracle."""
+    _say(f"decode batch of 64 sequences store={store}")
+    rng = np.random.default_rng(64)
+    qn, kn, sk = layer_weights(rng)
+    positions = [int(p) for p in rng.integers(0, 4001, 64)]
+    positions[0], positions[1], positions[63] = 4000, 0, 3999
+    n_slots = 4032
+    kv = fa.KVLayer(is_swa=False, has_rope=False, n_slots=n_slots, kv_dtype=store, q_norm=qn, k_norm=kn, sinks=sk,
+                    n_seq=64)
+    L = oracle_layer(kv, qn, kn, sk, store)
+    qkv = rng.standard_normal((64, QKV_DIM)).astype(np.float32)
+    wants = []
+    for s, p in enumerate(positions):
+        K, V = _history(rng, p + 1, store)
+        if p:
+            _fill_cache(kv, K[:p], V[:p], np.arange(p), s)
+        wants.append(fo.decode_step(L, qkv[s], p, K.copy(), V.copy(), n_threads=8))
+    dq = torch.from_numpy(qkv).to(cuda)
+    att = torch.zeros((64, Q_DIM), device=cuda)
+    kv.decode(dq, att, positions)
+    torch.cuda.synchronize()
+    got = att.cpu().numpy()
+    for s, p in enumerate(positions):
+        assert_close(got[s], wants[s], f"seq {s} pos {p}")
