@@ -243,18 +243,19 @@ __global__ __launch_bounds__(64 * MV_WAVES) void matvec_kernel(const MatvecParam
 #pragma unroll
         for (int k = 0; k < XPT / 4; k++) gv[k] = *(const f32x4 *)(norm_w + XPT * tid + 4 * k);
     }
-    // this wave's rows (quantised types; float rows are read in the dot loop)
+    // this wave's rows, as quantised-row units (float rows are read again in the dot loop;
+    // the units loaded here are within their rows and go unused). Every lane loads (lanes
+    // past the row's end re-read its last unit and do not store it), so the loads are
+    // unconditional and the RMSNorm below waits for x and the gains only.
     u32x4 u[R][UNITS];
     const int n_units = S.row_bytes >> 4;
-    if (!fl) {
 #pragma unroll
-        for (int r = 0; r < R; r++)
+    for (int r = 0; r < R; r++)
 #pragma unroll
-            for (int k = 0; k < UNITS; k++) {
-                const int idx = lane + 64 * k;
-                if (idx < n_units) u[r][k] = ((const u32x4 *)(wrow + (size_t)r * S.row_bytes))[idx];
-            }
-    }
+        for (int k = 0; k < UNITS; k++) {
+            const int idx = min(lane + 64 * k, n_units - 1);
+            u[r][k] = ((const u32x4 *)(wrow + (size_t)r * S.row_bytes))[idx];
+        }
     if (norm_w) {
         // RMSNorm as the CPU reference (ref_model.cpp:45-50): double sum of squares, float
         // scale, (x * scale) * g
