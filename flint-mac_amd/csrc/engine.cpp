@@ -63,6 +63,8 @@ struct Workspace {
     size_t bytes = 0;
     void *get(size_t need, bool zero = false) {
         if (need <= bytes) return ptr;
+        // earlier launches on any stream may still use the old buffer
+        if (ptr) check(hipDeviceSynchronize(), "hipDeviceSynchronize");
         if (ptr) check(hipFree(ptr), "hipFree");
         ptr = nullptr;
         bytes = 0;

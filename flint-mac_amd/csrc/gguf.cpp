@@ -200,7 +200,10 @@ File::File(const std::string &path) : path_(path) {
             t.type = in.type;
             t.dims = std::move(in.dims);
             uint64_t n = 1;
-            for (uint64_t d : t.dims) n *= d;
+            for (uint64_t d : t.dims) {
+                if (d != 0 && n > UINT64_MAX / d) throw std::runtime_error("tensor out of bounds: " + t.name);
+                n *= d;
+            }
             t.offset = data0 + in.rel;
             t.nbytes = n / g.elems * g.bytes;
             if (t.offset < data0 || t.offset + t.nbytes > size_ || t.offset + t.nbytes < t.offset)

@@ -162,6 +162,8 @@ struct flint_attn_model {
     }
     void reserve(int n_tok) {
         if (n_tok <= cap) return;
+        // earlier calls' kernels may still read the old buffers (they run on the callers' streams)
+        if (qkv || att) check(hipDeviceSynchronize(), "hipDeviceSynchronize");
         if (qkv) check(hipFree(qkv), "hipFree");
         if (att) check(hipFree(att), "hipFree");
         qkv = att = nullptr;
