@@ -53,9 +53,12 @@ constexpr int MERGE_MAX_SPLIT = 1024;
 // 32 lanes that write 16 bytes each spread evenly over the banks
 constexpr int ACC_ROW = HEAD_DIM + 4;
 
+// VS = V slices: the 128 output dims of a head split over VS workgroups (VS = 1 or 2). Each
+// workgroup computes every score (all of K) and the P*V product for its 128/VS dims.
+template <int VS>
 struct KvTile {
-    u32x4 k[2][4];  // K rows: sub-tile st, dim chunk c (8 packed 16-bit values each)
-    u32x4 v[8];     // V^T rows: dim tile d
+    u32x4 k[2][4];     // K rows: sub-tile st, dim chunk c (8 packed 16-bit values each)
+    u32x4 v[8 / VS];   // V^T rows: dim tile 8/VS * slice + d
 };
 
 // Issue the 16 loads of tile t (keys 32t .. 32t+31) for this lane: 1 KiB contiguous per
@@ -64,8 +67,9 @@ struct KvTile {
 // vector-offset form. A wave with no tile left (live == false) still issues the 16 loads,
 // which keeps the compiler's wait counts static, but every lane reads the tile's first
 // 16 bytes, so each costs one cache line instead of eight.
-__device__ inline void load_tile(KvTile &T, const uint16_t *__restrict__ kc, const uint16_t *__restrict__ vc,
-                                 int t, int lane, int slot_mask, bool live) {
+template <int VS>
+__device__ inline void load_tile(KvTile<VS> &T, const uint16_t *__restrict__ kc, const uint16_t *__restrict__ vc,
+                                 int t, int lane, int slot_mask, bool live, int slice) {
     const uint32_t base = ((uint32_t)(t * 32) & (uint32_t)slot_mask) * HEAD_DIM;
     // K: instruction (st, c) reads units (st*4 + c)*64 + lane: MFMA row n = lane & 15 holds
     // key 8(n>>2) + 4st + (n&3) of the tile, dims 32c + 8(lane>>4) .. +7
@@ -78,14 +82,15 @@ __device__ inline void load_tile(KvTile &T, const uint16_t *__restrict__ kc, con
     // V^T tile (8 KiB): row = dim 16d + n, keys 8g .. 8g+7 of the tile
     const uint32_t vo = base + (live ? (lane & 15) * 32 + 8 * (lane >> 4) : 0);
 #pragma unroll
-    for (int d = 0; d < 8; d++) T.v[d] = __builtin_nontemporal_load((const u32x4 *)(vc + vo + 16 * d * 32));
+    for (int d = 0; d < 8 / VS; d++)
+        T.v[d] = __builtin_nontemporal_load((const u32x4 *)(vc + vo + 16 * (8 / VS * slice + d) * 32));
 }
 
-template <int DT>
+template <int DT, int VS>
 struct DecodeState {
     typedef typename KvType<DT>::vec8 vec8;
-    float m, l;      // running max (log2 units) of this lane's head, this lane's partial sum
-    f32x4 acc[8];    // O^T tile d: rows = dims 16d + 4g + r, column = this lane's (head, hi/lo)
+    float m, l;          // running max (log2 units) of this lane's head, this lane's partial sum
+    f32x4 acc[8 / VS];   // O^T tile d: rows = slice dims 16d + 4g + r, column = this lane's (head, hi/lo)
 };
 
 // The running max is raised only when a score exceeds it by more than this (log2 units),
@@ -112,8 +117,8 @@ __device__ inline uint32_t split_pack<DT_BF16>(float p0, float p1, int hl) {
 }
 
 // Online-softmax update with one 32-key tile.
-template <int DT>
-__device__ inline void consume_tile(DecodeState<DT> &S, KvTile &T, const typename KvType<DT>::vec8 (&qb)[4], int t,
+template <int DT, int VS>
+__device__ inline void consume_tile(DecodeState<DT, VS> &S, KvTile<VS> &T, const typename KvType<DT>::vec8 (&qb)[4], int t,
                                     int k_begin, int pos, int g, int hl) {
     typedef KvType<DT> KT;
     f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
@@ -142,7 +147,7 @@ __device__ inline void consume_tile(DecodeState<DT> &S, KvTile &T, const typenam
             vmask[w] = (ok0 ? 0x0000ffffu : 0u) | (ok1 ? 0xffff0000u : 0u);
         }
 #pragma unroll
-        for (int d = 0; d < 8; d++)
+        for (int d = 0; d < 8 / VS; d++)
 #pragma unroll
             for (int w = 0; w < 4; w++) T.v[d][w] &= vmask[w];
     }
@@ -153,7 +158,7 @@ __device__ inline void consume_tile(DecodeState<DT> &S, KvTile &T, const typenam
         const float corr = __builtin_amdgcn_exp2f(S.m - m_new);
         S.l *= corr;
 #pragma unroll
-        for (int d = 0; d < 8; d++) S.acc[d] *= corr;
+        for (int d = 0; d < 8 / VS; d++) S.acc[d] *= corr;
         S.m = m_new;
     }
     float p[8];
@@ -164,10 +169,10 @@ __device__ inline void consume_tile(DecodeState<DT> &S, KvTile &T, const typenam
                       split_pack<DT>(p[6], p[7], hl)};
     const typename KT::vec8 pb = __builtin_bit_cast(typename KT::vec8, pu);
 #pragma unroll
-    for (int d = 0; d < 8; d++) S.acc[d] = KT::mfma16(__builtin_bit_cast(typename KT::vec8, T.v[d]), pb, S.acc[d]);
+    for (int d = 0; d < 8 / VS; d++) S.acc[d] = KT::mfma16(__builtin_bit_cast(typename KT::vec8, T.v[d]), pb, S.acc[d]);
 }
 
-template <int DT>
+template <int DT, int VS>
 __global__ __launch_bounds__(DEC_THREADS) void attn_decode_kernel(const DecodeParams P) {
     typedef KvType<DT> KT;
     typedef typename KT::vec8 vec8;
@@ -197,15 +202,16 @@ __global__ __launch_bounds__(DEC_THREADS) void attn_decode_kernel(const DecodePa
     asm volatile("" ::"v"(t_base), "v"(t_pos), "v"(t_tps), "v"(t_ns));
 
     // The grid is flat and holds exactly the launch's work units: sequence s owns workgroups
-    // wg_base[s] .. wg_base[s] + 4 n_split[s] - 1, kv head fastest. The hardware deals
-    // workgroups to the XCDs in id order, so equal-sized units spread every XCD's share of
-    // the stream evenly (a grid with idle slots skews it, and one XCD moves ~1.2 TB/s at most).
+    // wg_base[s] .. wg_base[s] + 4 VS n_split[s] - 1 (kv head fastest, then V slice, then
+    // split). The hardware deals workgroups to the XCDs in id order, so equal-sized units
+    // spread every XCD's share of the stream evenly (a grid with idle slots skews it, and one
+    // XCD moves ~1.2 TB/s at most).
     const int wid = blockIdx.x;
     const int seq = __builtin_popcountll(__builtin_amdgcn_ballot_w64(lane < n_seq && wid >= t_base)) - 1;
     const int n_split = __builtin_amdgcn_readlane(t_ns, seq), pos = __builtin_amdgcn_readlane(t_pos, seq);
     const int tps = __builtin_amdgcn_readlane(t_tps, seq);
     const int local = wid - __builtin_amdgcn_readlane(t_base, seq);
-    const int kvh = local & (N_HEAD_KV - 1), split = local / N_HEAD_KV;
+    const int kvh = local & (N_HEAD_KV - 1), slice = (local / N_HEAD_KV) % VS, split = local / (N_HEAD_KV * VS);
     if (seq < 0 || split >= n_split) return;  // not reached: the host sizes the grid exactly
     const bool last_split = split == n_split - 1;
     const int k_begin = is_swa ? max(pos - (window - 1), 0) : 0;
@@ -248,10 +254,10 @@ __global__ __launch_bounds__(DEC_THREADS) void attn_decode_kernel(const DecodePa
     // later load instructions stall at issue until the CU has room for them, so at long
     // contexts the prologue ends only as the stream does; the tiles land no earlier when
     // the prologue goes first, so nothing is gained by reordering.)
-    KvTile ta, tb;
+    KvTile<VS> ta, tb;
     int t_a = t_begin + wave, t_b = t_a + DEC_WAVES;
-    load_tile(ta, kc, vc, t_a < t_end ? t_a : t_begin, lane, slot_mask, t_a < t_end);
-    load_tile(tb, kc, vc, t_b < t_end ? t_b : t_begin, lane, slot_mask, t_b < t_end);
+    load_tile(ta, kc, vc, t_a < t_end ? t_a : t_begin, lane, slot_mask, t_a < t_end, slice);
+    load_tile(tb, kc, vc, t_b < t_end ? t_b : t_begin, lane, slot_mask, t_b < t_end, slice);
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- prologue: wave w normalises q head w (+ RoPE), the last split's last wave also
@@ -280,12 +286,14 @@ __global__ __launch_bounds__(DEC_THREADS) void attn_decode_kernel(const DecodePa
             sm_kv[1][lane] = KT::to_float(v0);
             sm_kv[1][lane + 64] = KT::to_float(v1);
             const int slot = pos & slot_mask;
+            if (slice == 0) {  // one V slice writes the token's K/V (every slice computes them)
             uint16_t *kw_ = k_cache + (size_t)seq * seq_stride;
             kw_[kt_index(kvh, slot, lane, n_slots)] = k0;
             kw_[kt_index(kvh, slot, lane + 64, n_slots)] = k1;
             uint16_t *vw = v_cache + (size_t)seq * seq_stride;
             vw[vt_index(kvh, slot, lane, n_slots)] = v0;
             vw[vt_index(kvh, slot, lane + 64, n_slots)] = v1;
+            }
         }
     }
     lds_barrier();  // the q operands are in LDS; the tile loads stay in flight
@@ -304,39 +312,39 @@ __global__ __launch_bounds__(DEC_THREADS) void attn_decode_kernel(const DecodePa
     }
 
     // ---- stream this wave's tiles t_begin + wave + 8i, two in flight ----
-    DecodeState<DT> S;
+    DecodeState<DT, VS> S;
     S.m = -1e30f;
     S.l = 0.f;
 #pragma unroll
-    for (int d = 0; d < 8; d++) S.acc[d] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int d = 0; d < 8 / VS; d++) S.acc[d] = f32x4{0.f, 0.f, 0.f, 0.f};
     // Two register sets, each refilled with the tile 16 further on as soon as it is
     // consumed. The steady-state loop runs while both refills are needed, so its loads
     // are unconditional and the wait counts static (consuming a tile waits for its own
     // 16 loads only); the drain then handles the last two or three tiles, issuing no
     // load that will not be consumed except in the three-tile case.
     while (t_b + 2 * DEC_WAVES < t_end) {
-        consume_tile<DT>(S, ta, qb, t_a, k_begin, pos, g, hl);
+        consume_tile<DT, VS>(S, ta, qb, t_a, k_begin, pos, g, hl);
         t_a += 2 * DEC_WAVES;
-        load_tile(ta, kc, vc, t_a, lane, slot_mask, true);
-        consume_tile<DT>(S, tb, qb, t_b, k_begin, pos, g, hl);
+        load_tile(ta, kc, vc, t_a, lane, slot_mask, true, slice);
+        consume_tile<DT, VS>(S, tb, qb, t_b, k_begin, pos, g, hl);
         t_b += 2 * DEC_WAVES;
-        load_tile(tb, kc, vc, t_b, lane, slot_mask, true);
+        load_tile(tb, kc, vc, t_b, lane, slot_mask, true, slice);
     }
     if (t_a < t_end) {
-        consume_tile<DT>(S, ta, qb, t_a, k_begin, pos, g, hl);
+        consume_tile<DT, VS>(S, ta, qb, t_a, k_begin, pos, g, hl);
         t_a += 2 * DEC_WAVES;
         const bool third = t_a < t_end;
         // unconditional (16 bytes per load when there is no third tile): tile b's wait
         // stays exact while the third tile streams in
-        load_tile(ta, kc, vc, third ? t_a : t_begin, lane, slot_mask, third);
-        if (t_b < t_end) consume_tile<DT>(S, tb, qb, t_b, k_begin, pos, g, hl);
-        if (third) consume_tile<DT>(S, ta, qb, t_a, k_begin, pos, g, hl);
+        load_tile(ta, kc, vc, third ? t_a : t_begin, lane, slot_mask, third, slice);
+        if (t_b < t_end) consume_tile<DT, VS>(S, tb, qb, t_b, k_begin, pos, g, hl);
+        if (third) consume_tile<DT, VS>(S, ta, qb, t_a, k_begin, pos, g, hl);
     }
 
     // ---- merge hi/lo columns and the waves (and the current token) through LDS ----
     S.l = xor32_sum(xor16_sum(S.l));
 #pragma unroll
-    for (int d = 0; d < 8; d++) {
+    for (int d = 0; d < 8 / VS; d++) {
         f32x4 v;
 #pragma unroll
         for (int r = 0; r < 4; r++) v[r] = S.acc[d][r] + lane_xor8(S.acc[d][r]);
@@ -349,8 +357,9 @@ __global__ __launch_bounds__(DEC_THREADS) void attn_decode_kernel(const DecodePa
     lds_barrier();
 
     // wave th merges head th: 8 wave partials + the current token, branch-free (a wave
-    // without keys has m = -1e30 and l = 0, so its weight is 0)
-    const int th = wave, d2 = lane * 2;
+    // without keys has m = -1e30 and l = 0, so its weight is 0). Lane pairs of dims d2, d2+1
+    // of this V slice's 128/VS dims (with VS = 2 the upper lanes read unused LDS and store nothing)
+    const int th = wave, d2 = lane * 2, dg = HEAD_DIM / VS * slice + d2;
     float mw[DEC_WAVES + 1], lw[DEC_WAVES + 1];
 #pragma unroll
     for (int w = 0; w < DEC_WAVES; w++) {
@@ -374,17 +383,18 @@ __global__ __launch_bounds__(DEC_THREADS) void attn_decode_kernel(const DecodePa
     if (last_split) {  // sm_kv is written only in the last split: elsewhere it is stale LDS
         const float c = __builtin_amdgcn_exp2f(mw[DEC_WAVES] - M);
         L += lw[DEC_WAVES] * c;
-        A0 += sm_kv[1][d2] * c;
-        A1 += sm_kv[1][d2 + 1] * c;
+        A0 += sm_kv[1][dg & (HEAD_DIM - 1)] * c;
+        A1 += sm_kv[1][(dg + 1) & (HEAD_DIM - 1)] * c;
     }
     const int hout = kvh * GQA + th;
     if (n_split == 1) {
-        float *out = att + (size_t)seq * Q_DIM + hout * HEAD_DIM + d2;
+        float *out = att + (size_t)seq * Q_DIM + hout * HEAD_DIM + dg;
         const float Mf = fmaxf(M, sink), cs = __builtin_amdgcn_exp2f(M - Mf);
         const float inv = 1.0f / (L * cs + __builtin_amdgcn_exp2f(sink - Mf));
-        *(float2 *)out = make_float2(A0 * cs * inv, A1 * cs * inv);
+        if (d2 < HEAD_DIM / VS) *(float2 *)out = make_float2(A0 * cs * inv, A1 * cs * inv);
         return;
     }
+    if constexpr (VS > 1) return;  // not reached: V slices are planned for one split per sequence
     float *pp = partial + (((size_t)seq * N_HEAD + hout) * max_split + split) * PART_STRIDE;
     *(float2 *)(pp + d2) = make_float2(A0, A1);
     if (lane == 0) *(float2 *)(pp + HEAD_DIM) = make_float2(M, L);
@@ -466,10 +476,14 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const DecodeParams P)
 
 hipError_t launch_decode(const DecodeParams &P, int dtype, hipStream_t stream) {
     dim3 grid(P.wg_base[P.n_seq]), block(DEC_THREADS);
-    if (dtype == DT_F16)
-        hipLaunchKernelGGL(attn_decode_kernel<DT_F16>, grid, block, 0, stream, P);
+    if (dtype == DT_F16 && P.v_slices == 2)
+        hipLaunchKernelGGL((attn_decode_kernel<DT_F16, 2>), grid, block, 0, stream, P);
+    else if (dtype == DT_F16)
+        hipLaunchKernelGGL((attn_decode_kernel<DT_F16, 1>), grid, block, 0, stream, P);
+    else if (P.v_slices == 2)
+        hipLaunchKernelGGL((attn_decode_kernel<DT_BF16, 2>), grid, block, 0, stream, P);
     else
-        hipLaunchKernelGGL(attn_decode_kernel<DT_BF16>, grid, block, 0, stream, P);
+        hipLaunchKernelGGL((attn_decode_kernel<DT_BF16, 1>), grid, block, 0, stream, P);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (P.max_split > 1) {

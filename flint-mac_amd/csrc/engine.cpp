@@ -184,11 +184,15 @@ void decode_impl(const flint_attn_layer *L, int n_seq, int64_t seq_stride, const
     }
     plan_splits(n_seq, tiles, keys_per_split, P.n_split, P.tps);
     int max_split = 1;
+    for (int s = 0; s < n_seq; s++) max_split = std::max(max_split, P.n_split[s]);
+    // One split per sequence (short key ranges, SWA layers): one CU streams each kv head's
+    // keys (~63 GB/s at most per CU), so two workgroups per kv head, each reading all of K
+    // and half of V, shorten the stream without a merge; the K both read comes from L2/MALL.
+    P.v_slices = max_split == 1 && n_seq * N_HEAD_KV * 2 <= 256 ? 2 : 1;
     P.wg_base[0] = 0;
     for (int s = 0; s < n_seq; s++) {
         P.pos[s] = pos[s];
-        max_split = std::max(max_split, P.n_split[s]);
-        P.wg_base[s + 1] = P.wg_base[s] + N_HEAD_KV * P.n_split[s];
+        P.wg_base[s + 1] = P.wg_base[s] + N_HEAD_KV * P.v_slices * P.n_split[s];
     }
     for (int s = n_seq + 1; s <= MAX_SEQ; s++) P.wg_base[s] = P.wg_base[n_seq];
     P.max_split = max_split;
