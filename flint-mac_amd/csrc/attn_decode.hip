@@ -53,7 +53,7 @@ constexpr int MERGE_MAX_SPLIT = 1024;
 // 32 lanes that write 16 bytes each spread evenly over the banks
 constexpr int ACC_ROW = HEAD_DIM + 4;
 
-// VS = V slices: the 128 output dims of a head split over VS workgroups (VS = 1 or 2). Each
+// VS = V slices: the 128 output dims of a head split over VS workgroups (VS = 1, 2 or 4). Each
 // workgroup computes every score (all of K) and the P*V product for its 128/VS dims.
 template <int VS>
 struct KvTile {
@@ -358,7 +358,7 @@ __global__ __launch_bounds__(DEC_THREADS) void attn_decode_kernel(const DecodePa
 
     // wave th merges head th: 8 wave partials + the current token, branch-free (a wave
     // without keys has m = -1e30 and l = 0, so its weight is 0). Lane pairs of dims d2, d2+1
-    // of this V slice's 128/VS dims (with VS = 2 the upper lanes read unused LDS and store nothing)
+    // of this V slice's 128/VS dims (with VS > 1 the upper lanes read unused LDS and store nothing)
     const int th = wave, d2 = lane * 2, dg = HEAD_DIM / VS * slice + d2;
     float mw[DEC_WAVES + 1], lw[DEC_WAVES + 1];
 #pragma unroll
@@ -476,7 +476,11 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const DecodeParams P)
 
 hipError_t launch_decode(const DecodeParams &P, int dtype, hipStream_t stream) {
     dim3 grid(P.wg_base[P.n_seq]), block(DEC_THREADS);
-    if (dtype == DT_F16 && P.v_slices == 2)
+    if (dtype == DT_F16 && P.v_slices == 4)
+        hipLaunchKernelGGL((attn_decode_kernel<DT_F16, 4>), grid, block, 0, stream, P);
+    else if (dtype == DT_BF16 && P.v_slices == 4)
+        hipLaunchKernelGGL((attn_decode_kernel<DT_BF16, 4>), grid, block, 0, stream, P);
+    else if (dtype == DT_F16 && P.v_slices == 2)
         hipLaunchKernelGGL((attn_decode_kernel<DT_F16, 2>), grid, block, 0, stream, P);
     else if (dtype == DT_F16)
         hipLaunchKernelGGL((attn_decode_kernel<DT_F16, 1>), grid, block, 0, stream, P);

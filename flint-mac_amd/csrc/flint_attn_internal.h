@@ -32,8 +32,8 @@ struct DecodeParams {
     int n_split[MAX_SEQ];       // key splits of sequence s
     int tps[MAX_SEQ];           // 32-key tiles per split of sequence s
     int wg_base[MAX_SEQ + 1];   // first workgroup of sequence s (4 x v_slices per split); [n_seq] = grid size
-    int v_slices;               // 1, or 2 when every sequence has one split: a head's 128 output
-                                // dims in two workgroups (each reads all of K and half of V)
+    int v_slices;               // 1, or 2 / 4 when every sequence has one split: a head's 128 output
+                                // dims in that many workgroups (each reads all of K and its part of V)
 };
 
 hipError_t launch_decode(const DecodeParams &P, int dtype, hipStream_t stream);
