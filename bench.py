@@ -33,7 +33,7 @@ N_FULL_FLINT, N_SWA_FLINT = 14, 35
 # HBM bytes per decode call (attn_decode_kernel + attn_combine_kernel) at 32k, from rocprofv3
 # --pmc FETCH_SIZE and WRITE_SIZE runs of `bench.py --only decode --no-cpu`, each scaled by the
 # counter's reading for the 64 MiB calibration copy (profiles/decode_32k_f16.md).
-DECODE_TRAFFIC_BYTES = 68904576
+DECODE_TRAFFIC_BYTES = 68915950
 
 
 def log(msg):
