@@ -236,3 +236,46 @@ def test_decode_batch_64_sequences(cuda, store):
     got = att.cpu().numpy()
     for s, p in enumerate(positions):
         assert_close(got[s], wants[s], f"seq {s} pos {p}")
+
+
+@pytest.mark.parametrize("store", ["f16", "bf16"])
+@pytest.mark.parametrize("n_seq", [16, 24])
+def test_decode_batch_swa_v_slices(cuda, store, n_seq):
+    """Batched SWA decode with V slices: every sequence has one split, so each kv head's
+    output dims are cut over 4 workgroups (16 sequences: 256 workgroups) or 2 (24
+    sequences: 4 would exceed 256). Positions before, at and past the ring wrap, and 0;
+    every sequence equals the oracle; the current token's K/V land in its ring slot, and
+    every other slot of the sequence's ring keeps what it held."""
+    _say(f"decode batch SWA v-slices n_seq={n_seq} store={store}")
+    rng = np.random.default_rng(100 + n_seq)
+    qn, kn, sk = layer_weights(rng)
+    positions = [int(p) for p in rng.integers(1, 2600, n_seq)]
+    positions[0], positions[1], positions[2] = 0, 1023, 1024
+    kv = fa.KVLayer(is_swa=True, has_rope=True, n_slots=1024, kv_dtype=store, q_norm=qn, k_norm=kn, sinks=sk,
+                    n_seq=n_seq)
+    L = oracle_layer(kv, qn, kn, sk, store)
+    qkv = rng.standard_normal((n_seq, QKV_DIM)).astype(np.float32)
+    wants, rings = [], []
+    for s, p in enumerate(positions):
+        K, V = _history(rng, p + 1, store)
+        first = max(0, p - 1023)
+        if p:
+            _fill_cache(kv, K[first:p], V[first:p], np.arange(first, p) & 1023, s)
+        Kc, Vc = K.copy(), V.copy()
+        wants.append(fo.decode_step(L, qkv[s], p, Kc, Vc, n_threads=8))
+        rings.append((Kc, Vc, first))
+    dq = torch.from_numpy(qkv).to(cuda)
+    att = torch.zeros((n_seq, Q_DIM), device=cuda)
+    kv.decode(dq, att, positions)
+    torch.cuda.synchronize()
+    got = att.cpu().numpy()
+    vcs = kv.v_slots().float().cpu().numpy()  # [n_seq][4][1024][128]
+    kcs = kv.k_slots().float().cpu().numpy()
+    for s, p in enumerate(positions):
+        assert_close(got[s], wants[s], f"seq {s} pos {p}")
+        Kc, Vc, first = rings[s]
+        ring = np.zeros((1024, KV_DIM), np.float32)
+        ring[np.arange(first, p + 1) & 1023] = Vc[first:p + 1]
+        assert np.array_equal(vcs[s].transpose(1, 0, 2).reshape(1024, KV_DIM), ring), f"seq {s}: V ring"
+        cur = p & 1023
+        assert k_close(kcs[s][:, cur, :], Kc[p].reshape(N_HEAD_KV, HEAD_DIM), store), f"seq {s}: K slot {cur}"
