@@ -365,9 +365,9 @@ def main():
                          "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(d["bytes_per_launch"] / (t_full * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                          "traffic": DECODE_TRAFFIC_BYTES,
-                         "kernel": "one flint_attn_decode call = attn_decode_kernel<f16> (43 key splits x 4 kv "
-                                   "heads = 172 workgroups) + attn_combine_kernel (split merge); time per call "
-                                   "from HIP events",
+                         "kernel": "one flint_attn_decode call = attn_decode_kernel<1, 1> (f16 KV, no V slices; 43 key "
+                                   "splits x 4 kv heads = 172 workgroups) + attn_combine_kernel (split merge); "
+                                   "time per call from HIP events",
                          "bytes_per_launch": d["bytes_per_launch"], "host_bound": d["host_bound"]},
         })
     if "prefill" in res:
