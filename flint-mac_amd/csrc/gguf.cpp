@@ -1,9 +1,16 @@
-// GGUF v3 reader (see gguf.h). Layout of a GGUF file:
-//   u32 magic "GGUF", u32 version, u64 n_tensors, u64 n_kv,
-//   n_kv x (string key, u32 value type, value),
-//   n_tensors x (string name, u32 n_dims, u64 dims[n_dims], u32 ggml type, u64 offset),
-//   padding to general.alignment, then the data section (offsets are relative to it).
-// Strings are u64 length + bytes; arrays are u32 element type + u64 count + elements.
+// GGUF v3 reader (see gguf.h), written from the format description:
+//
+//   header      u32 magic "GGUF" | u32 version | u64 tensor count | u64 key/value count
+//   key/values  string key | u32 value type | value
+//   tensor info string name | u32 rank | u64 dims[rank] | u32 ggml type | u64 offset
+//   padding     to general.alignment (32 when the key is absent)
+//   data        tensor offsets are relative to its start
+//
+// Strings are a u64 byte count and the bytes; an array is a u32 element type, a u64
+// count and the elements. Every scalar metadata type is a fixed-width little-endian
+// number, so one table (width and class per type id) drives the decoding of scalars
+// and of scalar arrays alike. Error texts are the ones the reference's reader gives
+// (/root/reference/src/gguf.cpp), so callers see the same messages.
 #include "gguf.h"
 
 #include <fcntl.h>
@@ -18,10 +25,28 @@ namespace flint {
 namespace gguf {
 namespace {
 
-// metadata value types of the format
-enum : uint32_t {
-    T_U8, T_I8, T_U16, T_I16, T_U32, T_I32, T_F32, T_BOOL, T_STRING, T_ARRAY, T_U64, T_I64, T_F64,
+using std::runtime_error;
+
+// ---- metadata value types -------------------------------------------------------------
+
+enum Class : uint8_t { NONE, UNSIGNED, SIGNED, REAL, FLAG };
+struct Scalar {
+    uint8_t width;  // bytes in the file
+    Class cls;
 };
+constexpr uint32_t kString = 8, kArray = 9;
+// indexed by the format's value-type id; ids 8 (string) and 9 (array) are not scalars
+constexpr Scalar kScalars[] = {
+    {1, UNSIGNED}, {1, SIGNED}, {2, UNSIGNED}, {2, SIGNED}, {4, UNSIGNED}, {4, SIGNED}, {4, REAL},
+    {1, FLAG},     {0, NONE},   {0, NONE},     {8, UNSIGNED}, {8, SIGNED}, {8, REAL},
+};
+constexpr uint32_t kNumTypes = sizeof(kScalars) / sizeof(kScalars[0]);
+
+const Scalar *scalar_of(uint32_t type) {
+    return type < kNumTypes && kScalars[type].cls != NONE ? &kScalars[type] : nullptr;
+}
+
+// ---- ggml tensor types ----------------------------------------------------------------
 
 struct TypeRow {
     uint32_t id;
@@ -37,102 +62,136 @@ constexpr TypeRow kTypes[] = {
     {23, "IQ4_XS", {256, 136}},  {29, "IQ1_M", {256, 56}},  {30, "BF16", {1, 2}},
 };
 
-class Reader {
-public:
-    Reader(const uint8_t *p, size_t n) : p_(p), end_(p + n), begin_(p) {}
-    template <typename T>
-    T get() {
-        need(sizeof(T));
-        T v;
-        std::memcpy(&v, p_, sizeof(T));
-        p_ += sizeof(T);
-        return v;
-    }
-    std::string str() {
-        const uint64_t n = get<uint64_t>();
-        need(n);
-        std::string s((const char *)p_, (size_t)n);
-        p_ += n;
-        return s;
-    }
-    uint64_t offset() const { return (uint64_t)(p_ - begin_); }
+const TypeRow *type_row(uint32_t id) {
+    for (const TypeRow &t : kTypes)
+        if (t.id == id) return &t;
+    return nullptr;
+}
 
-private:
-    void need(uint64_t n) const {
-        if ((uint64_t)(end_ - p_) < n) throw std::runtime_error("gguf: unexpected end of file");
+// ---- the byte stream ------------------------------------------------------------------
+
+// A window over the mapped file that hands out byte ranges front to back.
+struct Span {
+    const uint8_t *at, *end;
+
+    const uint8_t *take(uint64_t n) {
+        if ((uint64_t)(end - at) < n) throw runtime_error("gguf: unexpected end of file");
+        const uint8_t *p = at;
+        at += n;
+        return p;
     }
-    const uint8_t *p_, *end_, *begin_;
+    uint64_t left() const { return (uint64_t)(end - at); }
+    uint32_t u32() { return (uint32_t)bits(take(4), 4); }
+    uint64_t u64() { return bits(take(8), 8); }
+    std::string text() {
+        const uint64_t n = u64();
+        return std::string((const char *)take(n), (size_t)n);
+    }
+    static uint64_t bits(const uint8_t *p, int width) {
+        uint64_t u = 0;
+        std::memcpy(&u, p, width);  // the format is little-endian, as is the host
+        return u;
+    }
 };
 
-bool integral(uint32_t t) {
-    return t == T_U8 || t == T_I8 || t == T_U16 || t == T_I16 || t == T_U32 || t == T_I32 || t == T_U64 ||
-           t == T_I64;
+// One fixed-width scalar (bytes at p) as an integer, a real or a flag.
+int64_t to_int(const uint8_t *p, const Scalar &s) {
+    const uint64_t u = Span::bits(p, s.width);
+    if (s.cls == SIGNED && s.width < 8) {
+        const int shift = 64 - 8 * s.width;
+        return (int64_t)(u << shift) >> shift;
+    }
+    return (int64_t)u;
+}
+double to_real(const uint8_t *p, const Scalar &s) {
+    if (s.width == 4) {
+        float f;
+        std::memcpy(&f, p, 4);
+        return f;
+    }
+    double d;
+    std::memcpy(&d, p, 8);
+    return d;
 }
 
-int64_t get_integral(Reader &r, uint32_t t) {
-    switch (t) {
-        case T_U8: return r.get<uint8_t>();
-        case T_I8: return r.get<int8_t>();
-        case T_U16: return r.get<uint16_t>();
-        case T_I16: return r.get<int16_t>();
-        case T_U32: return r.get<uint32_t>();
-        case T_I32: return r.get<int32_t>();
-        case T_U64: return (int64_t)r.get<uint64_t>();
-        default: return r.get<int64_t>();
+// Append one scalar to the value: a scalar value when `array` is false, an element of
+// the array of that class otherwise.
+void put(Value &v, const uint8_t *p, const Scalar &s, bool array) {
+    switch (s.cls) {
+        case UNSIGNED:
+        case SIGNED:
+            if (array) v.ia.push_back(to_int(p, s)); else v.i = to_int(p, s);
+            break;
+        case REAL:
+            if (array) v.fa.push_back(to_real(p, s)); else v.f = to_real(p, s);
+            break;
+        default:
+            if (array) v.ba.push_back(*p != 0); else v.b = *p != 0;
+            break;
     }
 }
 
-Value get_value(Reader &r, uint32_t t) {
+Value::Kind kind_of(Class c, bool array) {
+    switch (c) {
+        case UNSIGNED:
+        case SIGNED: return array ? Value::INT_ARRAY : Value::INT;
+        case REAL: return array ? Value::FLOAT_ARRAY : Value::FLOAT;
+        default: return array ? Value::BOOL_ARRAY : Value::BOOL;
+    }
+}
+
+Value decode(Span &in, uint32_t type) {
     Value v;
-    if (integral(t)) {
-        v.kind = Value::INT;
-        v.i = get_integral(r, t);
+    if (const Scalar *s = scalar_of(type)) {
+        v.kind = kind_of(s->cls, false);
+        put(v, in.take(s->width), *s, false);
         return v;
     }
-    switch (t) {
-        case T_F32: v.kind = Value::FLOAT; v.f = r.get<float>(); return v;
-        case T_F64: v.kind = Value::FLOAT; v.f = r.get<double>(); return v;
-        case T_BOOL: v.kind = Value::BOOL; v.b = r.get<uint8_t>() != 0; return v;
-        case T_STRING: v.kind = Value::STRING; v.s = r.str(); return v;
-        case T_ARRAY: {
-            const uint32_t et = r.get<uint32_t>();
-            const uint64_t n = r.get<uint64_t>();
-            if (integral(et)) {
-                v.kind = Value::INT_ARRAY;
-                for (uint64_t k = 0; k < n; k++) v.ia.push_back(get_integral(r, et));
-            } else if (et == T_F32 || et == T_F64) {
-                v.kind = Value::FLOAT_ARRAY;
-                for (uint64_t k = 0; k < n; k++) v.fa.push_back(et == T_F32 ? r.get<float>() : r.get<double>());
-            } else if (et == T_BOOL) {
-                v.kind = Value::BOOL_ARRAY;
-                for (uint64_t k = 0; k < n; k++) v.ba.push_back(r.get<uint8_t>() != 0);
-            } else if (et == T_STRING) {
-                v.kind = Value::STRING_ARRAY;
-                for (uint64_t k = 0; k < n; k++) v.sa.push_back(r.str());
-            } else {
-                throw std::runtime_error("gguf: unsupported array element type");
-            }
-            return v;
-        }
+    if (type == kString) {
+        v.kind = Value::STRING;
+        v.s = in.text();
+        return v;
     }
-    throw std::runtime_error("gguf: unknown metadata type " + std::to_string(t));
+    if (type != kArray) throw runtime_error("gguf: unknown metadata type " + std::to_string(type));
+    const uint32_t elem = in.u32();
+    const uint64_t count = in.u64();
+    if (const Scalar *s = scalar_of(elem)) {
+        // the whole array must be in the file before anything is allocated for it
+        if (count > in.left() / s->width) throw runtime_error("gguf: unexpected end of file");
+        v.kind = kind_of(s->cls, true);
+        const uint8_t *p = in.take(count * s->width);
+        for (uint64_t k = 0; k < count; k++) put(v, p + k * s->width, *s, true);
+        return v;
+    }
+    if (elem != kString) throw runtime_error("gguf: unsupported array element type");
+    v.kind = Value::STRING_ARRAY;
+    for (uint64_t k = 0; k < count; k++) v.sa.push_back(in.text());
+    return v;
+}
+
+// Bytes of a tensor of the given dims in blocks of geometry g, or throws.
+uint64_t tensor_bytes(const std::vector<uint64_t> &dims, const BlockGeom &g, const std::string &name) {
+    uint64_t n = 1;
+    for (uint64_t d : dims) {
+        if (d != 0 && n > UINT64_MAX / d) throw runtime_error("tensor out of bounds: " + name);
+        n *= d;
+    }
+    const uint64_t blocks = n / g.elems;
+    if (n % g.elems != 0 || blocks > UINT64_MAX / g.bytes) throw runtime_error("tensor out of bounds: " + name);
+    return blocks * g.bytes;
 }
 
 }  // namespace
 
 bool block_geom(uint32_t type, BlockGeom *g) {
-    for (const TypeRow &t : kTypes)
-        if (t.id == type) {
-            *g = t.geom;
-            return true;
-        }
-    return false;
+    const TypeRow *t = type_row(type);
+    if (t) *g = t->geom;
+    return t != nullptr;
 }
 
 const char *type_name(uint32_t type) {
-    for (const TypeRow &t : kTypes)
-        if (t.id == type) return t.name;
-    return "?";
+    const TypeRow *t = type_row(type);
+    return t ? t->name : "?";
 }
 
 uint64_t Tensor::n_rows() const {
@@ -142,80 +201,75 @@ uint64_t Tensor::n_rows() const {
 }
 
 uint64_t Tensor::row_bytes() const {
-    BlockGeom g{};
-    block_geom(type, &g);
-    return dims.empty() ? 0 : dims[0] / g.elems * g.bytes;
+    const TypeRow *t = type_row(type);
+    return dims.empty() || !t ? 0 : dims[0] / t->geom.elems * t->geom.bytes;
 }
 
 File::File(const std::string &path) : path_(path) {
     fd_ = ::open(path.c_str(), O_RDONLY);
-    if (fd_ < 0) throw std::runtime_error("cannot open " + path);
     struct stat st {};
-    if (fstat(fd_, &st) != 0) {
-        ::close(fd_);
-        throw std::runtime_error("cannot open " + path);
+    if (fd_ < 0 || fstat(fd_, &st) != 0) {
+        if (fd_ >= 0) ::close(fd_);
+        throw runtime_error("cannot open " + path);
     }
     size_ = (size_t)st.st_size;
-    void *m = size_ ? mmap(nullptr, size_, PROT_READ, MAP_SHARED, fd_, 0) : MAP_FAILED;
+    if (size_ == 0) {
+        ::close(fd_);
+        throw runtime_error("gguf: unexpected end of file");
+    }
+    void *m = mmap(nullptr, size_, PROT_READ, MAP_SHARED, fd_, 0);
     if (m == MAP_FAILED) {
         ::close(fd_);
-        if (size_ == 0) throw std::runtime_error("gguf: unexpected end of file");
-        throw std::runtime_error("mmap failed: " + path);
+        throw runtime_error("mmap failed: " + path);
     }
     base_ = (const uint8_t *)m;
     try {
-        Reader r(base_, size_);
-        if (r.get<uint32_t>() != 0x46554747u) throw std::runtime_error("not a GGUF file: " + path);
-        if (r.get<uint32_t>() < 3) throw std::runtime_error("unsupported GGUF version");
-        const uint64_t n_tensors = r.get<uint64_t>(), n_kv = r.get<uint64_t>();
-        for (uint64_t k = 0; k < n_kv; k++) {
-            std::string key = r.str();
-            const uint32_t t = r.get<uint32_t>();
-            meta_[key] = get_value(r, t);
-        }
-        struct Info {
-            std::string name;
-            std::vector<uint64_t> dims;
-            uint32_t type;
-            uint64_t rel;
-        };
-        std::vector<Info> infos;
-        for (uint64_t k = 0; k < n_tensors; k++) {
-            Info in;
-            in.name = r.str();
-            const uint32_t nd = r.get<uint32_t>();
-            for (uint32_t d = 0; d < nd; d++) in.dims.push_back(r.get<uint64_t>());
-            in.type = r.get<uint32_t>();
-            in.rel = r.get<uint64_t>();
-            infos.push_back(std::move(in));
-        }
-        const uint64_t align = has("general.alignment") ? (uint64_t)get_int("general.alignment") : 32;
-        if (align == 0) throw std::runtime_error("gguf: general.alignment is 0");
-        const uint64_t data0 = (r.offset() + align - 1) / align * align;
-        for (Info &in : infos) {
-            BlockGeom g{};
-            if (!block_geom(in.type, &g)) throw std::runtime_error("unsupported ggml type " + std::to_string(in.type));
-            Tensor t;
-            t.name = std::move(in.name);
-            t.type = in.type;
-            t.dims = std::move(in.dims);
-            uint64_t n = 1;
-            for (uint64_t d : t.dims) {
-                if (d != 0 && n > UINT64_MAX / d) throw std::runtime_error("tensor out of bounds: " + t.name);
-                n *= d;
-            }
-            t.offset = data0 + in.rel;
-            t.nbytes = n / g.elems * g.bytes;
-            if (t.offset < data0 || t.offset + t.nbytes > size_ || t.offset + t.nbytes < t.offset)
-                throw std::runtime_error("tensor out of bounds: " + t.name);
-            t.data = base_ + t.offset;
-            index_[t.name] = tensors_.size();
-            tensors_.push_back(std::move(t));
-        }
+        parse();
     } catch (...) {
         munmap((void *)base_, size_);
         ::close(fd_);
         throw;
+    }
+}
+
+void File::parse() {
+    Span in{base_, base_ + size_};
+    if (in.u32() != 0x46554747u) throw runtime_error("not a GGUF file: " + path_);
+    if (in.u32() < 3) throw runtime_error("unsupported GGUF version");
+    const uint64_t n_tensors = in.u64(), n_kv = in.u64();
+    for (uint64_t k = 0; k < n_kv; k++) {
+        std::string key = in.text();
+        const uint32_t type = in.u32();
+        meta_[std::move(key)] = decode(in, type);
+    }
+    // The tensor table. `offset` holds the offset into the data section until the
+    // section's start is known (it follows the table, aligned).
+    for (uint64_t k = 0; k < n_tensors; k++) {
+        Tensor t;
+        t.name = in.text();
+        const uint32_t rank = in.u32();
+        if (rank > in.left() / 8) throw runtime_error("gguf: unexpected end of file");
+        t.dims.resize(rank);
+        for (uint64_t &d : t.dims) d = in.u64();
+        t.type = in.u32();
+        t.offset = in.u64();
+        tensors_.push_back(std::move(t));
+    }
+    const uint64_t align = has("general.alignment") ? (uint64_t)get_int("general.alignment") : 32;
+    if (align == 0) throw runtime_error("gguf: general.alignment is 0");
+    const uint64_t table_end = (uint64_t)(in.at - base_);
+    const uint64_t data0 = (table_end + align - 1) / align * align;
+    for (size_t i = 0; i < tensors_.size(); i++) {
+        Tensor &t = tensors_[i];
+        const TypeRow *row = type_row(t.type);
+        if (!row) throw runtime_error("unsupported ggml type " + std::to_string(t.type));
+        t.nbytes = tensor_bytes(t.dims, row->geom, t.name);
+        const uint64_t rel = t.offset;
+        t.offset = data0 + rel;
+        if (t.offset < rel || t.offset > size_ || t.nbytes > size_ - t.offset)
+            throw runtime_error("tensor out of bounds: " + t.name);
+        t.data = base_ + t.offset;
+        index_[t.name] = i;
     }
 }
 
@@ -226,43 +280,30 @@ File::~File() {
 
 const Value &File::value(const std::string &key) const {
     auto it = meta_.find(key);
-    if (it == meta_.end()) throw std::runtime_error("gguf: missing key " + key);
+    if (it == meta_.end()) throw runtime_error("gguf: missing key " + key);
     return it->second;
 }
 
-static std::runtime_error wrong_type(const std::string &key) {
-    return std::runtime_error("gguf: key " + key + " has the wrong type");
+// a value of the expected kind, or "gguf: key ... has the wrong type"
+const Value &File::typed(const std::string &key, int kind) const {
+    const Value &v = value(key);
+    if (v.kind != kind) throw runtime_error("gguf: key " + key + " has the wrong type");
+    return v;
 }
 
-int64_t File::get_int(const std::string &key) const {
-    const Value &v = value(key);
-    if (v.kind != Value::INT) throw wrong_type(key);
-    return v.i;
-}
+int64_t File::get_int(const std::string &key) const { return typed(key, Value::INT).i; }
 
 double File::get_float(const std::string &key) const {
     const Value &v = value(key);
-    if (v.kind == Value::INT) return (double)v.i;
-    if (v.kind != Value::FLOAT) throw wrong_type(key);
-    return v.f;
+    return v.kind == Value::INT ? (double)v.i : typed(key, Value::FLOAT).f;
 }
 
-bool File::get_bool(const std::string &key) const {
-    const Value &v = value(key);
-    if (v.kind != Value::BOOL) throw wrong_type(key);
-    return v.b;
-}
+bool File::get_bool(const std::string &key) const { return typed(key, Value::BOOL).b; }
 
-const std::string &File::get_string(const std::string &key) const {
-    const Value &v = value(key);
-    if (v.kind != Value::STRING) throw wrong_type(key);
-    return v.s;
-}
+const std::string &File::get_string(const std::string &key) const { return typed(key, Value::STRING).s; }
 
 const std::vector<uint8_t> &File::get_bool_array(const std::string &key) const {
-    const Value &v = value(key);
-    if (v.kind != Value::BOOL_ARRAY) throw wrong_type(key);
-    return v.ba;
+    return typed(key, Value::BOOL_ARRAY).ba;
 }
 
 const Tensor *File::find(const std::string &name) const {
@@ -272,7 +313,7 @@ const Tensor *File::find(const std::string &name) const {
 
 const Tensor &File::tensor(const std::string &name) const {
     const Tensor *t = find(name);
-    if (!t) throw std::runtime_error("missing tensor " + name);
+    if (!t) throw runtime_error("missing tensor " + name);
     return *t;
 }
 

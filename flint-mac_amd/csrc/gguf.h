@@ -1,8 +1,8 @@
 // Read-only GGUF v3 reader: the file is memory-mapped once; metadata is decoded
 // into typed values and the tensor table into (name, ggml type, dims, bytes).
-// Follows the format the reference parses at /root/reference/src/gguf.cpp:137-194
+// Reads the format the reference parses at /root/reference/src/gguf.cpp:137-194
 // (header, key/value section, tensor infos, data section aligned to
-// general.alignment, default 32) and reports the same errors.
+// general.alignment, default 32) and reports the same error messages.
 #pragma once
 
 #include <stddef.h>
@@ -70,7 +70,9 @@ public:
     const std::vector<Tensor> &tensors() const { return tensors_; }
 
 private:
+    void parse();  // header, metadata and tensor table of the mapped file
     const Value &value(const std::string &key) const;
+    const Value &typed(const std::string &key, int kind) const;
 
     std::string path_;
     int fd_ = -1;

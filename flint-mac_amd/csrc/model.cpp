@@ -130,6 +130,9 @@ const gguf::Tensor &want(const gguf::File &f, const std::string &name, uint64_t 
     return t;
 }
 
+// bytes of one 2048-element row of a projection type (proj_type() has accepted it)
+int64_t w_row_bytes_of(uint32_t type) { return flint_w_row_bytes((int32_t)type, FLINT_N_EMBD); }
+
 constexpr size_t kAlign = 256;  // every tensor's copy starts 256-byte aligned in HBM
 
 }  // namespace
@@ -236,7 +239,8 @@ flint_attn_model *flint_attn_model_open(const char *gguf_path, int32_t n_ctx, in
         auto dev = [&](size_t i) { return (const void *)((const char *)m->wmem + copies[i].at); };
         auto weight = [&](size_t i) { return flint_weight{dev(i), (int32_t)copies[i].t->type}; };
         m->embd = weight(c_embd);
-        m->embd_rows = (int64_t)te.dims[1];
+        // rows the copy holds (the reader has checked dims[0] * dims[1] against the tensor's bytes)
+        m->embd_rows = (int64_t)std::min<uint64_t>(te.dims[1], te.nbytes / (uint64_t)w_row_bytes_of(te.type));
         char e2[512] = {0};
         m->eng = flint_attn_engine_create(n_layer, m->hp.is_swa.data(), m->hp.has_rope.data(), n_ctx, kv_dtype,
                                           m->hp.h.rope_theta, e2, sizeof(e2));

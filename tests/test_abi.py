@@ -22,11 +22,83 @@ def test_library_exports_every_header_function():
     assert set(names) <= exported
 
 
+# The Rust server's bindings, as declared at /root/reference/server/src/ffi.rs:5-11 (the
+# #[repr(C)] config) and :19-29 (the extern "C" block), kept here as text.
+RUST_FFI = """
+fn flint_open(cfg: *const FlintConfig, err: *mut c_char, err_len: i32) -> *mut FlintEngineRaw;
+fn flint_close(e: *mut FlintEngineRaw);
+fn flint_n_ctx(e: *const FlintEngineRaw) -> i32;
+fn flint_n_vocab() -> i32;
+fn flint_pos(e: *const FlintEngineRaw) -> i32;
+fn flint_truncate(e: *mut FlintEngineRaw, pos: i32) -> i32;
+fn flint_prefill(e: *mut FlintEngineRaw, tokens: *const i32, n: i32, err: *mut c_char, err_len: i32) -> i32;
+fn flint_decode(e: *mut FlintEngineRaw, token: i32, err: *mut c_char, err_len: i32) -> i32;
+fn flint_logits(e: *const FlintEngineRaw) -> *const f32;
+"""
+RUST_CONFIG = [("model_path", "*const c_char"), ("metallib_dir", "*const c_char"), ("pool_gb", "f64"),
+               ("n_ctx", "i32")]
+# Rust FFI type -> the C type it binds to (flint_engine is opaque on both sides)
+RUST_TO_C = {"*const FlintConfig": "const flint_config*", "*mut c_char": "char*", "*const c_char": "const char*",
+             "i32": "int32_t", "f64": "double", "*const i32": "const int32_t*", "*const f32": "const float*",
+             "*mut FlintEngineRaw": "flint_engine*", "*const FlintEngineRaw": "const flint_engine*", "": "void"}
+
+
+def _c_prototypes():
+    """{name: (return type, [parameter types])} of include/capi.h, spacing normalised."""
+    import re
+    src = open(os.path.join(fa.INCLUDE, "capi.h")).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    out = {}
+    for ret, name, params in re.findall(r"([A-Za-z_][\w\s\*]*?)\b(flint_\w+)\s*\(([^)]*)\)\s*;", src):
+        norm = lambda t: re.sub(r"\s*\*\s*", "*", " ".join(t.split()))
+        types = []
+        for p in params.split(","):
+            p = p.strip()
+            if p in ("", "void"):
+                continue
+            types.append(norm(re.sub(r"\b\w+$", "", p)))  # drop the parameter name
+        out[name] = (norm(ret), types)
+    return out
+
+
+def _rust_prototypes():
+    import re
+    out = {}
+    for name, params, ret in re.findall(r"fn (flint_\w+)\(([^)]*)\)(?:\s*->\s*([^;]+))?;", RUST_FFI):
+        types = [RUST_TO_C[p.split(":", 1)[1].strip()] for p in params.split(",") if p.strip()]
+        out[name] = (RUST_TO_C[(ret or "").strip()], types)
+    return out
+
+
 def test_capi_header_matches_rust_ffi_signatures():
-    """The nine entry points the Rust server binds (/root/reference/server/src/ffi.rs:18-28)."""
-    want = {"flint_open", "flint_close", "flint_n_ctx", "flint_n_vocab", "flint_pos", "flint_truncate",
-            "flint_prefill", "flint_decode", "flint_logits"}
-    assert want <= set(fa.header_functions())
+    """Each of the nine entry points the Rust server binds has, in include/capi.h, the return
+    type and parameter types that its Rust declaration maps to."""
+    rust, c = _rust_prototypes(), _c_prototypes()
+    assert len(rust) == 9
+    for name, sig in rust.items():
+        assert name in c, name
+        assert c[name] == sig, (name, c[name], sig)
+
+
+def test_capi_config_layout_matches_rust_repr_c(tmp_path):
+    """flint_config's field offsets and size, compiled from include/capi.h, equal the
+    #[repr(C)] layout of the Rust FlintConfig (pointers 8 bytes, f64 8, i32 4, C alignment)."""
+    size = {"*const c_char": 8, "f64": 8, "i32": 4}
+    off, want = 0, []
+    for field, ty in RUST_CONFIG:
+        n = size[ty]
+        off = (off + n - 1) // n * n
+        want.append((field, off))
+        off += n
+    total = (off + 7) // 8 * 8
+    prog = tmp_path / "layout.c"
+    prog.write_text('#include <stddef.h>\n#include <stdio.h>\n#include "capi.h"\nint main(void) {\n' +
+                    "".join(f'  printf("%zu ", offsetof(flint_config, {f}));\n' for f, _ in RUST_CONFIG) +
+                    '  printf("%zu\\n", sizeof(flint_config));\n  return 0;\n}\n')
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-I", fa.INCLUDE, str(prog), "-o", str(exe)], check=True)
+    got = [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+    assert got == [o for _, o in want] + [total]
 
 
 def _err():

@@ -280,3 +280,18 @@ def test_loader_rejects_bad_encodings(model, tmp_path):
     # general.alignment 0
     p3 = _raw_meta_model(model, tmp_path, "align0", [("general.alignment", gw.GGUF_U32, 0)])
     assert model_open_error(p3) == "gguf: general.alignment is 0"
+
+
+def test_loader_rejects_wrapping_tensor_sizes(model, tmp_path):
+    """A tensor whose byte count does not fit 64 bits (an F32 token_embd.weight of 2048 x 2^51
+    elements: 2^62 elements, 2^64 bytes) or whose row is not a whole number of blocks is
+    rejected on the host, before any device work: no row index past the mapped bytes can
+    reach the embedding kernel."""
+    p1 = str(tmp_path / "wrap.gguf")
+    mb.write_model(p1, model, tensor_edit=lambda ts: [(t[0], np.zeros(16, np.uint8), 0, (2048, 1 << 51))
+                                                      if t[0] == "token_embd.weight" else t for t in ts])
+    assert model_open_error(p1) == "tensor out of bounds: token_embd.weight"
+    p2 = str(tmp_path / "partial_block.gguf")
+    mb.write_model(p2, model, tensor_edit=lambda ts: [(t[0], np.zeros(34, np.uint8), 8, (33, 1))
+                                                      if t[0] == "output.weight" else t for t in ts])
+    assert model_open_error(p2) == "tensor out of bounds: output.weight"
