@@ -279,3 +279,62 @@ def test_decode_batch_swa_v_slices(cuda, store, n_seq):
         assert np.array_equal(vcs[s].transpose(1, 0, 2).reshape(1024, KV_DIM), ring), f"seq {s}: V ring"
         cur = p & 1023
         assert k_close(kcs[s][:, cur, :], Kc[p].reshape(N_HEAD_KV, HEAD_DIM), store), f"seq {s}: K slot {cur}"
+
+
+def config5_contexts():
+    """The 16 contexts of benchmark config 5 (bench.py draws them the same way): U[4096, 65536], seed 4."""
+    return [int(c) for c in np.random.default_rng(4).integers(4096, 65537, 16)]
+
+
+@pytest.mark.parametrize("store", ["f16", "bf16"])
+@pytest.mark.parametrize("is_swa", [False, True], ids=["full", "swa"])
+def test_decode_batch_config5_workload(cuda, store, is_swa):
+    """Config 5 at its own workload: 16 sequences at the contexts the benchmark uses (4k-65k),
+    one token each, in one batched launch with the automatic plan. Full layer: each
+    sequence's key range is cut into its own number of splits over ~192 workgroups, merged
+    by the LSE combine. SWA layer (RoPE, 1024-slot ring, window 513): one split per
+    sequence, 4 V slices per kv head (256 workgroups). Every sequence equals the oracle, the
+    current token's K/V land in its slot, and on the SWA layer every ring slot keeps what it
+    held (/root/reference/src/engine.mm:735-766, batched over sequences)."""
+    ctx = config5_contexts()
+    _say(f"decode config-5 workload store={store} swa={is_swa} contexts={ctx}")
+    rng = np.random.default_rng(5 + is_swa)
+    qn, kn, sk = layer_weights(rng)
+    n_seq = len(ctx)
+    n_slots = 1024 if is_swa else (max(ctx) + 1 + 31) // 32 * 32
+    kv = fa.KVLayer(is_swa=is_swa, has_rope=is_swa, n_slots=n_slots, kv_dtype=store, rope_theta=1e6, q_norm=qn,
+                    k_norm=kn, sinks=sk, n_seq=n_seq)
+    L = oracle_layer(kv, qn, kn, sk, store)
+    qkv = rng.standard_normal((n_seq, QKV_DIM)).astype(np.float32)
+    wants, keep = [], []
+    for s, p in enumerate(ctx):
+        # the history the cache holds: every position (full) or the last n_slots (ring)
+        first = max(0, p - (n_slots - 1)) if is_swa else 0
+        K = np.zeros((p + 1, KV_DIM), np.float32)
+        V = np.zeros((p + 1, KV_DIM), np.float32)
+        K[first:p], V[first:p] = _history(rng, p - first, store, outlier_frac=0.0 if is_swa else 0.01)
+        slots = np.arange(first, p) & (n_slots - 1) if is_swa else np.arange(first, p)
+        _fill_cache(kv, K[first:p], V[first:p], slots, s)
+        wants.append(fo.decode_step(L, qkv[s], p, K, V, n_threads=16))  # writes row p of K, V
+        keep.append((K[p].copy(), V[p].copy(), V[max(0, p - (n_slots - 1)):p + 1].copy() if is_swa else None))
+        del K, V
+    dq = torch.from_numpy(qkv).to(cuda)
+    att = torch.zeros((n_seq, Q_DIM), device=cuda)
+    kv.decode(dq, att, ctx)
+    torch.cuda.synchronize()
+    got = att.cpu().numpy()
+    for s, p in enumerate(ctx):
+        assert_close(got[s], wants[s], f"seq {s} ctx {p}")
+        kcur, vcur, ring_hist = keep[s]
+        slot = kv.slot(p)
+        vc = kv.v[s].permute(0, 1, 3, 2).reshape(N_HEAD_KV, n_slots, HEAD_DIM)[:, slot, :].float().cpu().numpy()
+        assert np.array_equal(vc, vcur.reshape(N_HEAD_KV, HEAD_DIM)), f"seq {s}: V slot {slot}"
+        kidx = torch.as_tensor(fa.k_tile_offsets()[slot % 32], device=cuda)
+        kc = kv.k[s, :, slot // 32][:, kidx].float().cpu().numpy()
+        assert k_close(kc, kcur.reshape(N_HEAD_KV, HEAD_DIM), store), f"seq {s}: K slot {slot}"
+        if is_swa:
+            first = max(0, p - (n_slots - 1))
+            ring = np.zeros((n_slots, KV_DIM), np.float32)
+            ring[np.arange(first, p + 1) & (n_slots - 1)] = ring_hist
+            got_ring = kv.v_slots()[s].float().cpu().numpy().transpose(1, 0, 2).reshape(n_slots, KV_DIM)
+            assert np.array_equal(got_ring, ring), f"seq {s}: V ring"
