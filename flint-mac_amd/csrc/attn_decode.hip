@@ -39,6 +39,8 @@
 //    equal shares of the stream. Every kernel argument the block needs is read at wave
 //    start (the per-sequence tables one entry per lane), so the kernel-argument fetch
 //    costs one memory round trip.
+#include <mutex>
+
 #include "common.h"
 #include "flint_attn_internal.h"
 
@@ -189,14 +191,14 @@ __global__ __launch_bounds__(DEC_THREADS) void attn_decode_kernel(const DecodePa
     const int t_base = P.wg_base[lane], t_pos = P.pos[lane], t_tps = P.tps[lane], t_ns = P.n_split[lane];
     const int n_seq = P.n_seq;
     const int is_swa = P.is_swa, has_rope = P.has_rope, window = P.window;
-    const int n_slots = P.n_slots, slot_mask = P.slot_mask, max_split = P.max_split;
+    const int n_slots = P.n_slots, slot_mask = P.slot_mask;
     const float rms_eps = P.rms_eps;
     const long long seq_stride = P.seq_stride;
     const float *const qkv = P.qkv, *const q_norm = P.q_norm, *const k_norm = P.k_norm, *const sinks = P.sinks;
     uint16_t *const k_cache = P.k_cache, *const v_cache = P.v_cache;
     float *const att = P.att, *const partial = P.partial;
     pin_sgpr(n_seq), pin_sgpr(is_swa), pin_sgpr(has_rope), pin_sgpr(window);
-    pin_sgpr(n_slots), pin_sgpr(slot_mask), pin_sgpr(max_split), pin_sgpr(rms_eps), pin_sgpr(seq_stride);
+    pin_sgpr(n_slots), pin_sgpr(slot_mask), pin_sgpr(rms_eps), pin_sgpr(seq_stride);
     pin_sgpr(qkv), pin_sgpr(q_norm), pin_sgpr(k_norm), pin_sgpr(sinks), pin_sgpr(k_cache), pin_sgpr(v_cache);
     pin_sgpr(att), pin_sgpr(partial);
     asm volatile("" ::"v"(t_base), "v"(t_pos), "v"(t_tps), "v"(t_ns));
@@ -395,7 +397,10 @@ __global__ __launch_bounds__(DEC_THREADS) void attn_decode_kernel(const DecodePa
         return;
     }
     if constexpr (VS > 1) return;  // not reached: V slices are planned for one split per sequence
-    float *pp = partial + (((size_t)seq * N_HEAD + hout) * max_split + split) * PART_STRIDE;
+    // partials of a launch: sequence s's splits start at split wg_base[s] / 4 of the launch,
+    // and each head's splits are consecutive records
+    const int split0 = __builtin_amdgcn_readlane(t_base, seq) / N_HEAD_KV;
+    float *pp = partial + ((size_t)split0 * N_HEAD + hout * n_split + split) * PART_STRIDE;
     *(float2 *)(pp + d2) = make_float2(A0, A1);
     if (lane == 0) *(float2 *)(pp + HEAD_DIM) = make_float2(M, L);
 }
@@ -410,12 +415,12 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const DecodeParams P)
     __shared__ float red[2][4];
     __shared__ float4 part[8][32];
     const int hh = blockIdx.x, seq = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int ns = P.n_split[seq], max_split = P.max_split;
+    const int ns = P.n_split[seq], split0 = P.wg_base[seq] / N_HEAD_KV;
     const float *const partial = P.partial, *const sinks = P.sinks;
     float *const att = P.att;
-    pin_sgpr(ns), pin_sgpr(max_split), pin_sgpr(partial), pin_sgpr(sinks), pin_sgpr(att);
+    pin_sgpr(ns), pin_sgpr(split0), pin_sgpr(partial), pin_sgpr(sinks), pin_sgpr(att);
     if (ns <= 1) return;  // written directly by the decode kernel
-    const float *pp = partial + ((size_t)seq * N_HEAD + hh) * max_split * PART_STRIDE;
+    const float *pp = partial + ((size_t)split0 * N_HEAD + hh * ns) * PART_STRIDE;
     const int dg = tid & 31, sg = tid >> 5;
     float4 x[8];
 #pragma unroll
@@ -472,6 +477,31 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const DecodeParams P)
         *(float4 *)(att + (size_t)seq * Q_DIM + hh * HEAD_DIM + 4 * dg) =
             make_float4(t.x * inv, t.y * inv, t.z * inv, t.w * inv);
     }
+}
+
+// Split partials of the entry point that allocates nothing (flint_attn_decode_batch_noalloc):
+// a fixed array in device memory, one copy per GPU, held until the process ends. Host code
+// never passes `scratch` itself to a kernel (in host code the name is a stand-in, not a
+// device address): it takes the address hipGetSymbolAddress gives on each device.
+static __device__ __align__(256) float scratch[DECODE_SCRATCH_BYTES / sizeof(float)];
+
+hipError_t decode_scratch(float **ptr) {
+    constexpr int MAX_DEVICES = 64;
+    static std::mutex mu;
+    static float *addr[MAX_DEVICES] = {};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= MAX_DEVICES) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lk(mu);
+    if (!addr[dev]) {
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));  // with this device current
+        if (e != hipSuccess) return e;
+        addr[dev] = (float *)p;
+    }
+    *ptr = addr[dev];
+    return hipSuccess;
 }
 
 hipError_t launch_decode(const DecodeParams &P, int dtype, hipStream_t stream) {

@@ -149,8 +149,10 @@ void rope_freqs_cached(float theta, float *freq) {
 
 constexpr int PART_STRIDE = 132;
 
+// no_alloc: the split partials go to the library's static device array (decode_scratch), and
+// nothing is allocated on the device.
 void decode_impl(const flint_attn_layer *L, int n_seq, int64_t seq_stride, const float *qkv, float *att,
-                 const int32_t *pos, int32_t keys_per_split, hipStream_t stream) {
+                 const int32_t *pos, int32_t keys_per_split, hipStream_t stream, bool no_alloc = false) {
     validate_layer(L);
     if (n_seq < 1 || n_seq > MAX_SEQ) throw Error("n_seq must be in [1, " + std::to_string(MAX_SEQ) + "]");
     if (!qkv || !att || !pos) throw Error("qkv/att/pos pointer is NULL");
@@ -199,10 +201,20 @@ void decode_impl(const flint_attn_layer *L, int n_seq, int64_t seq_stride, const
     for (int s = n_seq + 1; s <= MAX_SEQ; s++) P.wg_base[s] = P.wg_base[n_seq];
     P.max_split = max_split;
     if (max_split > 1024) throw Error("too many key splits (max 1024): raise keys_per_split");
-    DeviceScratch &ws = scratch();
     if (max_split > 1) {
-        const size_t need = (size_t)n_seq * N_HEAD * max_split * PART_STRIDE * sizeof(float);
-        P.partial = (float *)ws.partial.get(need);
+        // one record per (split, head) of the launch (v_slices is 1 here: 4 workgroups a split)
+        const size_t need = (size_t)(P.wg_base[n_seq] / N_HEAD_KV) * N_HEAD * PART_STRIDE * sizeof(float);
+        if (no_alloc) {
+            if (need > DECODE_SCRATCH_BYTES)
+                throw Error("flint_attn_decode_batch_noalloc: the split plan needs " + std::to_string(need) +
+                            " bytes of partials, more than the " + std::to_string(DECODE_SCRATCH_BYTES) +
+                            " bytes this entry point holds (" +
+                            std::to_string(DECODE_SCRATCH_BYTES / (N_HEAD * PART_STRIDE * sizeof(float))) +
+                            " key splits over the batch): use fewer sequences or a larger keys_per_split");
+            check(decode_scratch(&P.partial), "decode scratch address");
+        } else {
+            P.partial = (float *)scratch().partial.get(need);
+        }
     }
     check(launch_decode(P, L->kv_dtype, stream), "decode launch");
 }
@@ -409,6 +421,14 @@ int32_t flint_attn_decode_batch(const flint_attn_layer *layer, int32_t n_seq, in
                                 int32_t err_len) {
     return guarded(err, err_len, [&] {
         decode_impl(layer, n_seq, seq_stride, qkv, att, pos, keys_per_split, (hipStream_t)stream);
+    });
+}
+
+int32_t flint_attn_decode_batch_noalloc(const flint_attn_layer *layer, int32_t n_seq, int64_t seq_stride,
+                                        const float *qkv, float *att, const int32_t *pos, int32_t keys_per_split,
+                                        void *stream, char *err, int32_t err_len) {
+    return guarded(err, err_len, [&] {
+        decode_impl(layer, n_seq, seq_stride, qkv, att, pos, keys_per_split, (hipStream_t)stream, true);
     });
 }
 

@@ -21,7 +21,8 @@ struct DecodeParams {
     uint16_t *v_cache;          // sequence 0: [4][n_slots/32][128][32] (V^T in 32-slot tiles)
     long long seq_stride;       // elements between two sequences' K (and V) caches
     float *att;                 // [n_seq][4096]
-    float *partial;             // [n_seq][32][max_split][132]
+    float *partial;             // [sum of n_split][32][132]: sequence s's splits start at split
+                                // wg_base[s] / 4, and each head's splits are consecutive records
     int n_slots;                // slots per kv head
     int slot_mask;              // SWA: n_slots - 1 (power of two); full: all ones
     int is_swa, has_rope, window, max_split;
@@ -37,6 +38,11 @@ struct DecodeParams {
 };
 
 hipError_t launch_decode(const DecodeParams &P, int dtype, hipStream_t stream);
+
+// The static device array that holds the split partials of flint_attn_decode_batch_noalloc, and
+// its address on the current device (looked up once per device, no allocation).
+constexpr size_t DECODE_SCRATCH_BYTES = 4u << 20;
+hipError_t decode_scratch(float **ptr);
 
 // Prefill: k/v prep (k_qk_prefill, prefill.metal:99-133) + flash attention with
 // the q prep fused (k_attn_prefill, prefill.metal:141-266).

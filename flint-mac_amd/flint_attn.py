@@ -70,6 +70,7 @@ _f32p = ctypes.POINTER(ctypes.c_float)
 _SIGS = {
     "flint_attn_decode": (_i32, [_lp, _vp, _vp, _i32, _i32, _vp, _cp, _i32]),
     "flint_attn_decode_batch": (_i32, [_lp, _i32, _i64, _vp, _vp, _i32p, _i32, _vp, _cp, _i32]),
+    "flint_attn_decode_batch_noalloc": (_i32, [_lp, _i32, _i64, _vp, _vp, _i32p, _i32, _vp, _cp, _i32]),
     "flint_attn_prefill": (_i32, [_lp, _vp, _i32, _i32, _i32, _vp, _vp, _cp, _i32]),
     "flint_attn_sync": (_i32, [_cp, _i32]),
     "flint_attn_engine_create": (_vp, [_i32, _u8p, _u8p, _i32, _i32, _f32, _cp, _i32]),

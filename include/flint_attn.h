@@ -93,6 +93,20 @@ int32_t flint_attn_decode_batch(const flint_attn_layer *layer, int32_t n_seq, in
                                 void *stream, char *err, int32_t err_len);
 
 /*
+ * flint_attn_decode_batch for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in
+ * the reference. It takes the same arguments and launches the same kernels, and allocates
+ * nothing: the key-split partials live in a static 4 MiB device array of the library, one
+ * per GPU, held until the process ends. That holds 248 key splits over the batch (the
+ * built-in plan uses about 48 over all sequences; one split needs no partials); a plan that
+ * needs more is rejected with an error before any launch. Every call on a GPU shares that
+ * GPU's array, so calls that overlap on one GPU (on two streams, or from two threads) race.
+ */
+int32_t flint_attn_decode_batch_noalloc(const flint_attn_layer *layer, int32_t n_seq, int64_t seq_stride,
+                                        const float *qkv, float *att, const int32_t *pos, int32_t keys_per_split,
+                                        void *stream, char *err, int32_t err_len);
+
+/*
  * Batched prefill attention of one layer for T tokens at positions p0..p0+T-1
  * (replaces k_qk_prefill + k_attn_prefill, /root/reference/src/metal/prefill.metal:99-266,
  * dispatched per chunk at /root/reference/src/engine.mm:1087-1104).
