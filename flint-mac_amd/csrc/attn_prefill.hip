@@ -58,23 +58,98 @@ __device__ inline size_t pv_index(int kvh, int row, int dim, int rows) {
     return (tile * 16 + 8 + (dim >> 5) * 2 + (k >> 4)) * 512 + ((((k >> 3) & 1) * 32 + (dim & 31)) << 3) + (k & 7);
 }
 
-template <int DT>
-__device__ inline _Float16 to_f16(uint16_t u) {
-    return (_Float16)KvType<DT>::to_float(u);
+// The id of the last prefill call that stored some tile of the attention copy scaled (its K
+// or V values did not fit f16 as they are): written by prefix_kernel and kv_prep_kernel,
+// compared with the call's own id by the flash kernel, which then takes its scaled path.
+// Ids are unique per call, so the flag needs no reset.
+static __device__ uint32_t g_scaled_call;
+
+// The exponent e a tile's values are scaled by (x * 2^-e) to be stored in f16 with its full
+// relative precision, from the tile's largest magnitude mx: 0 (stored as is) for mx in
+// [2^-6, 2^15), for 0 and for inf / nan (which f16 carries as they are); otherwise
+// ilogb(mx) - 14, which puts the scaled maximum in [2^14, 2^15). Tiny tiles are scaled up
+// only when `up` (V: the output inherits V's scale; a tiny K only makes its scores tiny,
+// which f16 carries to the same absolute accuracy as the reference's fp32).
+__device__ inline int tile_exp(float mx, bool up) {
+    if (!__builtin_isfinite(mx) || mx == 0.f) return 0;
+    if (mx < 32768.f && (!up || mx >= 0.015625f)) return 0;
+    return __builtin_amdgcn_frexp_expf(mx) - 15;  // frexp exponent f: mx in [2^(f-1), 2^f)
+}
+
+// Maximum over the 256 threads of a workgroup (red: 4 floats of LDS).
+__device__ inline float block_max256(float x, float *red) {
+    x = wave_max(x);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = x;
+    __syncthreads();
+    return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+// A tile's exponents into the table, and the call's flag when the tile is scaled.
+__device__ inline void put_texp(const PrefillParams &P, int kvh, int row0, int eK, int eV) {
+    P.texp[kvh * (P.k_rows >> 5) + (row0 >> 5)] = (eK & 0xffff) | (eV << 16);
+    if (eK | eV) __hip_atomic_store(&g_scaled_call, P.call_id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------------------
-// prefix: cache -> attention copy for positions [kbase, p0). grid (chunks of 64, kv head).
+// prefix: cache -> attention copy for the cached positions [kbase, p0). grid (tiles, kv head),
+// 256 threads. Block x < (p0 >> 5) - (kbase >> 5) takes a whole tile of cached positions: a
+// cache tile and a copy tile both hold 16-byte units of 8 dims of one key (K) or 8 keys of one
+// dim (V), so each thread moves 2 + 2 units: read, measure, scale, convert to f16, write at
+// the unit's place in the copy. When p0 is not 32-aligned, one more block copies the cached
+// positions [p0 & ~31, p0) of the tile that holds p0 into their places in the copy as the
+// cache's raw 16-bit values: kv_prep takes them from there (a long SWA prefill overwrites
+// their ring slots in its own launch) and writes the tile, new positions included.
 template <int DT>
 __global__ __launch_bounds__(256) void prefix_kernel(const PrefillParams P) {
-    const int kvh = blockIdx.y, c0 = blockIdx.x * 64;
-    const int n_pre = P.p0 - P.kbase, nc = min(64, n_pre - c0);
-    for (int i = threadIdx.x; i < 64 * HEAD_DIM; i += 256) {
-        const int r = i >> 7, d = i & 127;
-        if (r >= nc) break;
-        const int pos = P.kbase + c0 + r, slot = pos & P.cache_mask, row = pos - P.kbase;
-        P.sk[pk_index(kvh, row, d, P.k_rows)] = to_f16<DT>(P.cache_k[kt_index(kvh, slot, d, P.n_slots)]);
-        P.sk[pv_index(kvh, row, d, P.k_rows)] = to_f16<DT>(P.cache_v[vt_index(kvh, slot, d, P.n_slots)]);
+    typedef KvType<DT> KT;
+    __shared__ float red[2][4];
+    const int kvh = blockIdx.y, tid = threadIdx.x;
+    const int row0 = 32 * blockIdx.x, pos0 = P.kbase + row0;  // the tile's first position
+    if (pos0 + 32 > P.p0) {  // the tile holding p0: raw values of positions [pos0, p0)
+        uint16_t *raw = (uint16_t *)P.sk;
+        for (int i = tid; i < (P.p0 - pos0) * HEAD_DIM; i += 256) {
+            const int r = i >> 7, d = i & 127, slot = (pos0 + r) & P.cache_mask;
+            raw[pk_index(kvh, row0 + r, d, P.k_rows)] = P.cache_k[kt_index(kvh, slot, d, P.n_slots)];
+            raw[pv_index(kvh, row0 + r, d, P.k_rows)] = P.cache_v[vt_index(kvh, slot, d, P.n_slots)];
+        }
+        return;
+    }
+    const size_t ct = (size_t)kvh * (P.n_slots >> 5) + ((pos0 & P.cache_mask) >> 5);  // its cache tile
+    const u32x4 *kc = (const u32x4 *)(P.cache_k + ct * (32 * HEAD_DIM));
+    const u32x4 *vc = (const u32x4 *)(P.cache_v + ct * (32 * HEAD_DIM));
+    u32x4 ku[2], vu[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) ku[i] = kc[tid + 256 * i], vu[i] = vc[tid + 256 * i];
+    int eK = 0, eV = 0;
+    if constexpr (DT == DT_BF16) {
+        float mk = 0.f, mv = 0.f;
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                mk = fmaxf(mk, fmaxf(fabsf(KT::to_float(ku[i][w] & 0xffff)), fabsf(KT::to_float(ku[i][w] >> 16))));
+                mv = fmaxf(mv, fmaxf(fabsf(KT::to_float(vu[i][w] & 0xffff)), fabsf(KT::to_float(vu[i][w] >> 16))));
+            }
+        eK = tile_exp(block_max256(mk, red[0]), false);
+        eV = tile_exp(block_max256(mv, red[1]), true);
+    }
+    if (tid == 0) put_texp(P, kvh, row0, eK, eV);
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int u = tid + 256 * i;
+        f16x8 k8, v8;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const uint32_t kw = ku[i][e >> 1], vw = vu[i][e >> 1];
+            k8[e] = (_Float16)__builtin_amdgcn_ldexpf(KT::to_float(e & 1 ? kw >> 16 : kw & 0xffff), -eK);
+            v8[e] = (_Float16)__builtin_amdgcn_ldexpf(KT::to_float(e & 1 ? vw >> 16 : vw & 0xffff), -eV);
+        }
+        // K cache unit (st*4 + c)*64 + 16g + n: key 8(n>>2) + 4st + (n&3), dims 32c + 8g .. +7
+        const int st = u >> 8, c = (u >> 6) & 3, g = (u >> 4) & 3, n = u & 15;
+        const int r = 8 * (n >> 2) + 4 * st + (n & 3);
+        *(f16x8 *)(P.sk + pk_index(kvh, row0 + r, 32 * c + 8 * g, P.k_rows)) = k8;
+        // V cache unit 4d + g: dim d, keys 8g .. 8g+7
+        *(f16x8 *)(P.sk + pv_index(kvh, row0 + 8 * (u & 3), u >> 2, P.k_rows)) = v8;
     }
 }
 
@@ -83,14 +158,18 @@ __global__ __launch_bounds__(256) void prefix_kernel(const PrefillParams P) {
 // Chunk c holds positions 32 c0 + 32 c .. +31 (32-aligned, so it is one tile of the
 // attention copy, whose kbase is 32-aligned, and one tile of the cache). Each wave
 // normalises (+ RoPE) 8 tokens' k (lane = a NEOX pair of dims) and rounds k and v to
-// the cache dtype into LDS; then every 16-byte unit of the four destination tiles is
-// written with one store. A V unit spans 8 positions: where some of them are not new
-// (or, for the ring, not kept) its elements are stored one by one, so no unit is
-// read back and no two workgroups write the same bytes.
+// the cache dtype into LDS; the first chunk also takes the cached positions before p0
+// (from the copy, where prefix_kernel left their raw values), and positions past the last
+// new one are zero. Then every 16-byte unit
+// of the copy tile is written with one store (scaled by the tile's exponents), and the
+// new positions that the cache keeps go to the cache tile. A V unit of the cache spans 8
+// positions: where some of them are not new (or, for the ring, not kept) its elements are
+// stored one by one, so no cache unit is read back and no two workgroups write the same bytes.
 template <int DT>
 __global__ __launch_bounds__(256) void kv_prep_kernel(const PrefillParams P) {
     typedef KvType<DT> KT;
-    __shared__ uint16_t kl[32][HEAD_DIM + 8], vl[32][HEAD_DIM + 8];  // rounded k and v
+    __shared__ uint16_t kl[32][HEAD_DIM + 8], vl[32][HEAD_DIM + 8];  // k and v in the cache dtype
+    __shared__ float red[2][4];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, tid = threadIdx.x;
     const int kvh = blockIdx.y;
     const int c0 = (P.p0 >> 5) + blockIdx.x, pos0 = 32 * c0;  // first position of the chunk
@@ -98,7 +177,7 @@ __global__ __launch_bounds__(256) void kv_prep_kernel(const PrefillParams P) {
     const float2 kw = make_float2(P.k_norm[lane], P.k_norm[lane + 64]);
     const float rf = P.rope_freq[lane];
     // the wave's 8 tokens: all loads first (positions outside [lo, hi) read the chunk's
-    // first new token, in range, and are not stored), then the maths
+    // first new token, in range, and are not used), then the maths
     float2 kx[8], vx[8];
 #pragma unroll
     for (int i = 0; i < 8; i++) {
@@ -107,19 +186,58 @@ __global__ __launch_bounds__(256) void kv_prep_kernel(const PrefillParams P) {
         kx[i] = make_float2(kr[lane], kr[lane + 64]);
         vx[i] = make_float2(kr[KV_DIM + lane], kr[KV_DIM + lane + 64]);
     }
+    float mk = 0.f, mv = 0.f;  // this lane's largest |k| and |v| (bf16: they set the tile's exponents)
+    // Every row is computed as if new (rows outside [lo, hi) from the chunk's first new token)
+    // and selected afterwards: no branch between the rows, so their norm and RoPE chains
+    // interleave. Rows past the new positions are zero.
 #pragma unroll
     for (int i = 0; i < 8; i++) {
         const int r = wave + 4 * i, pos = pos0 + r;
+        const bool is_new = pos >= lo && pos < hi;
         float cs = 1.f, sn = 0.f;
         if (P.has_rope) rope_sincos((float)pos * rf, &sn, &cs);
         const float2 k2 = norm_rope_pair(kx[i], kw, P.rms_eps, P.has_rope, cs, sn);
-        kl[r][lane] = KT::from_float(k2.x);
-        kl[r][lane + 64] = KT::from_float(k2.y);
-        vl[r][lane] = KT::from_float(vx[i].x);
-        vl[r][lane + 64] = KT::from_float(vx[i].y);
+        const uint16_t k0 = is_new ? KT::from_float(k2.x) : 0, k1 = is_new ? KT::from_float(k2.y) : 0;
+        const uint16_t v0 = is_new ? KT::from_float(vx[i].x) : 0, v1 = is_new ? KT::from_float(vx[i].y) : 0;
+        kl[r][lane] = k0, kl[r][lane + 64] = k1, vl[r][lane] = v0, vl[r][lane + 64] = v1;
+        if constexpr (DT == DT_BF16) {
+            mk = fmaxf(mk, fmaxf(fabsf(KT::to_float(k0)), fabsf(KT::to_float(k1))));
+            mv = fmaxf(mv, fmaxf(fabsf(KT::to_float(v0)), fabsf(KT::to_float(v1))));
+        }
+    }
+    if (pos0 < lo) {
+        // the first chunk of a continuation that starts inside a tile: its cached positions
+        // [pos0, p0) come from the copy, where prefix_kernel left the cache's raw values
+        // (kbase <= pos0, 32-aligned)
+        const uint16_t *raw = (const uint16_t *)P.sk;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int r = wave + 4 * i, row = pos0 + r - P.kbase;
+            if (pos0 + r < lo) {
+                const uint16_t k0 = raw[pk_index(kvh, row, lane, P.k_rows)];
+                const uint16_t k1 = raw[pk_index(kvh, row, lane + 64, P.k_rows)];
+                const uint16_t v0 = raw[pv_index(kvh, row, lane, P.k_rows)];
+                const uint16_t v1 = raw[pv_index(kvh, row, lane + 64, P.k_rows)];
+                kl[r][lane] = k0, kl[r][lane + 64] = k1, vl[r][lane] = v0, vl[r][lane + 64] = v1;
+                if constexpr (DT == DT_BF16) {
+                    mk = fmaxf(mk, fmaxf(fabsf(KT::to_float(k0)), fabsf(KT::to_float(k1))));
+                    mv = fmaxf(mv, fmaxf(fabsf(KT::to_float(v0)), fabsf(KT::to_float(v1))));
+                }
+            }
+        }
+    }
+    if constexpr (DT == DT_BF16) {
+        mk = wave_max(mk), mv = wave_max(mv);
+        if (lane == 0) red[0][wave] = mk, red[1][wave] = mv;
     }
     __syncthreads();
-    const int row0 = pos0 - P.kbase;              // attention-copy row of the chunk's first position
+    int eK = 0, eV = 0;
+    if constexpr (DT == DT_BF16) {
+        eK = tile_exp(fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3])), false);
+        eV = tile_exp(fmaxf(fmaxf(red[1][0], red[1][1]), fmaxf(red[1][2], red[1][3])), true);
+    }
+    const int row0 = pos0 - P.kbase;               // attention-copy row of the chunk's first position
+    if (tid == 0) put_texp(P, kvh, row0, eK, eV);
     const bool to_cache = hi > P.cache_from;       // some positions go to the cache
     const int clo = max(lo, P.cache_from);         // cached positions [clo, hi)
     const int ctile = (pos0 & P.cache_mask) >> 5;  // the cache tile (slot = pos & mask, 32-aligned)
@@ -129,28 +247,20 @@ __global__ __launch_bounds__(256) void kv_prep_kernel(const PrefillParams P) {
         // K, attention copy: unit (st, hh, col) = key pf_sigma(col), dims 16 st + 8 hh .. +7
         {
             const int st = u >> 6, hh = (u >> 5) & 1, col = u & 31, r = pf_sigma(col);
-            if (pos0 + r >= lo && pos0 + r < hi) {
-                f16x8 v;
+            f16x8 v;
 #pragma unroll
-                for (int e = 0; e < 8; e++) v[e] = (_Float16)KT::to_float(kl[r][16 * st + 8 * hh + e]);
-                *(f16x8 *)(P.sk + pk_index(kvh, row0 + r, 16 * st + 8 * hh, P.k_rows)) = v;
-            }
+            for (int e = 0; e < 8; e++)
+                v[e] = (_Float16)__builtin_amdgcn_ldexpf(KT::to_float(kl[r][16 * st + 8 * hh + e]), -eK);
+            *(f16x8 *)(P.sk + pk_index(kvh, row0 + r, 16 * st + 8 * hh, P.k_rows)) = v;
         }
         // V, attention copy: unit (dt, kk, hh, d) = dim 32 dt + d, keys 16 kk + 8 hh .. +7
         {
             const int dt = u >> 7, kk = (u >> 6) & 1, hh = (u >> 5) & 1, d = 32 * dt + (u & 31);
             const int r0 = 16 * kk + 8 * hh;
-            _Float16 *dst = P.sk + pv_index(kvh, row0 + r0, d, P.k_rows);
-            if (pos0 + r0 >= lo && pos0 + r0 + 8 <= hi) {
-                f16x8 v;
+            f16x8 v;
 #pragma unroll
-                for (int e = 0; e < 8; e++) v[e] = (_Float16)KT::to_float(vl[r0 + e][d]);
-                *(f16x8 *)dst = v;
-            } else {
-#pragma unroll
-                for (int e = 0; e < 8; e++)
-                    if (pos0 + r0 + e >= lo && pos0 + r0 + e < hi) dst[e] = (_Float16)KT::to_float(vl[r0 + e][d]);
-            }
+            for (int e = 0; e < 8; e++) v[e] = (_Float16)__builtin_amdgcn_ldexpf(KT::to_float(vl[r0 + e][d]), -eV);
+            *(f16x8 *)(P.sk + pv_index(kvh, row0 + r0, d, P.k_rows)) = v;
         }
         if (to_cache) {
             // K, cache tile (kt_index order): unit (st, c, g, n) = key 8(n>>2) + 4st + (n&3),
@@ -279,6 +389,12 @@ __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const Pref
     // LDS: 8 KiB per wave that hands q over to the operand order, and later the output
     __shared__ f16x8 q_lds[PF_WAVES][8][64];
 
+    // Did this call store some tile of the copy scaled (prefix / kv_prep set the flag before this
+    // launch)? A plain read of a uniform address is a scalar load; it is issued here, with the
+    // kernel arguments the wave waits for anyway (left alone, the compiler sinks it to its use
+    // after the q prologue, one more memory round trip per workgroup).
+    const uint32_t scaled_call = g_scaled_call;
+    pin_sgpr(scaled_call);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int col = lane & 31, hh = lane >> 5;
     const int kvh = blockIdx.x & 3, hq = kvh * GQA + wave;
@@ -322,9 +438,20 @@ __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const Pref
     if (t_lo + 2 <= t_hi) pf_gload(R2, skv + (size_t)(t_lo + 2) * (PF_TILE_UNITS * 8), tid);
     if (t_lo + 3 <= t_hi) pf_gload(R3, skv + (size_t)(t_lo + 3) * (PF_TILE_UNITS * 8), tid);
 
+    // After the RMSNorm |q| <= sqrt(128) |gain|, and the scale log2(e)/sqrt(128) follows: q
+    // gains that could take q past f16's range, or keep it below 2^-6, make q be stored scaled
+    // by 2^-eQ (wave-uniform; every wave of the block reads the same gains), which the scaled
+    // path below undoes.
+    float gq = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+        gq = fmaxf(gq, fmaxf(fmaxf(fabsf(w[k].x), fabsf(w[k].y)), fmaxf(fabsf(w[k].z), fabsf(w[k].w))));
+    const int eQ = tile_exp(wave_max(gq) * (LOG2E * 1.001f), true);
+    const bool scaled = eQ != 0 || scaled_call == P.call_id;  // wave-uniform
+
     f16x8 qf[8];
     {
-        const float qs = LOG2E / sqrtf((float)HEAD_DIM);
+        const float qs = __builtin_amdgcn_ldexpf(LOG2E / sqrtf((float)HEAD_DIM), -eQ);
         uint2 *const qa = (uint2 *)&q_lds[wave][0][0];  // 8-byte halves of the f16x8 units
 #pragma unroll
         for (int g = 0; g < 4; g++) {
@@ -372,6 +499,61 @@ __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const Pref
     // rows past T attend to nothing
     const int key_hi = row_ok ? my_qp : -1;
     const int key_lo = P.is_swa ? max(my_qp - (P.window - 1), 0) : 0;
+    // wave-uniform: does any row of this block need masking in the tile at key kp0?
+    auto edge = [&](int kp0) { return kp0 + 31 > q_first || (P.is_swa && q_last - kp0 >= P.window) || t0 + PF_BQ > P.T; };
+    int E = 0;  // acc holds sum p V in units of 2^E (E != 0 only on the scaled path)
+
+    if (scaled) {
+        // ---- scaled path: some tile's K or V values were stored scaled by 2^-eK_t / 2^-eV_t to
+        //      fit f16, or q by 2^-eQ (rare: values beyond f16's range, or tiny V tiles).
+        //      Tile by tile, without the software pipeline: the scores of tile t are
+        //      2^(eK_t + eQ) K'Q'^T (exact power-of-two factors), the running max is exact
+        //      (no margin), and acc accumulates p V' 2^(eV_t - E) with E the largest V exponent
+        //      so far (acc is rescaled when it grows). ----
+        const int *te = P.texp + (size_t)kvh * (P.k_rows >> 5);
+        for (int t = t_lo; t <= t_hi; t++) {
+            __syncthreads();  // every wave is done with the previous tile's LDS
+            {
+                PfTile Rt;
+                pf_gload(Rt, skv + (size_t)t * (PF_TILE_UNITS * 8), tid);
+                pf_lstore(Rt, ring[0], tid);
+            }
+            __syncthreads();
+            f16x8 kf[8], vf[8];
+#pragma unroll
+            for (int st = 0; st < 8; st++) kf[st] = ring[0][st][lane];
+#pragma unroll
+            for (int i = 0; i < 8; i++) vf[i] = ring[0][8 + i][lane];
+            const int tx = te[t];  // wave-uniform
+            const int eK = (int)(int16_t)(tx & 0xffff), eV = tx >> 16;
+            f32x16 sc = pf_scores(kf, qf, f32x16{});
+            const float ssc = __builtin_amdgcn_ldexpf(1.f, eK + eQ);
+#pragma unroll
+            for (int e = 0; e < 16; e++) sc[e] *= ssc;
+            if (edge(P.kbase + 32 * t)) pf_mask(sc, P.kbase + 32 * t, hh, key_lo, key_hi);
+            float mt = sc[0];
+#pragma unroll
+            for (int e = 1; e < 16; e++) mt = fmaxf(mt, sc[e]);
+            const float m_new = fmaxf(m, xor32_max(mt));  // m is finite (it starts at the sink)
+            const float corr = __builtin_amdgcn_exp2f(m - m_new);
+            if (t == t_lo) E = eV;
+            const float vgrow = eV > E ? __builtin_amdgcn_ldexpf(1.f, E - eV) : 1.f;
+            E = max(E, eV);
+            m = m_new;
+            l *= corr;
+#pragma unroll
+            for (int dt = 0; dt < 4; dt++) acc[dt] *= corr * vgrow;
+            const float pscale = __builtin_amdgcn_ldexpf(1.f, eV - E);
+            f16x8 pf[2];
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const float p = __builtin_amdgcn_exp2f(sc[e] - m);
+                l += p;
+                pf[e >> 3][e & 7] = (_Float16)(p * pscale);
+            }
+            pf_pv(acc, vf, pf);
+        }
+    } else {
 
     // ---- software pipeline over the key tiles. Step t computes P of tile t and its P V
     //      product while the score MFMAs of tile t + 1 run, in explicit slots with a
@@ -394,8 +576,6 @@ __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const Pref
     if (t_lo + 4 <= t_hi) pf_gload(R, skv + (size_t)(t_lo + 4) * (PF_TILE_UNITS * 8), tid);
     __syncthreads();
 
-    // wave-uniform: does any row of this block need masking in the tile at key kp0?
-    auto edge = [&](int kp0) { return kp0 + 31 > q_first || (P.is_swa && q_last - kp0 >= P.window) || t0 + PF_BQ > P.T; };
     f16x8 kf[8], vf[8];
 #pragma unroll
     for (int st = 0; st < 8; st++) kf[st] = ring[0][st][lane];
@@ -470,12 +650,13 @@ __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const Pref
         pf_softmax(s_cur, pf, l);
         pf_pv(acc, vf, pf);
     }
+    }  // fast path
 
     // ---- output rows, normalised, through this wave's LDS area (32 rows x 64 dims of
     //      f32 at a time; float4 column c of row r at r * 16 + (c ^ (r & 15)), so both
     //      sides are conflict-free) and stored row-coalesced: 16 lanes write one row's
     //      256 bytes ----
-    const float inv = 1.0f / xor32_sum(l);  // rows past T: l = 1, acc = 0
+    const float inv = __builtin_amdgcn_ldexpf(1.0f / xor32_sum(l), E);  // rows past T: l = 1, acc = 0
     float4 *const ob = (float4 *)&q_lds[wave][0][0];
 #pragma unroll
     for (int half = 0; half < 2; half++) {
@@ -497,9 +678,9 @@ __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const Pref
 }
 
 hipError_t launch_prefill(const PrefillParams &P, int dtype, hipStream_t stream) {
-    const int n_pre = P.p0 - P.kbase;
+    const int n_pre = (P.p0 - P.kbase + 31) >> 5;  // tiles holding cached positions (kbase 32-aligned)
     const int nqb = (P.T + PF_BQ - 1) / PF_BQ;
-    const dim3 gp((n_pre + 63) / 64, N_HEAD_KV), gk(((P.p0 + P.T + 31) >> 5) - (P.p0 >> 5), N_HEAD_KV);
+    const dim3 gp(n_pre, N_HEAD_KV), gk(((P.p0 + P.T + 31) >> 5) - (P.p0 >> 5), N_HEAD_KV);
     if (dtype == DT_F16) {
         if (n_pre > 0) hipLaunchKernelGGL(prefix_kernel<DT_F16>, gp, dim3(256), 0, stream, P);
         hipLaunchKernelGGL(kv_prep_kernel<DT_F16>, gk, dim3(256), 0, stream, P);

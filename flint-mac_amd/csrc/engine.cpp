@@ -9,6 +9,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -254,9 +255,17 @@ void prefill_impl(const flint_attn_layer *L, const float *qkv, int q_stride, int
         P.kbase = 0;
     }
     P.k_rows = ((p0 + T - P.kbase) + PREFILL_ROW_ALIGN - 1) / PREFILL_ROW_ALIGN * PREFILL_ROW_ALIGN;
-    DeviceScratch &ws = scratch();
-    // zeroed when allocated: rows past the valid keys must hold finite values
-    P.sk = (_Float16 *)ws.kv.get((size_t)N_HEAD_KV * P.k_rows * 2 * HEAD_DIM * sizeof(_Float16), true);
+    // the attention copy, then its table of per-tile exponents (every tile the flash kernel reads
+    // is written in this call, padding rows included)
+    const size_t copy_bytes = (size_t)N_HEAD_KV * P.k_rows * 2 * HEAD_DIM * sizeof(_Float16);
+    char *ws = (char *)scratch().kv.get(copy_bytes + (size_t)N_HEAD_KV * (P.k_rows / 32) * sizeof(int));
+    P.sk = (_Float16 *)ws;
+    P.texp = (int *)(ws + copy_bytes);
+    // a nonzero id per call: the kernels flag a call that stored scaled tiles with its id
+    static std::atomic<uint32_t> next_call{0};
+    uint32_t id = ++next_call;
+    if (id == 0) id = ++next_call;
+    P.call_id = id;
     check(launch_prefill(P, L->kv_dtype, stream), "prefill launch");
 }
 

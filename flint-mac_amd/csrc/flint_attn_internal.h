@@ -62,6 +62,10 @@ struct PrefillParams {
     // kbase .. p0 + T - 1 at rows 0 .., k_rows rows per kv head (multiple of PREFILL_ROW_ALIGN)
     _Float16 *sk;
     int k_rows, kbase;
+    // per kv head and 32-key tile of the copy: the power-of-two exponents its K and V values
+    // were scaled by to fit f16, (eK & 0xffff) | eV << 16 ([4][k_rows / 32]; 0 = stored as is)
+    int *texp;
+    unsigned call_id;     // nonzero id of this call (see g_scaled_call in attn_prefill.hip)
     float *att;           // [T][4096]
 };
 

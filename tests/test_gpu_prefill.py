@@ -207,3 +207,52 @@ def test_prefill_after_rollback_swa_ring(cuda, rollback):
     want = _oracle_at(L, qkv_b, K, V, [p, p + 1, p + 31, p + 300, m - 1])
     for q, w in want.items():
         assert_close(got[q], w, f"rollback {rollback} pos {q}")
+
+
+@pytest.mark.parametrize("case", ["v_rows_1e5_1e-6", "v_all_1e-6", "k_gain_1e4_q_gain_1e-4"])
+@pytest.mark.parametrize("is_swa", [False, True], ids=["full", "swa"])
+def test_prefill_then_decode_bf16_beyond_f16_range(cuda, case, is_swa):
+    """bf16 K/V outside f16's range on one bf16 cache: V rows scaled to 1e5 (past f16's 65504)
+    and to 1e-6 (f16 subnormals), all of V at 1e-6, or K gains x1e4 (normalised K past 65504)
+    with q gains x1e-4. Prefill of 1300 tokens in two calls (700 + 600: the second copies whole
+    cached tiles and the part-cached tile of p0 = 700), then 4 decode steps on the same cache;
+    every position against the oracle. The prefill stores such tiles in f16 scaled by a power
+    of two and takes its scaled path; on the SWA layer the window masks large rows of earlier
+    positions. Errors are measured relative to each output row's largest magnitude (at least
+    1), at the usual bars; the ring / cache slots are bit-exact against the oracle's."""
+    _say(f"prefill + decode bf16 beyond f16 range: {case} swa={is_swa}")
+    rng = np.random.default_rng(71)
+    qn, kn, sk = layer_weights(rng)
+    n = 1304
+    qkv = rng.standard_normal((n, QKV_DIM)).astype(np.float32)
+    if case == "v_rows_1e5_1e-6":
+        qkv[3::7, 4608:] *= 1e5
+        qkv[5::11, 4608:] *= 1e-6
+    elif case == "v_all_1e-6":
+        qkv[:, 4608:] *= 1e-6
+    else:
+        kn = (kn * 1e4).astype(np.float32)
+        qn = (qn * 1e-4).astype(np.float32)
+    kv = fa.KVLayer(is_swa=is_swa, has_rope=True, n_slots=1024 if is_swa else 1312, kv_dtype="bf16",
+                    rope_theta=1e4, q_norm=qn, k_norm=kn, sinks=sk)
+    L = oracle_layer(kv, qn, kn, sk, "bf16")
+    dq = torch.from_numpy(qkv).to(cuda)
+    att = torch.zeros((n, Q_DIM), device=cuda)
+    kv.prefill(dq[:700], att[:700], 0)
+    kv.prefill(dq[700:1300], att[700:1300], 700)
+    for pos in range(1300, n):
+        kv.decode(dq[pos], att[pos], pos)
+    torch.cuda.synchronize()
+    got = att.cpu().numpy().astype(np.float64)
+    K = np.zeros((n, KV_DIM), np.float32)
+    V = np.zeros((n, KV_DIM), np.float32)
+    want = fo.prefill(L, qkv, 0, K, V, n_threads=16).astype(np.float64)
+    assert np.all(np.isfinite(got)), "non-finite output"
+    scale = np.maximum(1.0, np.abs(want).max(axis=1, keepdims=True))
+    if case == "v_all_1e-6":
+        scale = np.abs(want).max(axis=1, keepdims=True)
+    assert_close(got[:1300] / scale[:1300], want[:1300] / scale[:1300], f"{case}: prefill rows")
+    assert_close(got[1300:] / scale[1300:], want[1300:] / scale[1300:], f"{case}: decode rows")
+    vc = kv.v_slots()[0].float().cpu().numpy()
+    for p in range(max(0, n - 1024) if is_swa else 0, n):
+        assert np.array_equal(vc[:, kv.slot(p), :], V[p].reshape(N_HEAD_KV, HEAD_DIM)), f"V slot of pos {p}"
