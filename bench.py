@@ -6,17 +6,20 @@ LSE merge + sink). One step = one decode token through 8 full-attention layers,
 each with its own 64 MiB KV cache, so a step streams 512 MiB and the 256 MB
 Infinity Cache cannot serve it. value = algorithmic KV bytes / step time (GB/s).
 
-Also reported on the same line: decode tok/s at 32k (Flint's 14 full + 35 SWA
-layers, attention only), prefill attention TFLOPS at 4000 tokens (config 4,
-bf16 KV, full causal and SWA-513), the 16-sequence mixed-context decode
-(config 5), the decode kernel's roofline, and the CPU oracle's decode rate on
-this host (cpu_baseline; a reported baseline, not the target).
+Also on the same line:
+  * a whole decode step of the attention stage at 32k, timed: Flint's 14 full (pos 32768)
+    + 35 SWA layers back to back, each with its own cache (decode_step_49_layers_32k);
+  * prefill attention at 4000 tokens (config 4, bf16 KV, full causal and SWA-513), with a
+    roofline object per layer kind;
+  * the 16-sequence mixed-context decode (config 5);
+  * the attention blocks read from a 49-layer GGUF model (q8_0 q/k/v/o projections +
+    attention): one layer of each kind, a whole decode step at 32k, and the layer-major
+    prefill of 4000 tokens (flint_attn_model_prefill);
+  * the CPU oracle on every core of this host (cpu_baseline; a reported baseline, not the
+    target): config-3 decode GB/s and config-4 prefill TFLOPS.
 
-Also on the line: the attention block of a decode step read from a GGUF model (q8_0 q/k/v/o
-projections + attention; full layer at 32k and SWA layer), per layer and as tok/s for Flint's
-layer mix.
-
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only decode|prefill|config5|blocks]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+                       [--only decode|prefill|prefill_full|prefill_swa|config5|model]
 """
 import argparse
 import json
@@ -29,11 +32,17 @@ sys.path.insert(0, os.path.join(ROOT, "flint-mac_amd"))
 
 HBM_PEAK_GBS = 8000.0       # MI355X HBM3E
 MFMA_PEAK_TFLOPS = 2500.0   # MI355X dense bf16/f16 MFMA
-N_FULL_FLINT, N_SWA_FLINT = 14, 35
 # HBM bytes per decode call (attn_decode_kernel + attn_combine_kernel) at 32k, from rocprofv3
 # --pmc FETCH_SIZE and WRITE_SIZE runs of `bench.py --only decode --no-cpu`, each scaled by the
 # counter's reading for the 64 MiB calibration copy (profiles/decode_32k_f16.md).
 DECODE_TRAFFIC_BYTES = 68915950
+# HBM bytes per prefill call (kv_prep_kernel + flash_prefill_kernel) at T = 4000, bf16 KV, from
+# rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs of `bench.py --only prefill_full|prefill_swa
+# --no-cpu`, scaled like the decode figure (profiles/prefill_4000_bf16.md); None = not measured.
+PREFILL_TRAFFIC_BYTES = {"full": None, "swa": None}
+# Flint's 49 layers: full attention (no RoPE) at layers 0, 48 and i % 4 == 1, SWA + RoPE elsewhere
+# (/root/reference/src/metal/flint_config.h:37-38): 14 full, 35 SWA
+FLINT_FULL_LAYERS = [i == 0 or i == 48 or i % 4 == 1 for i in range(49)]
 
 
 def log(msg):
@@ -74,7 +83,7 @@ def queued_launch_ms(torch, step, reps, warmup=2):
     torch.cuda.synchronize()
     host_ms = (time.perf_counter() - t0) * 1e3
     e_spin, e0, e1 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
-    _sleep_ms(torch, min(2.0 * host_ms * reps + 5.0, 2000.0))
+    _sleep_ms(torch, min(4.0 * host_ms * reps + 20.0, 5000.0))
     e_spin.record()
     e0.record()
     for _ in range(reps):
@@ -156,14 +165,49 @@ def bench_decode_swa(torch, fa, reps=200, pos=32768):
     return queued_launch_ms(torch, step, max(1, reps // n))[0] / n
 
 
-def bench_prefill(torch, fa, T=4000, reps=10):
+def bench_decode_step_49(torch, fa, steps=20, ctx=32768):
+    """A whole decode step of the attention stage at 32k, timed: Flint's 49 layers in order
+    (14 full at pos 32768, each with its own 64 MiB cache, and 35 SWA layers with their rings),
+    one flint_attn_decode per layer, back to back on one stream (Engine::step's attention
+    stages, engine.mm:902-940 / 735-766)."""
+    import numpy as np
+    dev = torch.device("cuda:0")
+    rng = np.random.default_rng(7)
+    layers = []
+    for full in FLINT_FULL_LAYERS:
+        kv = fa.KVLayer(is_swa=not full, has_rope=not full, n_slots=ctx + 32 if full else 1024, kv_dtype="f16",
+                        q_norm=rng.uniform(0.5, 1.5, 128), k_norm=rng.uniform(0.5, 1.5, 128),
+                        sinks=rng.standard_normal(32), device=dev)
+        kv.k.normal_()
+        kv.v.normal_()
+        layers.append(kv)
+    qkv = torch.randn((len(layers), 5120), device=dev)
+    att = torch.empty((len(layers), 4096), device=dev)
+
+    def step():
+        for i, kv in enumerate(layers):
+            kv.decode(qkv[i], att[i], ctx)
+
+    ms, host_bound = queued_launch_ms(torch, step, steps, 2)
+    nbytes = sum(decode_bytes(ctx) if full else decode_bytes(512) for full in FLINT_FULL_LAYERS)
+    del layers
+    torch.cuda.empty_cache()
+    return dict(ms_per_step=ms, tok_s=1.0 / (ms * 1e-3), gbs=nbytes / (ms * 1e-3) / 1e9, bytes_per_step=nbytes,
+                n_full=sum(FLINT_FULL_LAYERS), n_swa=len(FLINT_FULL_LAYERS) - sum(FLINT_FULL_LAYERS),
+                host_bound=host_bound)
+
+
+def bench_prefill(torch, fa, T=4000, reps=10, kinds=("full", "swa")):
+    """Config 4: one prefill call of T = 4000 tokens from position 0 (kv_prep_kernel + flash_prefill_kernel),
+    bf16 KV, per layer kind; time per call from HIP events around `reps` calls on the launching stream."""
     import numpy as np
     dev = torch.device("cuda:0")
     rng = np.random.default_rng(3)
     out = {}
     qkv = torch.randn((T, 5120), device=dev)
     att = torch.empty((T, 4096), device=dev)
-    for name, is_swa in (("full", False), ("swa", True)):
+    for name in kinds:
+        is_swa = name == "swa"
         kv = fa.KVLayer(is_swa=is_swa, has_rope=is_swa, n_slots=1024 if is_swa else T, kv_dtype="bf16",
                         q_norm=rng.uniform(0.5, 1.5, 128), k_norm=rng.uniform(0.5, 1.5, 128),
                         sinks=rng.standard_normal(32), device=dev)
@@ -178,8 +222,16 @@ def bench_prefill(torch, fa, T=4000, reps=10):
         torch.cuda.synchronize()
         ms = e0.elapsed_time(e1) / reps
         flops = prefill_flops(T, 513 if is_swa else None)
-        out[name] = dict(ms=ms, flops=flops, tflops=flops / (ms * 1e-3) / 1e12,
-                         frac_of_mfma_peak=flops / (ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS)
+        tflops = flops / (ms * 1e-3) / 1e12
+        out[name] = dict(ms=ms, flops=flops, tflops=tflops, frac_of_mfma_peak=tflops / MFMA_PEAK_TFLOPS,
+                         roofline={"bound": "mfma", "achieved": round(tflops, 1), "peak": MFMA_PEAK_TFLOPS,
+                                   "unit": "TFLOP/s", "frac": round(tflops / MFMA_PEAK_TFLOPS, 4),
+                                   "traffic": PREFILL_TRAFFIC_BYTES[name],
+                                   "kernel": "one flint_attn_prefill call on a " + ("SWA-513" if is_swa else "full causal")
+                                             + " layer = kv_prep_kernel + flash_prefill_kernel (f16 MFMA 32x32x16 on "
+                                             "the exact f16 copy of the bf16 K/V); achieved = algorithmic FLOPs / "
+                                             "time per call from HIP events"})
+        del kv
     return out
 
 
@@ -215,13 +267,18 @@ def bench_config5(torch, fa, steps=3):
                 bytes_per_step=nbytes)
 
 
-def bench_blocks(torch, fa, reps=96, ctx=32768):
-    """The attention block of a decode step read from a GGUF file (include/flint_model.h):
-    RMSNorm + q/k/v projections, attention, o projection + residual, with q8_0 weights in
-    Flint's shapes (random N(0, 1/k) rows, ggml's q8_0 rounding). One full layer at `ctx` cached
-    positions and one SWA layer (window 513). The caches hold zeros: the kernels read every byte
-    whatever the values. Each block and its attention stage alone are timed like the decode
-    line; the projections are the difference."""
+def bench_model(torch, fa, reps=48, ctx=32768, T_prefill=4000):
+    """The attention blocks of a 49-layer Flint GGUF (include/flint_model.h): RMSNorm + q/k/v
+    projections, attention, o projection + residual, with q8_0 weights in Flint's shapes (random
+    N(0, 1/k) rows with ggml's q8_0 rounding; one set of rows written into every layer, each layer
+    its own copy in HBM) and Flint's layer pattern. The caches hold zeros: the kernels read every
+    byte whatever the values.
+      * one full layer at `ctx` cached positions and one SWA layer, each block and its attention
+        stage alone timed like the decode line (the projections are the difference);
+      * a whole decode step at ctx: the embedding row, then the 49 blocks at position ctx
+        (what flint_attn_model_step runs at that position);
+      * flint_attn_model_prefill of T_prefill tokens from position 0 (embedding, then layer-major
+        blocks)."""
     import ctypes
     import tempfile
     import numpy as np
@@ -233,68 +290,128 @@ def bench_blocks(torch, fa, reps=96, ctx=32768):
     def q8(n, k):
         return gw.quantize_q8_0((rng.standard_normal((n, k)) / np.sqrt(k)).astype(np.float32))
 
-    tensors = [("token_embd.weight", rng.standard_normal((16, E)).astype(np.float32), gw.T_F16),
+    rows = {name: (q8(n, k), (k, n)) for name, n, k in
+            (("attn_q", 4096, E), ("attn_k", 512, E), ("attn_v", 512, E), ("attn_output", E, 4096))}
+    wbytes = sum(r.nbytes for r, _ in rows.values())
+    n_vocab = 1024
+    tensors = [("token_embd.weight", rng.standard_normal((n_vocab, E)).astype(np.float32), gw.T_F16),
                ("output_norm.weight", np.ones(E, np.float32), gw.T_F32),
                ("output.weight", np.zeros((1, E), np.float32), gw.T_F16)]
-    wbytes = 0
-    for il in range(2):
+    for il in range(len(FLINT_FULL_LAYERS)):
         b = f"blk.{il}."
         tensors.append((b + "attn_norm.weight", rng.uniform(0.5, 1.5, E).astype(np.float32), gw.T_F32))
-        for name, n, k in (("attn_q", 4096, E), ("attn_k", 512, E), ("attn_v", 512, E), ("attn_output", E, 4096)):
-            rows = q8(n, k)
-            wbytes += rows.nbytes if il == 0 else 0
-            tensors.append((b + name + ".weight", rows, 8, (k, n)))
+        for name, (r, dims) in rows.items():
+            tensors.append((b + name + ".weight", r, 8, dims))
         tensors += [(b + "attn_q_norm.weight", rng.uniform(0.5, 1.5, 128).astype(np.float32), gw.T_F32),
                     (b + "attn_k_norm.weight", rng.uniform(0.5, 1.5, 128).astype(np.float32), gw.T_F32),
                     (b + "attn_sinks.weight", rng.standard_normal(32).astype(np.float32), gw.T_F32)]
         tensors += gw.flint_zero_ffn(il)
+    is_swa = [not f for f in FLINT_FULL_LAYERS]
     with tempfile.TemporaryDirectory() as tmp:
-        path = os.path.join(tmp, "blocks.gguf")
-        gw.write_gguf(path, gw.flint_meta([0, 1], [0, 1], 513, 1.0e4), tensors)
+        path = os.path.join(tmp, "flint49.gguf")
+        gw.write_gguf(path, gw.flint_meta(is_swa, is_swa, 513, 1.0e4), tensors)
+        del tensors
         model = fa.Model(path, n_ctx=ctx + 32)
     x = torch.randn(E, device=dev) * 0.1
     qkv = torch.randn(5120, device=dev)
     att = torch.empty(4096, device=dev)
     out = {}
-    for il, name in ((0, "full"), (1, "swa")):
+    full_il, swa_il = FLINT_FULL_LAYERS.index(True), FLINT_FULL_LAYERS.index(False)
+    for il, name in ((full_il, "full"), (swa_il, "swa")):
         desc = model.layer(il)
         t_block = queued_launch_ms(torch, lambda: model.block_decode(il, x, ctx, att), reps)[0]
         t_attn = queued_launch_ms(
             torch, lambda: fa._call(fa.lib().flint_attn_decode, ctypes.byref(desc), fa._ptr(qkv), fa._ptr(att), ctx,
                                     0, ctypes.c_void_p(fa._stream(None))), reps)[0]
         out[name] = dict(block_ms=t_block, attn_ms=t_attn, proj_ms=t_block - t_attn)
-    model.close()
     t_proj = 0.5 * (out["full"]["proj_ms"] + out["swa"]["proj_ms"])
+
+    def step():
+        model.embed([17], x)
+        for il in range(len(FLINT_FULL_LAYERS)):
+            model.block_decode(il, x, ctx, att)
+
+    t_step, step_host_bound = queued_launch_ms(torch, step, 8)
+    # layer-major prefill of T_prefill tokens from position 0
+    tokens = [int(t) for t in rng.integers(0, n_vocab, T_prefill)]
+    X = torch.empty((T_prefill, E), device=dev)
+    model.truncate(0)
+    model.prefill(tokens, X)  # warm-up (workspace growth)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    n_rep = 2
+    e0.record()
+    for _ in range(n_rep):
+        model.truncate(0)
+        model.prefill(tokens, X)
+    e1.record()
+    torch.cuda.synchronize()
+    t_prefill = e0.elapsed_time(e1) / n_rep
+    model.close()
     return dict(full_32k_block_ms=out["full"]["block_ms"], swa_block_ms=out["swa"]["block_ms"],
                 full_32k_attn_ms=out["full"]["attn_ms"], swa_attn_ms=out["swa"]["attn_ms"],
                 proj_ms=t_proj, proj_weight_bytes=wbytes, proj_gbs=wbytes / (t_proj * 1e-3) / 1e9,
-                tok_s_32k=1.0 / ((N_FULL_FLINT * out["full"]["block_ms"] + N_SWA_FLINT * out["swa"]["block_ms"])
-                                 * 1e-3))
+                step_49_layers_32k_ms=t_step, step_tok_s_32k=1.0 / (t_step * 1e-3), step_host_bound=step_host_bound,
+                prefill_4000_ms=t_prefill, prefill_4000_tok_s=T_prefill / (t_prefill * 1e-3))
 
 
-def cpu_baseline(target_s=10.0):
-    """The CPU oracle (C restatement of the reference's CPU attention) on this host:
-    config-3 decode steps (32768 cached positions, f16-rounded KV)."""
+def cpu_baseline(decode_s=10.0, prefill_s=6.0):
+    """The CPU oracle (C restatement of the reference's CPU attention, ref_model.cpp:95-149) on every
+    core this process may use: config-3 decode steps (32768 cached f16-rounded positions; threads over
+    the 32 q heads, so at most 32) and config-4 prefill (T = 4000, bf16-rounded KV; (row, head) pairs
+    over all cores) on a sample of rows, full causal and SWA-513, as TFLOPS over the sample's
+    algorithmic FLOPs."""
     import numpy as np
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as fo
-    threads = min(os.cpu_count() or 1, 16)
+    cores = len(os.sched_getaffinity(0))
+    dthreads = min(cores, 32)
     rng = np.random.default_rng(2)
     n = 32768
     L = fo.Layer(rng.uniform(0.5, 1.5, 128), rng.uniform(0.5, 1.5, 128), rng.standard_normal(32), 0, 0, "f16")
     K = fo.round_store(rng.standard_normal((n + 1, 512)).astype(np.float32), "f16")
     V = fo.round_store(rng.standard_normal((n + 1, 512)).astype(np.float32), "f16")
     qkv = rng.standard_normal(5120).astype(np.float32)
-    fo.decode_step(L, qkv, n, K, V, n_threads=threads)
+    fo.decode_step(L, qkv, n, K, V, n_threads=dthreads)
     reps, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < target_s:
-        fo.decode_step(L, qkv, n, K, V, n_threads=threads)
+    while time.perf_counter() - t0 < decode_s:
+        fo.decode_step(L, qkv, n, K, V, n_threads=dthreads)
         reps += 1
     dt = (time.perf_counter() - t0) / reps
-    return dict(value=decode_bytes(n) / dt / 1e9, unit="GB/s", cores=threads, kind="port",
-                sample=f"{reps} decode steps of config 3 (32768 cached f16-rounded positions, fp32 scores, "
-                       f"double softmax*V) on {threads} threads, {dt * 1e3:.1f} ms/step",
-                tok_s_32k_one_layer=1.0 / dt)
+    del K, V
+    # config 4: sample rows at the end of the prompt (the longest key ranges of the full layer)
+    T = 4000
+    rng = np.random.default_rng(3)
+    qkv4 = rng.standard_normal((T, 5120)).astype(np.float32)
+    pre = {}
+    for name, is_swa in (("full", 0), ("swa", 1)):
+        Lp = fo.Layer(rng.uniform(0.5, 1.5, 128), rng.uniform(0.5, 1.5, 128), rng.standard_normal(32), is_swa, is_swa,
+                      "bf16", 1e4)
+        Kp = np.zeros((T, 512), np.float32)
+        Vp = np.zeros((T, 512), np.float32)
+        # q/k/v of all 4000 tokens alone (no rows), then 64 rows to calibrate, then a sample of rows
+        # sized to ~prefill_s seconds; the sample is charged its share (rows / T) of the q/k/v time
+        r1 = T
+        t0 = time.perf_counter()
+        fo.prefill_rows(Lp, qkv4, 0, Kp, Vp, r1, r1, n_threads=cores)
+        t_prep = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        fo.prefill_rows(Lp, qkv4, 0, Kp, Vp, r1 - 64, r1, n_threads=cores)
+        per_row = max(time.perf_counter() - t0 - t_prep, 1e-6) / 64
+        rows = int(min(T, max(64, prefill_s / per_row)))
+        t0 = time.perf_counter()
+        fo.prefill_rows(Lp, qkv4, 0, Kp, Vp, r1 - rows, r1, n_threads=cores)
+        dtp = max(time.perf_counter() - t0 - t_prep, 1e-6) + t_prep * rows / T
+        keys = sum(min(i + 1, 513) if is_swa else i + 1 for i in range(r1 - rows, r1))
+        flops = 4 * 32 * 128 * keys
+        pre[name] = dict(tflops=flops / dtp / 1e12, rows=rows, seconds=dtp)
+    return dict(value=decode_bytes(n) / dt / 1e9, unit="GB/s", cores=cores, kind="port",
+                sample=f"config 3: {reps} decode steps (32768 cached f16-rounded positions, fp32 scores, double "
+                       f"softmax*V) on {dthreads} threads (one per q head at most), {dt * 1e3:.1f} ms/step; config 4: "
+                       f"the last {pre['full']['rows']} (full) / {pre['swa']['rows']} (SWA) of 4000 prefill rows "
+                       f"on {cores} threads, charged their share of the 4000 tokens' q/k/v prep",
+                decode_threads=dthreads, tok_s_32k_one_layer=1.0 / dt,
+                prefill_4000_full_tflops=pre["full"]["tflops"], prefill_4000_swa_tflops=pre["swa"]["tflops"])
 
 
 def main():
@@ -303,7 +420,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["decode", "prefill", "config5", "blocks"], default=None)
+    ap.add_argument("--only", choices=["decode", "prefill", "prefill_full", "prefill_swa", "config5", "model"],
+                    default=None)
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build runs on one GPU. The attention path would shard by key range (decode, "
@@ -321,21 +439,24 @@ def main():
         res["decode"] = bench_decode_32k(torch, fa, args.steps, args.warmup)
         log(f"decode: {res['decode']}")
         res["swa_ms"] = bench_decode_swa(torch, fa)
-        calibration_copy(torch)
         log(f"swa decode per layer: {res['swa_ms']:.4f} ms")
-    if args.only in (None, "prefill"):
-        log("prefill 4000 (config 4)")
-        res["prefill"] = bench_prefill(torch, fa)
+        res["step49"] = bench_decode_step_49(torch, fa)
+        log(f"decode step, 49 layers at 32k: {res['step49']}")
+        calibration_copy(torch)
+    if args.only in (None, "prefill", "prefill_full", "prefill_swa"):
+        kinds = {"prefill_full": ("full",), "prefill_swa": ("swa",)}.get(args.only, ("full", "swa"))
+        log(f"prefill 4000 (config 4): {kinds}")
+        res["prefill"] = bench_prefill(torch, fa, kinds=kinds)
         log(f"prefill: {res['prefill']}")
     if args.only in (None, "config5"):
         log("config 5: 16 sequences x 48 layers")
         res["config5"] = bench_config5(torch, fa)
         log(f"config5: ms {res['config5']['ms_per_step']:.3f} tok/s {res['config5']['tok_s']:.1f} "
             f"GB/s {res['config5']['gbs']:.1f}")
-    if args.only in (None, "blocks"):
-        log("attention blocks from a GGUF model (q8_0 projections)")
-        res["blocks"] = bench_blocks(torch, fa)
-        log(f"blocks: {res['blocks']}")
+    if args.only in (None, "model"):
+        log("attention blocks of a 49-layer GGUF model (q8_0 projections)")
+        res["model"] = bench_model(torch, fa)
+        log(f"model: {res['model']}")
     cpu = None
     if not args.no_cpu:
         log("cpu baseline")
@@ -351,6 +472,7 @@ def main():
         d = res["decode"]
         t_full = d["avg_launch_ms"]
         t_swa = res["swa_ms"]
+        s49 = res["step49"]
         line.update({
             "value": round(d["gbs"], 1),
             "ms_per_step": round(d["ms_per_step"], 5),
@@ -358,7 +480,12 @@ def main():
                                    "32 q / 4 kv heads, d=128, split-K + LSE merge + sink; step = 8 layers with "
                                    "their own KV (512 MiB streamed per step)",
                        "context": 32768, "layers_per_step": d["n_layers"], "kv_dtype": "f16"},
-            "decode_tok_s_32k": round(1.0 / ((N_FULL_FLINT * t_full + N_SWA_FLINT * t_swa) * 1e-3), 1),
+            "decode_tok_s_32k": round(s49["tok_s"], 1),
+            "decode_step_49_layers_32k": {"ms": round(s49["ms_per_step"], 5), "tok_s": round(s49["tok_s"], 1),
+                                          "gbs": round(s49["gbs"], 1), "bytes_per_step": s49["bytes_per_step"],
+                                          "layers": f"{s49['n_full']} full (pos 32768) + {s49['n_swa']} SWA, "
+                                                    "flint_config.h:37-38 order, one flint_attn_decode each, timed "
+                                                    "as one sequence", "host_bound": s49["host_bound"]},
             "decode_ms_per_layer_full_32k": round(t_full, 5),
             "decode_ms_per_layer_swa": round(t_swa, 5),
             "roofline": {"bound": "hbm", "achieved": round(d["bytes_per_launch"] / (t_full * 1e-3) / 1e9, 1),
@@ -377,11 +504,11 @@ def main():
         c = res["config5"]
         line["config5_16seq_48layers"] = {"ms_per_step": round(c["ms_per_step"], 4), "tok_s": round(c["tok_s"], 1),
                                           "gbs": round(c["gbs"], 1), "bytes_per_step": c["bytes_per_step"]}
-    if "blocks" in res:
-        line["attention_block_decode_q8_0"] = {k: (round(v, 5) if isinstance(v, float) else v)
-                                               for k, v in res["blocks"].items()}
+    if "model" in res:
+        line["attention_blocks_q8_0_49_layers"] = {k: (round(v, 5) if isinstance(v, float) else v)
+                                                   for k, v in res["model"].items()}
     if cpu:
-        line["cpu_baseline"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in cpu.items()}
+        line["cpu_baseline"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in cpu.items()}
     print(json.dumps(line), flush=True)
 
 

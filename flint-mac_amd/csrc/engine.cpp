@@ -288,15 +288,35 @@ int64_t w_row_bytes(int type, int64_t k) {
 
 bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
-void get_row_impl(int type, const void *w, int64_t k, int64_t row, float *out, hipStream_t stream) {
+// rows[0 .. n) of a tensor with rows of k elements into out[i * k ..], GR_MAX_ROWS per launch
+void get_rows_impl(int type, const void *w, int64_t k, const int64_t *rows, int64_t n_rows_max, int n, float *out,
+                   hipStream_t stream, const char *what) {
+    const std::string tag(what);
     const int64_t rb = w_row_bytes(type, k);
-    if (rb < 0) throw Error("get_row: unsupported weight type or row length");
-    if (!w || !out) throw Error("get_row: NULL pointer");
-    if (row < 0) throw Error("get_row: negative row");
-    if (k > (int64_t)1 << 30) throw Error("get_row: row too long");
-    if (!aligned16(out)) throw Error("get_row: out must be 16-byte aligned");
-    if ((((uintptr_t)w + (uintptr_t)(row * rb)) & 1) != 0) throw Error("get_row: row data must be 2-byte aligned");
-    check(launch_get_row((const uint8_t *)w + row * rb, type, k, out, stream), "get_row launch");
+    if (rb < 0) throw Error(tag + ": unsupported weight type or row length");
+    if (!w || !out || !rows) throw Error(tag + ": NULL pointer");
+    if (n < 1) throw Error(tag + ": no rows");
+    if (k > (int64_t)1 << 30) throw Error(tag + ": row too long");
+    if (!aligned16(out)) throw Error(tag + ": out must be 16-byte aligned");
+    if (((uintptr_t)w & 1) || (rb & 1)) throw Error(tag + ": row data must be 2-byte aligned");
+    for (int i = 0; i < n; i++) {
+        if (rows[i] < 0) throw Error(tag + ": negative row");
+        if (n_rows_max >= 0 && rows[i] >= n_rows_max)
+            throw Error(tag + ": row " + std::to_string(rows[i]) + " out of range");
+        if (rows[i] > (int64_t)INT32_MAX) throw Error(tag + ": row index too large");
+    }
+    RowsParams P{};
+    P.w = (const uint8_t *)w;
+    P.row_bytes = rb;
+    P.out_stride = k;
+    P.type = type;
+    P.n_sub = (int)(k / 32);
+    for (int i0 = 0; i0 < n; i0 += GR_MAX_ROWS) {
+        P.n = std::min(GR_MAX_ROWS, n - i0);
+        P.out = out + (size_t)i0 * (size_t)k;
+        for (int i = 0; i < P.n; i++) P.rows[i] = (int)rows[i0 + i];
+        check(launch_get_rows(P, stream), (tag + " launch").c_str());
+    }
 }
 
 // rows of k elements of one matvec tensor: 16-byte aligned rows are what the kernel reads
@@ -370,7 +390,18 @@ int64_t flint_w_row_bytes(int32_t type, int64_t k) { return w_row_bytes(type, k)
 
 int32_t flint_w_get_row(int32_t type, const void *w, int64_t k, int64_t row, float *out, void *stream, char *err,
                         int32_t err_len) {
-    return guarded(err, err_len, [&] { get_row_impl(type, w, k, row, out, (hipStream_t)stream); });
+    return guarded(err, err_len, [&] { get_rows_impl(type, w, k, &row, -1, 1, out, (hipStream_t)stream, "get_row"); });
+}
+
+int32_t flint_w_get_rows(int32_t type, const void *w, int64_t k, int64_t n_rows, const int32_t *rows, int32_t n,
+                         float *out, void *stream, char *err, int32_t err_len) {
+    return guarded(err, err_len, [&] {
+        if (!rows) throw Error("get_rows: NULL pointer");
+        if (n < 1 || n > 1 << 24) throw Error("get_rows: n must be in [1, 2^24]");
+        if (n_rows < 1) throw Error("get_rows: n_rows must be >= 1");
+        std::vector<int64_t> r(rows, rows + n);
+        get_rows_impl(type, w, k, r.data(), n_rows, n, out, (hipStream_t)stream, "get_rows");
+    });
 }
 
 int32_t flint_attn_qkv_proj(const flint_weight *wq, const flint_weight *wk, const flint_weight *wv, const float *x,

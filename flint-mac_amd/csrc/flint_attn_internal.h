@@ -89,7 +89,16 @@ struct MatvecParams {
     int n_tok;             // tokens (grid x), >= 1
     long long x_stride, y_stride;
 };
-hipError_t launch_get_row(const uint8_t *row, int type, int64_t k, float *out, hipStream_t stream);
+// Rows rows[0 .. n) of a weight tensor (row_bytes each) dequantised into out + i * out_stride.
+constexpr int GR_MAX_ROWS = 448;  // rows per launch (the table travels in the kernel arguments)
+struct RowsParams {
+    const uint8_t *w;
+    long long row_bytes, out_stride;
+    float *out;
+    int type, n_sub, n;   // n_sub: 32-element sub-blocks per row; n <= GR_MAX_ROWS
+    int rows[GR_MAX_ROWS];
+};
+hipError_t launch_get_rows(const RowsParams &P, hipStream_t stream);
 hipError_t launch_matvec(const MatvecParams &P, int k, hipStream_t stream);
 int matvec_row_multiple(int k);  // n_rows of a matvec launch must be a multiple of this
 

@@ -283,10 +283,9 @@ int32_t flint_attn_model_embed(flint_attn_model *m, const int32_t *tokens, int32
             if (tokens[i] < 0 || tokens[i] >= m->embd_rows)
                 throw std::runtime_error("embed: token " + std::to_string(tokens[i]) + " out of range");
         char e2[512] = {0};
-        for (int i = 0; i < n; i++)
-            call(flint_w_get_row(m->embd.type, m->embd.data, FLINT_N_EMBD, tokens[i], x + (size_t)i * FLINT_N_EMBD,
-                                 stream, e2, sizeof(e2)),
-                 e2);
+        call(flint_w_get_rows(m->embd.type, m->embd.data, FLINT_N_EMBD, m->embd_rows, tokens, n, x, stream, e2,
+                              sizeof(e2)),
+             e2);
     });
 }
 

@@ -1,6 +1,7 @@
 // Attention projections in the engine's GGUF weight formats, for gfx950:
-//   * get_row_kernel: one row dequantised to fp32 (Engine::debug_get_row,
-//     /root/reference/src/engine.mm:1370-1383; kernel k_get_row, fused.metal:589-600);
+//   * get_rows_kernel: rows dequantised to fp32 (Engine::debug_get_row,
+//     /root/reference/src/engine.mm:1370-1383, kernel k_get_row, fused.metal:589-600; and
+//     the prefill's embedding, k_embed_rows, prefill.metal:272, engine.mm:1067-1069);
 //   * matvec_kernel: y = W x with 2048- or 4096-element rows, optionally on RMSNorm(x) * g
 //     (the q/k/v projections, engine.mm:728-732) or added to y (o_proj with the residual,
 //     engine.mm:811).
@@ -161,21 +162,24 @@ __device__ inline void deq32(int type, const uint8_t *row, int sb, float (&w)[32
 __device__ inline bool w_is_float(int t) { return t == W_F32 || t == W_F16 || t == W_BF16; }
 
 // ---------------------------------------------------------------------------
-// get_row: wave c dequantises sub-blocks 64c .. 64c+63 of the row. Its bytes start on a
-// block boundary; they are staged through LDS with 2-byte loads (any row alignment that
-// the block size allows).
+// get_rows: workgroup (c, i) dequantises sub-blocks 64c .. 64c+63 of row rows[i] into
+// out + i * out_stride, so one launch serves every token of a prefill's embedding (the
+// reference's k_embed_rows, prefill.metal:272). The row's bytes start on a block boundary;
+// they are staged through LDS with 2-byte loads (any row alignment the block size allows).
 constexpr int GR_STAGE = 64 * 32 * 4;  // bytes of 64 f32 sub-blocks, the largest chunk
-__global__ __launch_bounds__(64) void get_row_kernel(const uint8_t *__restrict__ row, int type, int n_sub,
-                                                     float *__restrict__ out) {
+__global__ __launch_bounds__(64) void get_rows_kernel(const RowsParams P) {
     __shared__ __align__(16) uint8_t stage[GR_STAGE];
-    const int lane = threadIdx.x, c = blockIdx.x;
+    const int lane = threadIdx.x, c = blockIdx.x, i = blockIdx.y;
+    const int type = P.type, n_sub = P.n_sub;
+    const uint8_t *__restrict__ row = P.w + (size_t)P.rows[i] * (size_t)P.row_bytes;
+    float *__restrict__ out = P.out + (size_t)i * (size_t)P.out_stride;
     const int sub0 = 64 * c, nsub = min(64, n_sub - sub0);
     const int be = w_block_elems(type), bb = w_block_bytes(type);
     const size_t off = (size_t)sub0 * 32 / be * bb;
     const int nbytes = nsub * 32 / be * bb;  // chunks are whole blocks (64 is a multiple of 8)
     const uint16_t *src = (const uint16_t *)(row + off);
     uint16_t *dst = (uint16_t *)stage;
-    for (int i = lane; i < nbytes / 2; i += 64) dst[i] = src[i];
+    for (int j = lane; j < nbytes / 2; j += 64) dst[j] = src[j];
     __syncthreads();
     if (lane < nsub) {
         float w[32];
@@ -341,9 +345,8 @@ __global__ __launch_bounds__(64 * MV_WAVES) void matvec_kernel(const MatvecParam
     }
 }
 
-hipError_t launch_get_row(const uint8_t *row, int type, int64_t k, float *out, hipStream_t stream) {
-    const int n_sub = (int)(k / 32);
-    hipLaunchKernelGGL(get_row_kernel, dim3((n_sub + 63) / 64), dim3(64), 0, stream, row, type, n_sub, out);
+hipError_t launch_get_rows(const RowsParams &P, hipStream_t stream) {
+    hipLaunchKernelGGL(get_rows_kernel, dim3((P.n_sub + 63) / 64, P.n), dim3(64), 0, stream, P);
     return hipGetLastError();
 }
 

@@ -83,6 +83,7 @@ _SIGS = {
     "flint_attn_engine_debug_attn": (_i32, [_vp, _i32, _f32p, _i32, _i32, _f32p, _cp, _i32]),
     "flint_w_row_bytes": (_i64, [_i32, _i64]),
     "flint_w_get_row": (_i32, [_i32, _vp, _i64, _i64, _vp, _vp, _cp, _i32]),
+    "flint_w_get_rows": (_i32, [_i32, _vp, _i64, _i64, _i32p, _i32, _vp, _vp, _cp, _i32]),
     "flint_attn_qkv_proj": (_i32, [ctypes.POINTER(WeightDesc)] * 3 + [_vp, _vp, _f32, _vp, _vp, _cp, _i32]),
     "flint_attn_o_proj": (_i32, [ctypes.POINTER(WeightDesc), _vp, _vp, _vp, _cp, _i32]),
     "flint_attn_qkv_proj_rows": (_i32, [ctypes.POINTER(WeightDesc)] * 3 + [_vp, _i32, _vp, _f32, _vp, _i32, _vp, _cp,
@@ -241,6 +242,15 @@ def get_row(wtype, w, k, row, out, stream=None):
     """Dequantise row `row` of the weight bytes `w` (a uint8 device tensor) into out [k] fp32
     (flint_w_get_row; the reference's Engine::debug_get_row)."""
     _call(lib().flint_w_get_row, W_TYPES[wtype], _ptr(w), k, row, _ptr(out), _vp(_stream(stream)))
+
+
+def get_rows(wtype, w, k, n_rows, rows, out, stream=None):
+    """Dequantise rows `rows` (a sequence of ints in [0, n_rows)) of the weight bytes `w` into
+    out [len(rows)][k] fp32 in one dispatch per 448 rows (flint_w_get_rows; the reference's
+    k_embed_rows)."""
+    arr = (ctypes.c_int32 * len(rows))(*[int(r) for r in rows])
+    _call(lib().flint_w_get_rows, W_TYPES[wtype], _ptr(w), k, n_rows, arr, len(rows), _ptr(out),
+          _vp(_stream(stream)))
 
 
 def _wdesc(w):

@@ -51,6 +51,16 @@ int32_t flint_w_get_row(int32_t type, const void *w, int64_t k, int64_t row, flo
                         char *err, int32_t err_len);
 
 /*
+ * Rows rows[0 .. n) (host array; each in [0, n_rows), the tensor's row count) of a weight
+ * tensor with rows of k elements, dequantised to fp32 into out[i * k .. (i + 1) * k) (device,
+ * 16-byte aligned), each bit-identical to flint_w_get_row of that row. The prefill's token
+ * embedding: all n prompt tokens in one dispatch per 448 rows, as k_embed_rows
+ * (/root/reference/src/metal/prefill.metal:272) at /root/reference/src/engine.mm:1067-1069.
+ */
+int32_t flint_w_get_rows(int32_t type, const void *w, int64_t k, int64_t n_rows, const int32_t *rows, int32_t n,
+                         float *out, void *stream, char *err, int32_t err_len);
+
+/*
  * The attention block's input side for one token: xn = RMSNorm(x) * attn_norm, then
  * qkv[0:4096] = Wq xn, qkv[4096:4608] = Wk xn, qkv[4608:5120] = Wv xn.
  *   x: device [2048], attn_norm: device [2048] gains, qkv: device [5120] (the raw q|k|v

@@ -262,6 +262,67 @@ void fo_prefill(const fo_layer *L, const float *qkv, int q_stride, int p0, int T
         fo_decode_step(L, qkv + (size_t)t * q_stride, p0 + t, K, V, att + (size_t)t * FO_Q_DIM, n_threads);
 }
 
+/* ---- the same prefill on many threads (the CPU baseline): every token's q/k/v first, in
+ * position order as fo_prefill writes them, then the attention of rows [r0, r1), each
+ * (row, head) pair on one of n_threads threads (interleaved). attend_heads per head is
+ * fo_prefill's own, so every row written equals fo_prefill's bit for bit. ---- */
+
+typedef struct {
+    const fo_layer *L;
+    const float *qkv;
+    float *Q, *K, *V;
+    int q_stride, p0, T, r0, r1, tid, nth;
+    float *att;
+} prefill_job;
+
+static void *prep_thread(void *p) {
+    prefill_job *j = (prefill_job *)p;
+    for (int t = j->tid; t < j->T; t += j->nth)
+        fo_qkv_prep(j->L, j->qkv + (size_t)t * j->q_stride, j->p0 + t, j->Q + (size_t)t * FO_Q_DIM,
+                    &j->K[(size_t)(j->p0 + t) * FO_KV_DIM], &j->V[(size_t)(j->p0 + t) * FO_KV_DIM]);
+    return NULL;
+}
+
+static void *prefill_thread(void *p) {
+    prefill_job *j = (prefill_job *)p;
+    const long n_pairs = (long)(j->r1 - j->r0) * FO_N_HEAD;
+    for (long i = j->tid; i < n_pairs; i += j->nth) {
+        const int row = j->r0 + (int)(i / FO_N_HEAD), hh = (int)(i % FO_N_HEAD);
+        attend_heads(j->L, j->Q + (size_t)row * FO_Q_DIM, j->K, j->V, j->p0 + row, j->att + (size_t)row * FO_Q_DIM,
+                     hh, hh + 1);
+    }
+    return NULL;
+}
+
+int fo_prefill_mt(const fo_layer *L, const float *qkv, int q_stride, int p0, int T, int r0, int r1, float *K,
+                  float *V, float *att, int n_threads) {
+    enum { MAXT = 512 };
+    if (r0 < 0 || r1 > T || r0 > r1) return -1;
+    float *Q = (float *)malloc(sizeof(float) * (size_t)T * FO_Q_DIM);
+    if (!Q) return -1;
+    if (n_threads < 1) n_threads = 1;
+    if (n_threads > MAXT) n_threads = MAXT;
+    pthread_t th[MAXT];
+    prefill_job jobs[MAXT];
+    /* two phases: every token's q/k/v (tokens interleaved over the threads; each writes its own
+     * K, V rows), then the (row, head) pairs */
+    for (int phase = 0; phase < 2; phase++) {
+        void *(*fn)(void *) = phase == 0 ? prep_thread : prefill_thread;
+        int n = 0;
+        for (int t = 0; t < n_threads; t++) {
+            jobs[t] = (prefill_job){L, qkv, Q, K, V, q_stride, p0, T, r0, r1, t, n_threads, att};
+            if (pthread_create(&th[n], NULL, fn, &jobs[t]) != 0) {
+                fn(&jobs[t]);
+                continue;
+            }
+            n++;
+        }
+        for (int t = 0; t < n; t++) pthread_join(th[t], NULL);
+    }
+    free(Q);
+    return 0;
+}
+
 /* ---- weight formats of the attention projections ----
  * Restated from ggml's published block formats and dequantisation (the reference
  * vendors them: /root/reference/third_party/ggml/ggml-common.h block_q8_0 :251-256,

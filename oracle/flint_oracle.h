@@ -101,6 +101,13 @@ void fo_decode_step(const fo_layer *L, const float *qkv, int pos, float *K, floa
 void fo_prefill(const fo_layer *L, const float *qkv, int q_stride, int p0, int T, float *K, float *V,
                 float *att, int n_threads);
 
+/* The same prefill with its attention spread over n_threads threads: every token's
+ * q/k/v (K, V rows p0 .. p0+T-1 written), then att rows [r0, r1) of the T, one (row, head)
+ * pair per job. The rows written equal fo_prefill's bit for bit (the same per-head code);
+ * the CPU baseline times it on a sample of rows. 0 / -1 (bad row range, no memory). */
+int fo_prefill_mt(const fo_layer *L, const float *qkv, int q_stride, int p0, int T, int r0, int r1, float *K,
+                  float *V, float *att, int n_threads);
+
 /* Weight formats of the attention projections: ggml type ids
  * (/root/reference/src/gguf.h:14-19). fo_row_bytes is -1 for an unsupported type or
  * a k that is not a whole number of blocks. */

@@ -72,6 +72,8 @@ def lib():
         L.fo_decode_step.argtypes = [lp, _f32p, ctypes.c_int, _f32p, _f32p, _f32p, ctypes.c_int]
         L.fo_prefill.argtypes = [lp, _f32p, ctypes.c_int, ctypes.c_int, ctypes.c_int, _f32p, _f32p, _f32p,
                                  ctypes.c_int]
+        L.fo_prefill_mt.argtypes = [lp, _f32p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                    _f32p, _f32p, _f32p, ctypes.c_int]
         for f in ("fo_block_elems", "fo_block_bytes"):
             getattr(L, f).restype = ctypes.c_long
             getattr(L, f).argtypes = [ctypes.c_int]
@@ -184,6 +186,19 @@ def prefill(layer, qkv, p0, K, V, n_threads=1):
     assert K.shape[0] >= p0 + T
     att = np.empty((T, Q_DIM), np.float32)
     lib().fo_prefill(layer.ref, _p(qkv), QKV_DIM, int(p0), int(T), _p(K), _p(V), _p(att), int(n_threads))
+    return att
+
+
+def prefill_rows(layer, qkv, p0, K, V, r0, r1, n_threads=1):
+    """The prefill of qkv [T][5120] at p0 on n_threads threads (fo_prefill_mt): K, V rows
+    p0..p0+T-1 are written, att rows [r0, r1) computed (bit-identical to prefill's rows).
+    Returns att [T][4096] with the other rows zero."""
+    qkv = np.ascontiguousarray(qkv, np.float32)
+    T = qkv.shape[0]
+    assert K.shape[0] >= p0 + T and 0 <= r0 <= r1 <= T
+    att = np.zeros((T, Q_DIM), np.float32)
+    assert lib().fo_prefill_mt(layer.ref, _p(qkv), QKV_DIM, int(p0), int(T), int(r0), int(r1), _p(K), _p(V), _p(att),
+                               int(n_threads)) == 0
     return att
 
 

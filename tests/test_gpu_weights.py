@@ -42,6 +42,28 @@ def test_get_row_bit_exact(cuda, wtype, k):
         assert np.array_equal(got.view(np.uint32), want[r].view(np.uint32)), (wtype, k, r)
 
 
+@pytest.mark.parametrize("wtype", ["q8_0", "q6_K", "iq4_xs", "f16", "bf16"])
+def test_get_rows_matches_get_row(cuda, wtype):
+    """The batched row dequantisation (the prefill's token embedding, one dispatch per 448 rows)
+    against the oracle row by row: 1000 rows drawn with repeats from a 300-row table, so the
+    table crosses two launch boundaries; every row bit-identical."""
+    import torch
+    k = 2048
+    rng = np.random.default_rng(11 + len(wtype))
+    table = oracle.random_blocks(wtype, 300, k, rng)
+    want = oracle.dequant_rows(wtype, table, k)
+    w = _dev(table, cuda)
+    rows = rng.integers(0, 300, 1000)
+    rows[:3] = [0, 299, 0]
+    out = torch.full((1000, k), float("nan"), dtype=torch.float32, device=cuda)
+    fa.get_rows(wtype, w, k, 300, rows, out)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), want[rows].view(np.uint32)), wtype
+    with pytest.raises(fa.FlintAttnError, match="out of range"):
+        fa.get_rows(wtype, w, k, 300, [5, 300], out)
+
+
 def test_get_row_golden_rows(cuda):
     """The committed reference rows (tests/golden/weight_rows.npz, 512 elements: one wave with
     16 sub-blocks), straight against the reference's float bits."""

@@ -217,3 +217,26 @@ def test_decode_step_rounds_current_kv_and_matches_prefill():
     # attending with the rounded history reproduces the step outputs
     q, _, _ = fo.qkv_prep(L, qkv[n - 1], n - 1)
     assert np.array_equal(fo.attend(L, q, K, V, n - 1), outs[-1])
+
+
+@pytest.mark.parametrize("is_swa,p0", [(0, 0), (1, 37), (1, 600)])
+def test_prefill_rows_threaded_equals_prefill(is_swa, p0):
+    """fo_prefill_mt (the CPU baseline's prefill: q/k/v of every token, then (row, head) pairs on
+    many threads) writes the same K/V history and the same att rows, bit for bit, as the
+    token-by-token fo_prefill; rows outside [r0, r1) are left zero."""
+    rng = np.random.default_rng(21 + p0)
+    qn, kn, sk = layer_weights(rng)
+    L = fo.Layer(qn, kn, sk, is_swa, 1, "bf16", 1e6)
+    T = 90
+    qkv = rng.standard_normal((T, 5120)).astype(np.float32)
+    hist = rng.standard_normal((p0, 512)).astype(np.float32)
+    K = np.zeros((p0 + T, 512), np.float32)
+    V = np.zeros((p0 + T, 512), np.float32)
+    K[:p0] = fo.round_store(hist, "bf16")
+    V[:p0] = fo.round_store(hist[::-1], "bf16")
+    K2, V2 = K.copy(), V.copy()
+    want = fo.prefill(L, qkv, p0, K, V)
+    got = fo.prefill_rows(L, qkv, p0, K2, V2, 10, 77, n_threads=7)
+    assert np.array_equal(K, K2) and np.array_equal(V, V2)
+    assert np.array_equal(got[10:77], want[10:77])
+    assert not got[:10].any() and not got[77:].any()

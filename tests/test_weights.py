@@ -130,6 +130,16 @@ def test_projection_entry_points_reject_bad_arguments():
     assert b"NULL" in e.value
     assert L.flint_w_get_row(8, ctypes.c_void_p(16), 2048, 0, ctypes.c_void_p(20), None, e, 256) == -1
     assert b"aligned" in e.value
+    rows = (ctypes.c_int32 * 3)(0, 7, 3)
+    assert L.flint_w_get_rows(8, ctypes.c_void_p(16), 2048, 7, rows, 3, ctypes.c_void_p(16), None, e, 256) == -1
+    assert b"get_rows: row 7 out of range" in e.value
+    assert L.flint_w_get_rows(8, ctypes.c_void_p(16), 2048, 8, None, 3, ctypes.c_void_p(16), None, e, 256) == -1
+    assert b"NULL" in e.value
+    assert L.flint_w_get_rows(8, ctypes.c_void_p(16), 2048, 8, rows, 0, ctypes.c_void_p(16), None, e, 256) == -1
+    assert b"n must be" in e.value
+    neg = (ctypes.c_int32 * 1)(-1)
+    assert L.flint_w_get_rows(8, ctypes.c_void_p(16), 2048, 8, neg, 1, ctypes.c_void_p(16), None, e, 256) == -1
+    assert b"negative row" in e.value
     good = fa.WeightDesc(16, fa.W_TYPES["q8_0"])
     odd = fa.WeightDesc(24, fa.W_TYPES["q8_0"])
     bad = fa.WeightDesc(16, 2)
