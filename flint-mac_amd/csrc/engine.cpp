@@ -77,7 +77,7 @@ struct Workspace {
 };
 
 struct DeviceScratch {
-    Workspace partial, kv;
+    Workspace partial, kv, gemm;
 };
 
 std::mutex g_scratch_mu;
@@ -331,6 +331,54 @@ void check_tokens(int n_tok, const char *name) {
     if (n_tok < 1 || n_tok > 1 << 20) throw Error(std::string(name) + ": n_tok must be in [1, 2^20]");
 }
 
+// A batch of T tokens through one projection on the matrix cores (proj_gemm.hip): the weight
+// rows of the segments and the activation rows as f16 hi/lo planes in the device workspace, then
+// y[t][0:N] (+)= W x[t] (x RMSNorm'd with norm_w when given).
+void proj_gemm(const MatvecSeg *seg, int n_seg, int N, int K, const float *x, long long x_stride, const float *norm_w,
+               float eps, int T, float *y, long long y_stride, int add, hipStream_t stream) {
+    const int T_pad = (T + GEMM_TILE - 1) / GEMM_TILE * GEMM_TILE;
+    const size_t wbytes = (size_t)N * K * sizeof(_Float16), xbytes = (size_t)T_pad * K * sizeof(_Float16);
+    size_t off = 0;
+    auto take = [&](size_t b) {
+        const size_t o = off;
+        off += (b + 255) / 256 * 256;
+        return o;
+    };
+    const size_t o_wh = take(wbytes), o_wl = take(wbytes), o_f = take((size_t)N * sizeof(int));
+    const size_t o_xh = take(xbytes), o_xl = take(xbytes), o_e = take((size_t)T_pad * sizeof(int));
+    char *ws = (char *)scratch().gemm.get(off);
+    GemmWeightParams W{};
+    for (int i = 0; i < n_seg; i++) W.seg[i] = seg[i];
+    W.n_seg = n_seg;
+    W.wh = (_Float16 *)(ws + o_wh);
+    W.wl = (_Float16 *)(ws + o_wl);
+    W.fexp = (int *)(ws + o_f);
+    GemmActParams X{};
+    X.x = x;
+    X.x_stride = x_stride;
+    X.norm_w = norm_w;
+    X.eps = eps;
+    X.T = T;
+    X.T_pad = T_pad;
+    X.xh = (_Float16 *)(ws + o_xh);
+    X.xl = (_Float16 *)(ws + o_xl);
+    X.eexp = (int *)(ws + o_e);
+    GemmParams G{};
+    G.wh = W.wh, G.wl = W.wl, G.fexp = W.fexp, G.xh = X.xh, G.xl = X.xl, G.eexp = X.eexp;
+    G.y = y;
+    G.y_stride = y_stride;
+    G.add = add;
+    G.N = N;
+    G.K = K;
+    G.T = T;
+    check(launch_proj_gemm(W, X, G, stream), "projection GEMM launch");
+}
+
+// the GEMM takes batches of GEMM_MIN_TOKENS and more whose output rows are 16-byte aligned
+bool use_gemm(int n_tok, const float *y, long long y_stride) {
+    return n_tok >= GEMM_MIN_TOKENS && aligned16(y) && y_stride % 4 == 0;
+}
+
 void qkv_proj_impl(const flint_weight *wq, const flint_weight *wk, const flint_weight *wv, const float *x, int n_tok,
                    const float *attn_norm, float eps, float *qkv, int qkv_stride, hipStream_t stream) {
     check_weight(wq, N_EMBD, "wq");
@@ -357,6 +405,10 @@ void qkv_proj_impl(const flint_weight *wq, const flint_weight *wk, const flint_w
     P.eps = eps;
     P.y = qkv;
     P.add = 0;
+    if (use_gemm(n_tok, qkv, qkv_stride)) {
+        proj_gemm(P.seg, 3, QKV_DIM, N_EMBD, x, N_EMBD, attn_norm, eps, n_tok, qkv, qkv_stride, 0, stream);
+        return;
+    }
     check(launch_matvec(P, N_EMBD, stream), "qkv_proj launch");
 }
 
@@ -376,6 +428,10 @@ void o_proj_impl(const flint_weight *wo, const float *att, int n_tok, float *x, 
     P.x = att;
     P.y = x;
     P.add = 1;
+    if (use_gemm(n_tok, x, N_EMBD)) {
+        proj_gemm(P.seg, 1, N_EMBD, Q_DIM, att, Q_DIM, nullptr, 0.f, n_tok, x, N_EMBD, 1, stream);
+        return;
+    }
     check(launch_matvec(P, Q_DIM, stream), "o_proj launch");
 }
 

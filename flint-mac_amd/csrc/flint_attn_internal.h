@@ -100,6 +100,35 @@ struct RowsParams {
 };
 hipError_t launch_get_rows(const RowsParams &P, hipStream_t stream);
 hipError_t launch_matvec(const MatvecParams &P, int k, hipStream_t stream);
+
+// Batched projections on the matrix cores (proj_gemm.hip): weight rows and activation rows as
+// f16 hi/lo planes scaled by per-row powers of two, then Y[t][n] (+)= 2^(e_t + f_n) sum_k ...
+struct GemmWeightParams {  // wprep: rows [0, N) of the segments -> wh, wl [N][K], fexp [N]
+    MatvecSeg seg[3];
+    int n_seg;
+    _Float16 *wh, *wl;
+    int *fexp;
+};
+struct GemmActParams {     // xprep: rows [0, T_pad) -> xh, xl [T_pad][K], eexp [T_pad]
+    const float *x;        // [T] rows of x_stride floats (16-byte aligned)
+    long long x_stride;
+    const float *norm_w;   // [K] RMSNorm gains, or null (no norm)
+    float eps;
+    int T, T_pad;          // T_pad: T rounded up to the GEMM tile (rows past T are zeros)
+    _Float16 *xh, *xl;
+    int *eexp;
+};
+struct GemmParams {
+    const _Float16 *wh, *wl, *xh, *xl;
+    const int *fexp, *eexp;
+    float *y;              // [T] rows of y_stride floats (16-byte aligned, stride a multiple of 4)
+    long long y_stride;
+    int add, N, K, T;
+};
+constexpr int GEMM_TILE = 128;       // tokens and rows per gemm3 workgroup
+constexpr int GEMM_MIN_TOKENS = 16;  // batches from this size take the GEMM
+hipError_t launch_proj_gemm(const GemmWeightParams &W, const GemmActParams &X, const GemmParams &G,
+                            hipStream_t stream);
 int matvec_row_multiple(int k);  // n_rows of a matvec launch must be a multiple of this
 
 }  // namespace flint

@@ -1,0 +1,280 @@
+// The attention projections of a prefill batch on the matrix cores (gfx950).
+//
+// Y[t][n] = sum_k W[n][k] X[t][k] for T tokens at once: the q/k/v projection of the RMSNorm'd
+// hidden rows and the o projection (added to the residual) of a layer-major prefill step
+// (/root/reference/src/engine.mm:1083-1086, 1105-1111). The reference's CPU path sums in double
+// (ref_model.cpp:74-93); the one-token kernels here sum fp32 FMAs. The batch reaches the same
+// fp32-level accuracy on v_mfma_f32_32x32x16_f16 by splitting both operands into f16 hi/lo
+// pairs:
+//   * every weight row (dequantised as in proj.hip) and every activation row is scaled by a
+//     power of two that puts its largest magnitude in [2^14, 2^15), then split as
+//     v = hi + lo with hi = f16(v), lo = f16(v - hi): 22 significant bits, and no value
+//     overflows f16 whatever the row's range;
+//   * the GEMM accumulates hi*hi + hi*lo + lo*hi in fp32 (the lo*lo term is below 2^-22 of
+//     the product) and scales each output by 2^(e_t + f_n), which is exact.
+// Three launches: wprep (weights -> planes), xprep (activations -> planes, the RMSNorm fused
+// for q/k/v) and gemm3. The weight planes are rebuilt each call from the GGUF rows (~25 us for
+// a layer's 19M weights), so nothing is cached across calls.
+#include "common.h"
+#include "dequant.h"
+#include "flint_attn_internal.h"
+
+namespace flint {
+
+namespace {
+
+// exponent that puts a row's largest magnitude mx in [2^14, 2^15): x * 2^-e fits f16 with its
+// full 11 bits at the top of the row (0 for an all-zero row, inf / nan left as they are)
+__device__ inline int row_exp(float mx) {
+    if (!(mx > 0.f) || !__builtin_isfinite(mx)) return 0;
+    return __builtin_amdgcn_frexp_expf(mx) - 15;  // mx in [2^(f-1), 2^f)
+}
+
+__device__ inline void split_store(float v, int e, _Float16 *hi, _Float16 *lo) {
+    const float s = __builtin_amdgcn_ldexpf(v, -e);
+    const _Float16 h = (_Float16)s;
+    *hi = h;
+    *lo = (_Float16)(s - (float)h);
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// wprep: one wave per weight row: the row's bytes staged through LDS (2-byte copies: q8_0 and
+// q6_K blocks are only 2-byte aligned), dequantised 32 elements per lane per sub-block (lane l
+// owns sub-blocks l, l + 64, ...), the row's exponent from its largest magnitude, then the
+// hi/lo planes ([n][K] f16, row-major) and f_n.
+constexpr int WP_MAX_K = 4096;
+constexpr int WP_STAGE = WP_MAX_K / 32 * 34;  // largest quantised row of the batch (q8_0)
+template <int K>
+__global__ __launch_bounds__(64) void wprep_kernel(const GemmWeightParams P) {
+    constexpr int SUBS = K / 32 / 64;
+    __shared__ __align__(16) uint8_t stage[WP_STAGE > K * 4 ? WP_STAGE : K * 4];
+    const int lane = threadIdx.x, n = blockIdx.x;  // plane row
+    const int in2 = P.n_seg > 2 && n >= P.seg[2].row0, in1 = !in2 && P.n_seg > 1 && n >= P.seg[1].row0;
+    const MatvecSeg S = in2 ? P.seg[2] : in1 ? P.seg[1] : P.seg[0];
+    const uint8_t *row = S.w + (size_t)(n - S.row0) * S.row_bytes;
+    const uint16_t *src = (const uint16_t *)row;
+    uint16_t *dst = (uint16_t *)stage;
+    for (int i = lane; i < S.row_bytes / 2; i += 64) dst[i] = src[i];
+    __syncthreads();
+    float w[SUBS][32];
+    float mx = 0.f;
+#pragma unroll
+    for (int i = 0; i < SUBS; i++) {
+        deq32(S.type, stage, lane + 64 * i, w[i]);
+#pragma unroll
+        for (int e = 0; e < 32; e++) mx = fmaxf(mx, fabsf(w[i][e]));
+    }
+    const int f = row_exp(wave_max(mx));
+    _Float16 *hi = P.wh + (size_t)n * K, *lo = P.wl + (size_t)n * K;
+#pragma unroll
+    for (int i = 0; i < SUBS; i++) {
+        const int k0 = 32 * (lane + 64 * i);
+        f16x8 h8[4], l8[4];
+#pragma unroll
+        for (int e = 0; e < 32; e++) {
+            _Float16 h, l;
+            split_store(w[i][e], f, &h, &l);
+            h8[e >> 3][e & 7] = h;
+            l8[e >> 3][e & 7] = l;
+        }
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            *(f16x8 *)(hi + k0 + 8 * q) = h8[q];
+            *(f16x8 *)(lo + k0 + 8 * q) = l8[q];
+        }
+    }
+    if (lane == 0) P.fexp[n] = f;
+}
+
+// ---------------------------------------------------------------------------
+// xprep: one 256-thread workgroup per activation row t (rows T .. T_pad - 1 are written as
+// zeros): the RMSNorm exactly as matvec_kernel computes it when gains are given (double sum
+// of squares per thread over XPT consecutive elements, then across lanes and waves in a fixed
+// order; xn = (x * scale) * g), the row's exponent, then the hi/lo planes ([t][K] f16).
+template <int K>
+__global__ __launch_bounds__(256) void xprep_kernel(const GemmActParams P) {
+    constexpr int XPT = K / 256;
+    __shared__ double part[4];
+    __shared__ float red[4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, t = blockIdx.x;
+    float xv[XPT];
+    if (t < P.T) {
+        const float *xt = P.x + (size_t)t * P.x_stride + XPT * tid;
+#pragma unroll
+        for (int k = 0; k < XPT / 4; k++) {
+            const f32x4 v = *(const f32x4 *)(xt + 4 * k);
+            xv[4 * k] = v[0], xv[4 * k + 1] = v[1], xv[4 * k + 2] = v[2], xv[4 * k + 3] = v[3];
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < XPT; k++) xv[k] = 0.f;
+    }
+    if (P.norm_w) {
+        double ss = 0;
+#pragma unroll
+        for (int k = 0; k < XPT; k++) ss += (double)xv[k] * xv[k];
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
+        if (lane == 0) part[wave] = ss;
+        __syncthreads();
+        ss = 0;
+#pragma unroll
+        for (int w = 0; w < 4; w++) ss += part[w];
+        const float scale = 1.0f / sqrtf((float)(ss / K) + P.eps);
+#pragma unroll
+        for (int k = 0; k < XPT; k++) xv[k] = xv[k] * scale * P.norm_w[XPT * tid + k];
+    }
+    float mx = 0.f;
+#pragma unroll
+    for (int k = 0; k < XPT; k++) mx = fmaxf(mx, fabsf(xv[k]));
+    mx = wave_max(mx);
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    const int e = row_exp(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
+    _Float16 *hi = P.xh + (size_t)t * K + XPT * tid, *lo = P.xl + (size_t)t * K + XPT * tid;
+#pragma unroll
+    for (int k = 0; k < XPT / 8; k++) {
+        f16x8 h8, l8;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            _Float16 h, l;
+            split_store(xv[8 * k + j], e, &h, &l);
+            h8[j] = h;
+            l8[j] = l;
+        }
+        *(f16x8 *)(hi + 8 * k) = h8;
+        *(f16x8 *)(lo + 8 * k) = l8;
+    }
+    if (tid == 0) P.eexp[t] = e;
+}
+
+// ---------------------------------------------------------------------------
+// gemm3: workgroup tile 128 weight rows (n) x 128 tokens (t), 4 waves in a 2 x 2 grid of
+// 64 x 64, each four 32 x 32 MFMA blocks. K runs in chunks of 32 (two MFMA k-steps of 16). A
+// chunk of each operand (hi and lo planes, 128 rows x 32 k) goes into LDS in the MFMA operand
+// order: per plane, 32-row block and k-step, 1 KiB in which lane l's 16 bytes hold row l & 31,
+// k 8 (l >> 5) .. +7 (the same order for the weight rows, operand A, and for the tokens,
+// operand B), so every fragment read is one conflict-free ds_read_b128 per lane. Two chunks in
+// flight: the next chunk's global loads are issued before this chunk's MFMAs.
+constexpr int GM_TILE = GEMM_TILE, GM_KC = 32, GM_THREADS = 256;
+constexpr int GM_PLANE_CHUNK = GM_TILE * GM_KC * 2;  // bytes of one plane's chunk (8 KiB)
+
+__global__ __launch_bounds__(GM_THREADS, 2) void gemm3_kernel(const GemmParams P) {
+    // [buffer][operand (A = weights, B = tokens)][plane (hi, lo)]: 8 KiB each
+    __shared__ __align__(16) uint8_t lds[2][2][2][GM_PLANE_CHUNK];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wn = wave & 1, wt = wave >> 1;
+    const int n0 = blockIdx.x * GM_TILE, t0 = blockIdx.y * GM_TILE;
+    const int K = P.K;
+    // global -> LDS: per plane, 512 units of 16 bytes (128 rows x 4 k8); thread tid takes units
+    // tid and tid + 256 (row u >> 2, k8 = u & 3: four threads read a row's 64 contiguous bytes)
+    const _Float16 *srcA[2] = {P.wh + (size_t)n0 * K, P.wl + (size_t)n0 * K};
+    const _Float16 *srcB[2] = {P.xh + (size_t)t0 * K, P.xl + (size_t)t0 * K};
+    int goff[2], loff[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int u = tid + GM_THREADS * i, r = u >> 2, k8 = u & 3;
+        goff[i] = r * K + 8 * k8;
+        // LDS: block r >> 5, k-step k8 >> 1, lane slot (r & 31) + 32 (k8 & 1)
+        loff[i] = (((r >> 5) * 2 + (k8 >> 1)) * 64 + (r & 31) + 32 * (k8 & 1)) * 16;
+    }
+    u32x4 g[2][2][2];  // [operand][plane][unit]
+    auto gload = [&](int kc) {
+#pragma unroll
+        for (int p = 0; p < 2; p++)
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                g[0][p][i] = *(const u32x4 *)(srcA[p] + goff[i] + kc);
+                g[1][p][i] = *(const u32x4 *)(srcB[p] + goff[i] + kc);
+            }
+    };
+    auto lstore = [&](int buf) {
+#pragma unroll
+        for (int o = 0; o < 2; o++)
+#pragma unroll
+            for (int p = 0; p < 2; p++)
+#pragma unroll
+                for (int i = 0; i < 2; i++) *(u32x4 *)(lds[buf][o][p] + loff[i]) = g[o][p][i];
+    };
+    f32x16 acc[2][2];
+#pragma unroll
+    for (int a = 0; a < 2; a++)
+#pragma unroll
+        for (int b = 0; b < 2; b++) acc[a][b] = f32x16{};
+    const int n_chunks = K / GM_KC;
+    gload(0);
+    lstore(0);
+    if (n_chunks > 1) gload(GM_KC);
+    __syncthreads();
+    for (int c = 0; c < n_chunks; c++) {
+        const int buf = c & 1;
+        // chunk c + 1 (in registers since the previous iteration) into the other buffer, whose
+        // chunk every wave finished before the last barrier, then chunk c + 2 into registers
+        if (c + 1 < n_chunks) {
+            lstore(buf ^ 1);
+            if (c + 2 < n_chunks) gload((c + 2) * GM_KC);
+        }
+#pragma unroll
+        for (int s = 0; s < 2; s++) {  // k-steps of 16
+            f16x8 ah[2], al[2], bh[2], bl[2];
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const int ob = ((2 * wn + j) * 2 + s) * 1024 + lane * 16;  // A block 2wn + j
+                const int tb = ((2 * wt + j) * 2 + s) * 1024 + lane * 16;  // B block 2wt + j
+                ah[j] = *(const f16x8 *)(lds[buf][0][0] + ob);
+                al[j] = *(const f16x8 *)(lds[buf][0][1] + ob);
+                bh[j] = *(const f16x8 *)(lds[buf][1][0] + tb);
+                bl[j] = *(const f16x8 *)(lds[buf][1][1] + tb);
+            }
+#pragma unroll
+            for (int a = 0; a < 2; a++)
+#pragma unroll
+                for (int b = 0; b < 2; b++) {
+                    acc[a][b] = mfma32_f16(ah[a], bh[b], acc[a][b]);
+                    acc[a][b] = mfma32_f16(ah[a], bl[b], acc[a][b]);
+                    acc[a][b] = mfma32_f16(al[a], bh[b], acc[a][b]);
+                }
+        }
+        __syncthreads();
+    }
+    // epilogue: block (a, b) element e is weight row n0 + 64 wn + 32 a + 8 (e >> 2) + 4 (lane >> 5) + (e & 3)
+    // and token t0 + 64 wt + 32 b + (lane & 31)
+#pragma unroll
+    for (int b = 0; b < 2; b++) {
+        const int t = t0 + 64 * wt + 32 * b + (lane & 31);
+        if (t >= P.T) continue;
+        const int et = P.eexp[t];
+        float *yt = P.y + (size_t)t * P.y_stride;
+#pragma unroll
+        for (int a = 0; a < 2; a++)
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const int n = n0 + 64 * wn + 32 * a + 8 * q + 4 * (lane >> 5);
+                const int4 f = *(const int4 *)(P.fexp + n);
+                f32x4 v = {__builtin_amdgcn_ldexpf(acc[a][b][4 * q], et + f.x),
+                           __builtin_amdgcn_ldexpf(acc[a][b][4 * q + 1], et + f.y),
+                           __builtin_amdgcn_ldexpf(acc[a][b][4 * q + 2], et + f.z),
+                           __builtin_amdgcn_ldexpf(acc[a][b][4 * q + 3], et + f.w)};
+                f32x4 *dst = (f32x4 *)(yt + n);
+                if (P.add) v += *dst;
+                *dst = v;
+            }
+    }
+}
+
+hipError_t launch_proj_gemm(const GemmWeightParams &W, const GemmActParams &X, const GemmParams &G,
+                            hipStream_t stream) {
+    if (G.K == 2048) {
+        hipLaunchKernelGGL(wprep_kernel<2048>, dim3(G.N), dim3(64), 0, stream, W);
+        hipLaunchKernelGGL(xprep_kernel<2048>, dim3(X.T_pad), dim3(256), 0, stream, X);
+    } else {
+        hipLaunchKernelGGL(wprep_kernel<4096>, dim3(G.N), dim3(64), 0, stream, W);
+        hipLaunchKernelGGL(xprep_kernel<4096>, dim3(X.T_pad), dim3(256), 0, stream, X);
+    }
+    hipLaunchKernelGGL(gemm3_kernel, dim3(G.N / GM_TILE, X.T_pad / GM_TILE), dim3(GM_THREADS), 0, stream, G);
+    return hipGetLastError();
+}
+
+}  // namespace flint

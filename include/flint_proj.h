@@ -85,10 +85,15 @@ int32_t flint_attn_o_proj(const flint_weight *wo, const float *att, float *x, vo
                           int32_t err_len);
 
 /*
- * The same two projections for n_tok tokens in one launch each (the prefill side):
+ * The same two projections for n_tok tokens (the prefill side):
  * x: device [n_tok][2048]; qkv: device [n_tok] rows of qkv_stride floats (>= 5120), the raw
- * q|k|v at each row's start; att: device [n_tok][4096]. Each token's result equals the
- * single-token call's.
+ * q|k|v at each row's start; att: device [n_tok][4096].
+ * Below 16 tokens (or when the output rows are not 16-byte aligned) each token runs the
+ * single-token kernel and gets exactly its bits. From 16 tokens the batch runs as a GEMM on
+ * the matrix cores: weight and activation rows split into f16 hi/lo pairs (22 bits, each row
+ * scaled by a power of two), products summed in fp32; every output is within fp32 reassociation
+ * of the single-token result (both within the oracle's bound). It uses a device workspace of
+ * 4 (rows + 128-token-padded n_tok) x K bytes, allocated on first use and reused.
  * Replace the prefill's k_rmsnorm_rows + three mm (q, k, v), and mm(o) + k_add_rows, at
  * /root/reference/src/engine.mm:1083-1086 and 1105-1111.
  */

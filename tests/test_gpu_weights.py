@@ -5,7 +5,8 @@
     which allows 1e-5);
   * the q/k/v projection with the attention RMSNorm, and o_proj with the residual add, within
     fp32 reassociation of the oracle's double-accumulated matvec (ref_model.cpp:74-93, 107-110,
-    150-151).
+    150-151): one token, small batches (bit-identical to one token), and batches on the GEMM
+    (proj_gemm.hip, f16 hi/lo planes) in every format and over rows of any range.
 """
 import numpy as np
 import pytest
@@ -164,12 +165,13 @@ def test_projection_block_round_trip(cuda):
         assert np.all(np.abs(got - x_ref) <= scale), (p, float(np.abs(got - x_ref).max()))
 
 
-def test_projection_rows_equal_single_token_calls(cuda):
-    """The batched projections (flint_attn_qkv_proj_rows / flint_attn_o_proj_rows) give each
-    token exactly the single-token call's bits, also into a strided qkv row (q_stride 5248)."""
+def test_projection_rows_small_batch_equal_single_token_calls(cuda):
+    """Batches below the GEMM's size (flint_attn_qkv_proj_rows / flint_attn_o_proj_rows with
+    n_tok < 16) run the one-token kernel per token: each token gets exactly the single-token
+    call's bits, also into a strided qkv row (q_stride 5248)."""
     import torch
     rng = np.random.default_rng(41)
-    T = 37
+    T = 9
     wq = (_dev(oracle.random_blocks("q5_K", 4096, 2048, rng), cuda), "q5_K")
     wk = (_dev(oracle.random_blocks("iq4_xs", 512, 2048, rng), cuda), "iq4_xs")
     wv = (_dev(oracle.random_blocks("q8_0", 512, 2048, rng), cuda), "q8_0")
@@ -190,3 +192,66 @@ def test_projection_rows_equal_single_token_calls(cuda):
     assert torch.equal(qkv_rows[:, :5120], qkv_one)
     assert torch.isnan(qkv_rows[:, 5120:]).all()  # the row padding is left alone
     assert torch.equal(y_rows, y_one)
+
+
+def _gemm_case(cuda, rng, types, wo_type, T, x_scale=None, att_scale=None):
+    """qkv_proj_rows and o_proj_rows on T tokens (the GEMM path) against the oracle's matvec of
+    every token, within _rows_bound. x_scale / att_scale: per-row factors for the inputs."""
+    import torch
+    E = fa.N_EMBD
+    x = (rng.standard_normal((T, E)) * 2).astype(np.float32)
+    if x_scale is not None:
+        x *= x_scale[:, None].astype(np.float32)
+    g = rng.uniform(0.5, 1.5, E).astype(np.float32)
+    ws, dense = [], []
+    for t, n in zip(types, (4096, 512, 512)):
+        rows = oracle.random_blocks(t, n, E, rng)
+        ws.append((_dev(rows, cuda), t))
+        dense.append(oracle.dequant_rows(t, rows, E))
+    dense = np.concatenate(dense)
+    wo_rows = oracle.random_blocks(wo_type, E, 4096, rng)
+    wo_dense = oracle.dequant_rows(wo_type, wo_rows, 4096)
+    att = rng.standard_normal((T, 4096)).astype(np.float32)
+    if att_scale is not None:
+        att *= att_scale[:, None].astype(np.float32)
+    x0 = rng.standard_normal((T, E)).astype(np.float32)
+    qkv = torch.full((T, 5248), float("nan"), device=cuda)
+    fa.qkv_proj_rows(ws[0], ws[1], ws[2], _dev(x, cuda), _dev(g, cuda), qkv)
+    y = _dev(x0, cuda)
+    fa.o_proj_rows((_dev(wo_rows, cuda), wo_type), _dev(att, cuda), y)
+    torch.cuda.synchronize()
+    got_qkv = qkv.cpu().numpy()[:, :5120].astype(np.float64)
+    got_y = y.cpu().numpy().astype(np.float64)
+    assert torch.isnan(qkv[:, 5120:]).all()
+    for t in range(T):
+        xn = np.empty(E, np.float32)
+        oracle.lib().fo_rmsnorm(oracle._p(np.ascontiguousarray(x[t])), oracle._p(g), oracle._p(xn), E, 1e-6)
+        want = oracle.matvec_f32(dense, xn)
+        bound = _rows_bound(dense, xn)
+        err = np.abs(got_qkv[t] - want)
+        assert np.all(err <= bound), ("qkv", types, t, float((err / bound).max()))
+        want_y = x0[t] + oracle.matvec_f32(wo_dense, att[t])
+        bound_y = _rows_bound(wo_dense, att[t]) + 1e-7 * np.abs(x0[t])
+        err = np.abs(got_y[t] - want_y)
+        assert np.all(err <= bound_y), ("o", wo_type, t, float((err / bound_y).max()))
+
+
+@pytest.mark.parametrize("types,wo_type", [(("q8_0",) * 3, "q8_0"), (("q5_K", "q6_K", "iq4_xs"), "q6_K"),
+                                           (("bf16", "f16", "f32"), "iq4_xs"), (("q6_K",) * 3, "q5_K"),
+                                           (("iq4_xs",) * 3, "bf16")])
+def test_projection_rows_gemm_matches_oracle(cuda, types, wo_type):
+    """Batches from 16 tokens (the GEMM on f16 hi/lo planes): every output within the fp32
+    reassociation bound of the oracle's double-accumulated matvec, at 131 tokens (a partial
+    128-token tile) in the engine's formats, the residual added in the o projection."""
+    _gemm_case(cuda, np.random.default_rng(51 + len(wo_type)), types, wo_type, 131)
+
+
+def test_projection_rows_gemm_row_ranges(cuda):
+    """The GEMM's per-row power-of-two scaling: hidden rows at 1e4 .. 1e-6 (the RMSNorm makes
+    them alike) and attention rows at 1e6 .. 1e-7 (beyond f16's range both ways), each within
+    the bound of the oracle; 16 tokens, the smallest GEMM batch."""
+    rng = np.random.default_rng(57)
+    T = 16
+    scales = 10.0 ** np.linspace(4, -6, T)
+    att_scales = 10.0 ** np.linspace(6, -7, T)
+    _gemm_case(cuda, rng, ("q8_0", "q6_K", "f16"), "q8_0", T, x_scale=scales, att_scale=att_scales)
