@@ -275,10 +275,10 @@ def bench_model(torch, fa, reps=48, ctx=32768, T_prefill=4000):
     byte whatever the values.
       * one full layer at `ctx` cached positions and one SWA layer, each block and its attention
         stage alone timed like the decode line (the projections are the difference);
-      * a whole decode step at ctx: the embedding row, then the 49 blocks at position ctx
-        (what flint_attn_model_step runs at that position);
       * flint_attn_model_prefill of T_prefill tokens from position 0 (embedding, then layer-major
-        blocks)."""
+        blocks), and of the whole ctx-token prompt;
+      * then flint_attn_model_step (Engine::step over the blocks) at position ctx: 8 tokens per
+        rep, rolled back to ctx between reps."""
     import ctypes
     import tempfile
     import numpy as np
@@ -311,7 +311,7 @@ def bench_model(torch, fa, reps=48, ctx=32768, T_prefill=4000):
         path = os.path.join(tmp, "flint49.gguf")
         gw.write_gguf(path, gw.flint_meta(is_swa, is_swa, 513, 1.0e4), tensors)
         del tensors
-        model = fa.Model(path, n_ctx=ctx + 32)
+        model = fa.Model(path, n_ctx=ctx + 64)
     x = torch.randn(E, device=dev) * 0.1
     qkv = torch.randn(5120, device=dev)
     att = torch.empty(4096, device=dev)
@@ -325,34 +325,47 @@ def bench_model(torch, fa, reps=48, ctx=32768, T_prefill=4000):
                                     0, ctypes.c_void_p(fa._stream(None))), reps)[0]
         out[name] = dict(block_ms=t_block, attn_ms=t_attn, proj_ms=t_block - t_attn)
     t_proj = 0.5 * (out["full"]["proj_ms"] + out["swa"]["proj_ms"])
-
-    def step():
-        model.embed([17], x)
-        for il in range(len(FLINT_FULL_LAYERS)):
-            model.block_decode(il, x, ctx, att)
-
-    t_step, step_host_bound = queued_launch_ms(torch, step, 8)
-    # layer-major prefill of T_prefill tokens from position 0
-    tokens = [int(t) for t in rng.integers(0, n_vocab, T_prefill)]
-    X = torch.empty((T_prefill, E), device=dev)
-    model.truncate(0)
-    model.prefill(tokens, X)  # warm-up (workspace growth)
-    torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    n_rep = 2
-    e0.record()
-    for _ in range(n_rep):
+
+    def timed(fn, reps):
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    # layer-major prefill (flint_attn_model_prefill: embedding, then every layer's block over the
+    # whole prompt) of T_prefill tokens from position 0
+    tokens = [int(t) for t in rng.integers(0, n_vocab, ctx)]
+    X = torch.empty((ctx, E), device=dev)
+
+    def prefill_from_0(n):
         model.truncate(0)
-        model.prefill(tokens, X)
-    e1.record()
-    torch.cuda.synchronize()
-    t_prefill = e0.elapsed_time(e1) / n_rep
+        model.prefill(tokens[:n], X[:n])
+
+    prefill_from_0(T_prefill)  # warm-up (workspace growth)
+    t_prefill = timed(lambda: prefill_from_0(T_prefill), 2)
+    # the whole 32k prompt, then Engine::step at position ctx (flint_attn_model_step: the token's
+    # embedding and the 49 blocks, one C call per token); each rep steps 8 tokens from ctx
+    t_prefill_ctx = timed(lambda: prefill_from_0(ctx), 1)
+    xs = torch.empty((8, E), device=dev)
+
+    def eight_steps():
+        model.truncate(ctx)
+        for i in range(8):
+            model.step(17 + i, xs[i])
+
+    eight_steps()
+    t_step = timed(eight_steps, 3) / 8
     model.close()
     return dict(full_32k_block_ms=out["full"]["block_ms"], swa_block_ms=out["swa"]["block_ms"],
                 full_32k_attn_ms=out["full"]["attn_ms"], swa_attn_ms=out["swa"]["attn_ms"],
                 proj_ms=t_proj, proj_weight_bytes=wbytes, proj_gbs=wbytes / (t_proj * 1e-3) / 1e9,
-                step_49_layers_32k_ms=t_step, step_tok_s_32k=1.0 / (t_step * 1e-3), step_host_bound=step_host_bound,
-                prefill_4000_ms=t_prefill, prefill_4000_tok_s=T_prefill / (t_prefill * 1e-3))
+                step_32k_ms=t_step, step_tok_s_32k=1.0 / (t_step * 1e-3),
+                prefill_4000_ms=t_prefill, prefill_4000_tok_s=T_prefill / (t_prefill * 1e-3),
+                prefill_32k_ms=t_prefill_ctx, prefill_32k_tok_s=ctx / (t_prefill_ctx * 1e-3))
 
 
 def cpu_baseline(decode_s=10.0, prefill_s=6.0):

@@ -156,8 +156,8 @@ __global__ __launch_bounds__(256) void xprep_kernel(const GemmActParams P) {
 // chunk of each operand (hi and lo planes, 128 rows x 32 k) goes into LDS in the MFMA operand
 // order: per plane, 32-row block and k-step, 1 KiB in which lane l's 16 bytes hold row l & 31,
 // k 8 (l >> 5) .. +7 (the same order for the weight rows, operand A, and for the tokens,
-// operand B), so every fragment read is one conflict-free ds_read_b128 per lane. Two chunks in
-// flight: the next chunk's global loads are issued before this chunk's MFMAs.
+// operand B), so every fragment read is one conflict-free ds_read_b128 per lane. While a chunk
+// is computed from LDS, the next one is stored there and the two after it are in flight.
 constexpr int GM_TILE = GEMM_TILE, GM_KC = 32, GM_THREADS = 256;
 constexpr int GM_PLANE_CHUNK = GM_TILE * GM_KC * 2;  // bytes of one plane's chunk (8 KiB)
 
@@ -166,7 +166,21 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemm3_kernel(const GemmParams P
     __shared__ __align__(16) uint8_t lds[2][2][2][GM_PLANE_CHUNK];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wn = wave & 1, wt = wave >> 1;
-    const int n0 = blockIdx.x * GM_TILE, t0 = blockIdx.y * GM_TILE;
+    // Tile of this workgroup. The hardware deals workgroups to the 8 XCDs in id order (id % 8),
+    // each XCD with its own L2: XCD x takes the stripe of weight-row tiles [x w, x w + w) and
+    // walks it token-tile-major, so the workgroups resident on one XCD share their weight and
+    // token chunks in that L2 (a row-major deal spreads them over the whole output grid).
+    const int NT = P.N / GM_TILE, id = blockIdx.x;
+    int nt, tt;
+    if (NT % 8 == 0) {
+        const int w = NT / 8, j = id >> 3;
+        nt = (id & 7) * w + j % w;
+        tt = j / w;
+    } else {
+        nt = id % NT;
+        tt = id / NT;
+    }
+    const int n0 = nt * GM_TILE, t0 = tt * GM_TILE;
     const int K = P.K;
     // global -> LDS: per plane, 512 units of 16 bytes (128 rows x 4 k8); thread tid takes units
     // tid and tid + 256 (row u >> 2, k8 = u & 3: four threads read a row's 64 contiguous bytes)
@@ -180,8 +194,9 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemm3_kernel(const GemmParams P
         // LDS: block r >> 5, k-step k8 >> 1, lane slot (r & 31) + 32 (k8 & 1)
         loff[i] = (((r >> 5) * 2 + (k8 >> 1)) * 64 + (r & 31) + 32 * (k8 & 1)) * 16;
     }
-    u32x4 g[2][2][2];  // [operand][plane][unit]
-    auto gload = [&](int kc) {
+    // two register sets of loaded chunks, so two chunks are in flight while one is computed
+    u32x4 ga[2][2][2], gb[2][2][2];  // [operand][plane][unit]
+    auto gload = [&](u32x4 (&g)[2][2][2], int kc) {
 #pragma unroll
         for (int p = 0; p < 2; p++)
 #pragma unroll
@@ -190,7 +205,7 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemm3_kernel(const GemmParams P
                 g[1][p][i] = *(const u32x4 *)(srcB[p] + goff[i] + kc);
             }
     };
-    auto lstore = [&](int buf) {
+    auto lstore = [&](const u32x4 (&g)[2][2][2], int buf) {
 #pragma unroll
         for (int o = 0; o < 2; o++)
 #pragma unroll
@@ -203,19 +218,7 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemm3_kernel(const GemmParams P
     for (int a = 0; a < 2; a++)
 #pragma unroll
         for (int b = 0; b < 2; b++) acc[a][b] = f32x16{};
-    const int n_chunks = K / GM_KC;
-    gload(0);
-    lstore(0);
-    if (n_chunks > 1) gload(GM_KC);
-    __syncthreads();
-    for (int c = 0; c < n_chunks; c++) {
-        const int buf = c & 1;
-        // chunk c + 1 (in registers since the previous iteration) into the other buffer, whose
-        // chunk every wave finished before the last barrier, then chunk c + 2 into registers
-        if (c + 1 < n_chunks) {
-            lstore(buf ^ 1);
-            if (c + 2 < n_chunks) gload((c + 2) * GM_KC);
-        }
+    auto compute = [&](int buf) {
 #pragma unroll
         for (int s = 0; s < 2; s++) {  // k-steps of 16
             f16x8 ah[2], al[2], bh[2], bl[2];
@@ -237,7 +240,31 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemm3_kernel(const GemmParams P
                     acc[a][b] = mfma32_f16(al[a], bh[b], acc[a][b]);
                 }
         }
-        __syncthreads();
+    };
+    // chunk c lives in LDS buffer c & 1; chunks c + 1 and c + 2 are in registers (set gb holds
+    // the odd chunks, ga the even ones) while chunk c is computed. K is a multiple of 64, so
+    // the chunk count is even. The barriers order LDS only (lds_barrier): a full __syncthreads
+    // would also wait for the chunk loads in flight.
+    const int n_chunks = K / GM_KC;
+    gload(ga, 0);
+    gload(gb, GM_KC);
+    lstore(ga, 0);
+    gload(ga, 2 * GM_KC);
+    lds_barrier();
+    // Loads and stores are unconditional (past the last chunk they re-read it and store it into
+    // a buffer no one reads again), so the compiler's wait counts are static: a store waits for
+    // its own register set only, with the other set's loads still in flight.
+    const int last = (n_chunks - 1) * GM_KC;
+    for (int c = 0; c < n_chunks; c += 2) {
+        // chunk c + 1 into buffer 1 (its chunk c - 1 was finished before the last barrier)
+        lstore(gb, 1);
+        gload(gb, min((c + 3) * GM_KC, last));
+        compute(0);
+        lds_barrier();
+        lstore(ga, 0);
+        gload(ga, min((c + 4) * GM_KC, last));
+        compute(1);
+        lds_barrier();
     }
     // epilogue: block (a, b) element e is weight row n0 + 64 wn + 32 a + 8 (e >> 2) + 4 (lane >> 5) + (e & 3)
     // and token t0 + 64 wt + 32 b + (lane & 31)
@@ -273,7 +300,7 @@ hipError_t launch_proj_gemm(const GemmWeightParams &W, const GemmActParams &X, c
         hipLaunchKernelGGL(wprep_kernel<4096>, dim3(G.N), dim3(64), 0, stream, W);
         hipLaunchKernelGGL(xprep_kernel<4096>, dim3(X.T_pad), dim3(256), 0, stream, X);
     }
-    hipLaunchKernelGGL(gemm3_kernel, dim3(G.N / GM_TILE, X.T_pad / GM_TILE), dim3(GM_THREADS), 0, stream, G);
+    hipLaunchKernelGGL(gemm3_kernel, dim3(G.N / GM_TILE * (X.T_pad / GM_TILE)), dim3(GM_THREADS), 0, stream, G);
     return hipGetLastError();
 }
 
