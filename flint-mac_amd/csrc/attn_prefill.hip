@@ -397,15 +397,27 @@ __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const Pref
     pin_sgpr(scaled_call);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int col = lane & 31, hh = lane >> 5;
+    // workgroup = (query block, key split, kv head), kv head fastest, then split; longest (causal)
+    // query blocks first
+    const int n_split = P.n_split;
     const int kvh = blockIdx.x & 3, hq = kvh * GQA + wave;
-    const int qb = n_qblocks - 1 - (int)(blockIdx.x >> 2);  // longest (causal) blocks first
+    const int rest = (int)(blockIdx.x >> 2), split = rest % n_split;
+    const int qb = n_qblocks - 1 - rest / n_split;
     const int t0 = qb * PF_BQ;
     const int q_first = P.p0 + t0, q_last = P.p0 + min(t0 + PF_BQ, P.T) - 1;
     const int my_t = t0 + col, my_qp = P.p0 + my_t;
     const bool row_ok = my_t < P.T;
 
     const int k_lo = P.is_swa ? max(P.kbase, q_first - (P.window - 1)) : 0;
-    const int t_lo = (k_lo - P.kbase) >> 5, t_hi = (q_last - P.kbase) >> 5;  // 32-key tiles
+    // 32-key tiles of this block, then of this split (P.tps tiles each)
+    const int tb_lo = (k_lo - P.kbase) >> 5, tb_hi = (q_last - P.kbase) >> 5;
+    const int t_lo = tb_lo + split * P.tps, t_hi = min(tb_hi, t_lo + P.tps - 1);
+    // the record of row t, head hq of this split (acc[128], m in log2 units, l)
+    auto part_row = [&](int t) { return P.part + ((size_t)(split * P.T + t) * N_HEAD + hq) * PF_PART_STRIDE; };
+    if (t_lo > t_hi) {  // wave-uniform: a split past this block's keys (shorter blocks of a causal layer)
+        if (hh == 0 && row_ok) *(float2 *)(part_row(my_t) + HEAD_DIM) = make_float2(P.sinks[hq] * LOG2E, 0.f);
+        return;
+    }
     const _Float16 *__restrict__ skv = P.sk + (size_t)kvh * (P.k_rows >> 5) * (16 * 64 * 8);
 
     // ---- Q fragments (B operand of S^T = K Q^T): lane (col, hh) needs query row `col`,
@@ -488,7 +500,9 @@ __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const Pref
         for (int st = 0; st < 8; st++) qf[st] = q_lds[wave][st][lane];
     }
 
-    float m = P.sinks[hq] * LOG2E, l = hh == 0 ? 1.f : 0.f;
+    // m starts at the sink; l counts the sink once (l = 1) unless the keys are split, in which
+    // case the merge adds it
+    float m = P.sinks[hq] * LOG2E, l = hh == 0 && n_split == 1 ? 1.f : 0.f;
     f32x16 negm;  // -m in every element: the C operand of each tile's first score MFMA
 #pragma unroll
     for (int e = 0; e < 16; e++) negm[e] = -m;
@@ -656,7 +670,10 @@ __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const Pref
     //      f32 at a time; float4 column c of row r at r * 16 + (c ^ (r & 15)), so both
     //      sides are conflict-free) and stored row-coalesced: 16 lanes write one row's
     //      256 bytes ----
-    const float inv = __builtin_amdgcn_ldexpf(1.0f / xor32_sum(l), E);  // rows past T: l = 1, acc = 0
+    // split keys: the unnormalised partial (acc in true units, m, l) goes to this split's records
+    const float lsum = xor32_sum(l);
+    const float inv = __builtin_amdgcn_ldexpf(n_split == 1 ? 1.0f / lsum : 1.0f, E);  // rows past T: l = 1, acc = 0
+    if (n_split > 1 && hh == 0 && row_ok) *(float2 *)(part_row(my_t) + HEAD_DIM) = make_float2(m, lsum);
     float4 *const ob = (float4 *)&q_lds[wave][0][0];
 #pragma unroll
     for (int half = 0; half < 2; half++) {
@@ -672,9 +689,43 @@ __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const Pref
         for (int i = 0; i < 8; i++) {
             const int r = 4 * i + (lane >> 4), c = lane & 15;
             const float4 v = ob[r * 16 + (c ^ (r & 15))];
-            if (t0 + r < P.T) *(float4 *)(P.att + (size_t)(t0 + r) * Q_DIM + hq * HEAD_DIM + 64 * half + 4 * c) = v;
+            if (t0 + r < P.T) {
+                float *dst = n_split == 1 ? P.att + (size_t)(t0 + r) * Q_DIM + hq * HEAD_DIM : part_row(t0 + r);
+                *(float4 *)(dst + 64 * half + 4 * c) = v;
+            }
         }
     }
+}
+
+// Merge of a split prefill (fused.metal:331-350 per query row): one wave per (row t, head),
+// lane l holds dims 2l, 2l + 1 and the (m, l) pair of split l; the records are read 8 splits
+// at a time (indices past n_split repeat the last one with weight 0); splits with l = 0 (no
+// key of the row) get weight 0 and are skipped.
+__global__ __launch_bounds__(256) void prefill_combine_kernel(const PrefillParams P) {
+    const int lane = threadIdx.x & 63, pair = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (pair >= P.T * N_HEAD) return;
+    const int t = pair / N_HEAD, hq = pair % N_HEAD, ns = P.n_split;
+    const float *rec = P.part + ((size_t)t * N_HEAD + hq) * PF_PART_STRIDE;
+    const size_t sstride = (size_t)P.T * N_HEAD * PF_PART_STRIDE;
+    const float sink = P.sinks[hq] * LOG2E;
+    float2 ml = make_float2(sink, 0.f);
+    if (lane < ns) ml = *(const float2 *)(rec + lane * sstride + HEAD_DIM);
+    const float M = fmaxf(wave_max(ml.y != 0.f ? ml.x : -INFINITY), sink);
+    const float w = ml.y != 0.f ? __builtin_amdgcn_exp2f(ml.x - M) : 0.f;
+    const float L = wave_sum(ml.y * w) + __builtin_amdgcn_exp2f(sink - M);
+    float o0 = 0.f, o1 = 0.f;
+    for (int s0 = 0; s0 < ns; s0 += 8) {  // ns <= 64, so s0 + i < 64
+        float2 a[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) a[i] = *(const float2 *)(rec + min(s0 + i, ns - 1) * sstride + 2 * lane);
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float ws = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), s0 + i));
+            if (ws != 0.f) o0 += a[i].x * ws, o1 += a[i].y * ws;  // wave-uniform: a skipped split may hold anything
+        }
+    }
+    const float inv = 1.0f / L;
+    *(float2 *)(P.att + (size_t)t * Q_DIM + hq * HEAD_DIM + 2 * lane) = make_float2(o0 * inv, o1 * inv);
 }
 
 hipError_t launch_prefill(const PrefillParams &P, int dtype, hipStream_t stream) {
@@ -688,7 +739,9 @@ hipError_t launch_prefill(const PrefillParams &P, int dtype, hipStream_t stream)
         if (n_pre > 0) hipLaunchKernelGGL(prefix_kernel<DT_BF16>, gp, dim3(256), 0, stream, P);
         hipLaunchKernelGGL(kv_prep_kernel<DT_BF16>, gk, dim3(256), 0, stream, P);
     }
-    hipLaunchKernelGGL(flash_prefill_kernel, dim3(nqb * N_HEAD_KV), dim3(PF_THREADS), 0, stream, P, nqb);
+    hipLaunchKernelGGL(flash_prefill_kernel, dim3(nqb * P.n_split * N_HEAD_KV), dim3(PF_THREADS), 0, stream, P, nqb);
+    if (P.n_split > 1)
+        hipLaunchKernelGGL(prefill_combine_kernel, dim3((P.T * N_HEAD + 3) / 4), dim3(256), 0, stream, P);
     return hipGetLastError();
 }
 

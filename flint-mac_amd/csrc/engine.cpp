@@ -77,7 +77,7 @@ struct Workspace {
 };
 
 struct DeviceScratch {
-    Workspace partial, kv, gemm;
+    Workspace partial, kv, gemm, pf_part;
 };
 
 std::mutex g_scratch_mu;
@@ -266,6 +266,26 @@ void prefill_impl(const flint_attn_layer *L, const float *qkv, int q_stride, int
     uint32_t id = ++next_call;
     if (id == 0) id = ++next_call;
     P.call_id = id;
+    // Key splits when the grid of (query block, kv head) workgroups would leave most CUs idle on
+    // a long key range (a short prefill at a long context: one workgroup per kv head would stream
+    // the whole cache through one CU). Splits of the longest block's tiles, 8 at least, so the
+    // launch has about 512 workgroups; the merge kernel adds the sink.
+    {
+        const int nqb = (T + 31) / 32;
+        // tiles of the longest query block: the last one on a full layer; on an SWA layer at
+        // most the 18 tiles that a 32-query block's window [first - (window - 1), first + 31] spans
+        const int longest = L->is_swa ? std::min(((p0 + T - 1 - P.kbase) >> 5) + 1, (L->window + 62) / 32 + 1)
+                                      : ((p0 + T - 1) >> 5) + 1;
+        const int base = nqb * N_HEAD_KV;
+        int ns = 1;
+        if (base < 256 && longest >= 16)
+            ns = std::min({PF_MAX_SPLIT, (512 + base - 1) / base, (longest + 7) / 8});
+        const int tps = (longest + ns - 1) / ns;
+        P.n_split = (longest + tps - 1) / tps;
+        P.tps = P.n_split > 1 ? tps : 1 << 24;
+        if (P.n_split > 1)
+            P.part = (float *)scratch().pf_part.get((size_t)P.n_split * T * N_HEAD * PF_PART_STRIDE * sizeof(float));
+    }
     check(launch_prefill(P, L->kv_dtype, stream), "prefill launch");
 }
 

@@ -67,7 +67,14 @@ struct PrefillParams {
     int *texp;
     unsigned call_id;     // nonzero id of this call (see g_scaled_call in attn_prefill.hip)
     float *att;           // [T][4096]
+    // key splits (few query blocks over a long key range): each query block's tiles in n_split
+    // runs of tps tiles, partial records [n_split][T][32][PF_PART_STRIDE] in part, merged by
+    // prefill_combine_kernel; n_split = 1: no split, part unused
+    int n_split, tps;
+    float *part;
 };
+constexpr int PF_PART_STRIDE = 132;  // acc[128], m (log2 units), l, 2 pad
+constexpr int PF_MAX_SPLIT = 64;
 
 hipError_t launch_prefill(const PrefillParams &P, int dtype, hipStream_t stream);
 

@@ -256,3 +256,38 @@ def test_prefill_then_decode_bf16_beyond_f16_range(cuda, case, is_swa):
     vc = kv.v_slots()[0].float().cpu().numpy()
     for p in range(max(0, n - 1024) if is_swa else 0, n):
         assert np.array_equal(vc[:, kv.slot(p), :], V[p].reshape(N_HEAD_KV, HEAD_DIM)), f"V slot of pos {p}"
+
+
+@pytest.mark.parametrize("store", ["f16", "bf16"])
+@pytest.mark.parametrize("is_swa", [False, True], ids=["full", "swa"])
+def test_prefill_short_at_long_context_split_keys(cuda, store, is_swa):
+    """Short prefills after a long one, where the prefill cuts every query block's key range
+    into splits merged with the sink by a second kernel: continuations of T = 1, 7, 40, 100
+    tokens from p0 = 20005 (full layer: 626-630 key tiles, 63 splits of 10 tiles for the
+    first three, 32 of 20 for T = 100) and from p0 = 5003 (SWA ring: at most 18 tiles, 3
+    splits of 6). Every new position against the oracle, at the usual bars."""
+    p0 = 5003 if is_swa else 20005
+    Ts = (1, 7, 40, 100)
+    n = p0 + sum(Ts)
+    _say(f"short prefills at long context (split keys) swa={is_swa} store={store} p0={p0}")
+    rng = np.random.default_rng(81)
+    qn, kn, sk = layer_weights(rng)
+    qkv = rng.standard_normal((n, QKV_DIM)).astype(np.float32)
+    kv = fa.KVLayer(is_swa=is_swa, has_rope=True, n_slots=1024 if is_swa else (n + 31) // 32 * 32,
+                    kv_dtype=store, rope_theta=1e4, q_norm=qn, k_norm=kn, sinks=sk)
+    L = oracle_layer(kv, qn, kn, sk, store)
+    dq = torch.from_numpy(qkv).to(cuda)
+    att = torch.zeros((n, Q_DIM), device=cuda)
+    kv.prefill(dq[:p0], att[:p0], 0)
+    p = p0
+    for T in Ts:
+        kv.prefill(dq[p:p + T], att[p:p + T], p)
+        p += T
+    torch.cuda.synchronize()
+    got = att.cpu().numpy()
+    K, V = _oracle_history(L, qkv)
+    want = _oracle_at(L, qkv, K, V, range(p0, n))
+    p = p0
+    for T in Ts:
+        assert_close(got[p:p + T], np.stack([want[q] for q in range(p, p + T)]), f"T={T} at p0={p}")
+        p += T
