@@ -154,10 +154,10 @@ __global__ __launch_bounds__(256) void prefix_kernel(const PrefillParams P) {
 }
 
 // ---------------------------------------------------------------------------
-// kv_prep: the new tokens' K and V. grid (32-position chunks, kv head), 256 threads.
+// kv_prep: the new tokens' K and V. grid (32-position chunks, kv head), KP_THREADS threads.
 // Chunk c holds positions 32 c0 + 32 c .. +31 (32-aligned, so it is one tile of the
 // attention copy, whose kbase is 32-aligned, and one tile of the cache). Each wave
-// normalises (+ RoPE) 8 tokens' k (lane = a NEOX pair of dims) and rounds k and v to
+// normalises (+ RoPE) KP_ROWS tokens' k (lane = a NEOX pair of dims) and rounds k and v to
 // the cache dtype into LDS; the first chunk also takes the cached positions before p0
 // (from the copy, where prefix_kernel left their raw values), and positions past the last
 // new one are zero. Then every 16-byte unit
@@ -165,11 +165,12 @@ __global__ __launch_bounds__(256) void prefix_kernel(const PrefillParams P) {
 // new positions that the cache keeps go to the cache tile. A V unit of the cache spans 8
 // positions: where some of them are not new (or, for the ring, not kept) its elements are
 // stored one by one, so no cache unit is read back and no two workgroups write the same bytes.
+constexpr int KP_WAVES = 4, KP_THREADS = 64 * KP_WAVES, KP_ROWS = 32 / KP_WAVES;  // rows per wave
 template <int DT>
-__global__ __launch_bounds__(256) void kv_prep_kernel(const PrefillParams P) {
+__global__ __launch_bounds__(KP_THREADS) void kv_prep_kernel(const PrefillParams P) {
     typedef KvType<DT> KT;
     __shared__ uint16_t kl[32][HEAD_DIM + 8], vl[32][HEAD_DIM + 8];  // k and v in the cache dtype
-    __shared__ float red[2][4];
+    __shared__ float red[2][KP_WAVES];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, tid = threadIdx.x;
     const int kvh = blockIdx.y;
     const int c0 = (P.p0 >> 5) + blockIdx.x, pos0 = 32 * c0;  // first position of the chunk
@@ -178,10 +179,10 @@ __global__ __launch_bounds__(256) void kv_prep_kernel(const PrefillParams P) {
     const float rf = P.rope_freq[lane];
     // the wave's 8 tokens: all loads first (positions outside [lo, hi) read the chunk's
     // first new token, in range, and are not used), then the maths
-    float2 kx[8], vx[8];
+    float2 kx[KP_ROWS], vx[KP_ROWS];
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const int pos = pos0 + wave + 4 * i, t = (pos >= lo && pos < hi ? pos : lo) - P.p0;
+    for (int i = 0; i < KP_ROWS; i++) {
+        const int pos = pos0 + wave + KP_WAVES * i, t = (pos >= lo && pos < hi ? pos : lo) - P.p0;
         const float *kr = P.qkv + (size_t)t * P.q_stride + Q_DIM + kvh * HEAD_DIM;
         kx[i] = make_float2(kr[lane], kr[lane + 64]);
         vx[i] = make_float2(kr[KV_DIM + lane], kr[KV_DIM + lane + 64]);
@@ -191,8 +192,8 @@ __global__ __launch_bounds__(256) void kv_prep_kernel(const PrefillParams P) {
     // and selected afterwards: no branch between the rows, so their norm and RoPE chains
     // interleave. Rows past the new positions are zero.
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const int r = wave + 4 * i, pos = pos0 + r;
+    for (int i = 0; i < KP_ROWS; i++) {
+        const int r = wave + KP_WAVES * i, pos = pos0 + r;
         const bool is_new = pos >= lo && pos < hi;
         float cs = 1.f, sn = 0.f;
         if (P.has_rope) rope_sincos((float)pos * rf, &sn, &cs);
@@ -211,8 +212,8 @@ __global__ __launch_bounds__(256) void kv_prep_kernel(const PrefillParams P) {
         // (kbase <= pos0, 32-aligned)
         const uint16_t *raw = (const uint16_t *)P.sk;
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int r = wave + 4 * i, row = pos0 + r - P.kbase;
+        for (int i = 0; i < KP_ROWS; i++) {
+            const int r = wave + KP_WAVES * i, row = pos0 + r - P.kbase;
             if (pos0 + r < lo) {
                 const uint16_t k0 = raw[pk_index(kvh, row, lane, P.k_rows)];
                 const uint16_t k1 = raw[pk_index(kvh, row, lane + 64, P.k_rows)];
@@ -233,8 +234,11 @@ __global__ __launch_bounds__(256) void kv_prep_kernel(const PrefillParams P) {
     __syncthreads();
     int eK = 0, eV = 0;
     if constexpr (DT == DT_BF16) {
-        eK = tile_exp(fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3])), false);
-        eV = tile_exp(fmaxf(fmaxf(red[1][0], red[1][1]), fmaxf(red[1][2], red[1][3])), true);
+        float xk = red[0][0], xv = red[1][0];
+#pragma unroll
+        for (int w = 1; w < KP_WAVES; w++) xk = fmaxf(xk, red[0][w]), xv = fmaxf(xv, red[1][w]);
+        eK = tile_exp(xk, false);
+        eV = tile_exp(xv, true);
     }
     const int row0 = pos0 - P.kbase;               // attention-copy row of the chunk's first position
     if (tid == 0) put_texp(P, kvh, row0, eK, eV);
@@ -242,8 +246,8 @@ __global__ __launch_bounds__(256) void kv_prep_kernel(const PrefillParams P) {
     const int clo = max(lo, P.cache_from);         // cached positions [clo, hi)
     const int ctile = (pos0 & P.cache_mask) >> 5;  // the cache tile (slot = pos & mask, 32-aligned)
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-        const int u = tid + 256 * i;  // 16-byte unit of a 512-unit (8 KiB) tile
+    for (int i = 0; i < 512 / KP_THREADS; i++) {
+        const int u = tid + KP_THREADS * i;  // 16-byte unit of a 512-unit (8 KiB) tile
         // K, attention copy: unit (st, hh, col) = key pf_sigma(col), dims 16 st + 8 hh .. +7
         {
             const int st = u >> 6, hh = (u >> 5) & 1, col = u & 31, r = pf_sigma(col);
@@ -734,10 +738,10 @@ hipError_t launch_prefill(const PrefillParams &P, int dtype, hipStream_t stream)
     const dim3 gp(n_pre, N_HEAD_KV), gk(((P.p0 + P.T + 31) >> 5) - (P.p0 >> 5), N_HEAD_KV);
     if (dtype == DT_F16) {
         if (n_pre > 0) hipLaunchKernelGGL(prefix_kernel<DT_F16>, gp, dim3(256), 0, stream, P);
-        hipLaunchKernelGGL(kv_prep_kernel<DT_F16>, gk, dim3(256), 0, stream, P);
+        hipLaunchKernelGGL(kv_prep_kernel<DT_F16>, gk, dim3(KP_THREADS), 0, stream, P);
     } else {
         if (n_pre > 0) hipLaunchKernelGGL(prefix_kernel<DT_BF16>, gp, dim3(256), 0, stream, P);
-        hipLaunchKernelGGL(kv_prep_kernel<DT_BF16>, gk, dim3(256), 0, stream, P);
+        hipLaunchKernelGGL(kv_prep_kernel<DT_BF16>, gk, dim3(KP_THREADS), 0, stream, P);
     }
     hipLaunchKernelGGL(flash_prefill_kernel, dim3(nqb * P.n_split * N_HEAD_KV), dim3(PF_THREADS), 0, stream, P, nqb);
     if (P.n_split > 1)

@@ -8,7 +8,11 @@
  * the error style of the reference's C API (/root/reference/src/capi.mm:17-22).
  * Nothing here is thread-safe across concurrent calls on one engine or one
  * device workspace; callers serialise, as the reference requires of its
- * engine (/root/reference/src/capi.h:1).
+ * engine (/root/reference/src/capi.h:1). The workspace (split partials, the
+ * prefill's attention copy and partial records, projection scratch) is one set
+ * per device, shared by every layer, engine and model, so the calls must also be
+ * ordered on the GPU: one stream per device, or an event between streams. Host
+ * order alone lets kernels of two streams overlap.
  *
  * KV cache layout per layer and kv head (HBM, 16-bit elements), in tiles of 32 slots:
  *   K: [N_HEAD_KV][n_slots/32][4096]; within a tile, (slot r = slot % 32, dim d) is at
