@@ -67,6 +67,15 @@ __global__ __launch_bounds__(64) void get_rows_kernel(const RowsParams P) {
 // kernel start, and reads its lanes' 32-element slices of x from LDS.
 constexpr int MV_WAVES = 4;
 
+// x in LDS: float4 column c (elements 4c .. 4c+3) of sub-block s at s * 32 + 4 (c ^ ((s >> 1) & 7)).
+// Lane l reads its own sub-block's eight columns one instruction at a time; unswizzled, the
+// 64 lanes' addresses 128 bytes apart fell on two groups of 4 banks (32-way conflicts), and
+// with the swizzle any 8 consecutive lanes read 8 different columns.
+__device__ inline int xs_index(int e) {
+    const int s = e >> 5, c = (e >> 2) & 7;
+    return s * 32 + 4 * (c ^ ((s >> 1) & 7)) + (e & 3);
+}
+
 __device__ inline double wave_sum_f64(double v) {
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
@@ -151,7 +160,7 @@ __global__ __launch_bounds__(64 * MV_WAVES) void matvec_kernel(const MatvecParam
             for (int e = 0; e < 4; e++) xv[k][e] = xv[k][e] * scale * gv[k][e];
     }
 #pragma unroll
-    for (int k = 0; k < XPT / 4; k++) *(f32x4 *)&xs[XPT * tid + 4 * k] = xv[k];
+    for (int k = 0; k < XPT / 4; k++) *(f32x4 *)&xs[xs_index(XPT * tid + 4 * k)] = xv[k];
     __syncthreads();
 
     // this lane's slices of x: sub-blocks lane + 64 i
@@ -160,7 +169,7 @@ __global__ __launch_bounds__(64 * MV_WAVES) void matvec_kernel(const MatvecParam
     for (int i = 0; i < SUBS; i++)
 #pragma unroll
         for (int k = 0; k < 8; k++) {
-            const f32x4 v = *(const f32x4 *)&xs[32 * (lane + 64 * i) + 4 * k];
+            const f32x4 v = *(const f32x4 *)&xs[xs_index(32 * (lane + 64 * i) + 4 * k)];
             xl[i][4 * k] = v[0], xl[i][4 * k + 1] = v[1], xl[i][4 * k + 2] = v[2], xl[i][4 * k + 3] = v[3];
         }
     // The two row sources take separate code paths, so that each dequantiser's reads have a
@@ -180,12 +189,29 @@ __global__ __launch_bounds__(64 * MV_WAVES) void matvec_kernel(const MatvecParam
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
             float a = 0.f;
+            if (S.type == W_Q8_0) {
+                // d * sum(q x) per block: the dot needs no dequantised weights (one multiply
+                // per block instead of one per weight)
 #pragma unroll
-            for (int i = 0; i < SUBS; i++) {
-                float w[32];
-                deq32(S.type, stage[wave], lane + 64 * i, w);
+                for (int i = 0; i < SUBS; i++) {
+                    const uint16_t *p = (const uint16_t *)(stage[wave] + 34 * (lane + 64 * i));
+                    float b = 0.f;
 #pragma unroll
-                for (int e = 0; e < 32; e++) a = fmaf(w[e], xl[i][e], a);
+                    for (int e = 0; e < 16; e++) {
+                        const uint32_t v = p[1 + e];
+                        b = fmaf((float)(int8_t)(v & 0xff), xl[i][2 * e], b);
+                        b = fmaf((float)(int8_t)(v >> 8), xl[i][2 * e + 1], b);
+                    }
+                    a = fmaf(h2f(p[0]), b, a);
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < SUBS; i++) {
+                    float w[32];
+                    deq32(S.type, stage[wave], lane + 64 * i, w);
+#pragma unroll
+                    for (int e = 0; e < 32; e++) a = fmaf(w[e], xl[i][e], a);
+                }
             }
             acc[r] = a;
         }
