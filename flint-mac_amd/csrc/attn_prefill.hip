@@ -91,8 +91,9 @@ __device__ inline void put_texp(const PrefillParams &P, int kvh, int row0, int e
 }
 
 // ---------------------------------------------------------------------------
-// prefix: cache -> attention copy for the cached positions [kbase, p0). grid (tiles, kv head),
-// 256 threads. Block x < (p0 >> 5) - (kbase >> 5) takes a whole tile of cached positions: a
+// prefix: cache -> attention copy for the cached positions [kbase + 32 n_direct, p0) (the
+// n_direct whole tiles before them are read from the cache by the flash kernel itself).
+// grid (tiles, kv head), 256 threads. Block x takes tile n_direct + x; a whole tile of cached positions: a
 // cache tile and a copy tile both hold 16-byte units of 8 dims of one key (K) or 8 keys of one
 // dim (V), so each thread moves 2 + 2 units: read, measure, scale, convert to f16, write at
 // the unit's place in the copy. When p0 is not 32-aligned, one more block copies the cached
@@ -104,7 +105,7 @@ __global__ __launch_bounds__(256) void prefix_kernel(const PrefillParams P) {
     typedef KvType<DT> KT;
     __shared__ float red[2][4];
     const int kvh = blockIdx.y, tid = threadIdx.x;
-    const int row0 = 32 * blockIdx.x, pos0 = P.kbase + row0;  // the tile's first position
+    const int row0 = 32 * (P.n_direct + (int)blockIdx.x), pos0 = P.kbase + row0;  // the tile's first position
     if (pos0 + 32 > P.p0) {  // the tile holding p0: raw values of positions [pos0, p0)
         uint16_t *raw = (uint16_t *)P.sk;
         for (int i = tid; i < (P.p0 - pos0) * HEAD_DIM; i += 256) {
@@ -387,6 +388,9 @@ __device__ __forceinline__ void pf_pv(f32x16 (&acc)[4], const f16x8 (&vf)[8], co
 // Workgroup: 32 query positions x the 8 q heads of kv head kvh, wave w = head 8 kvh + w.
 // Two waves per SIMD (about 250 registers each): while one wave runs softmax
 // instructions the other can issue MFMAs.
+// DIRECT: some tiles come from the cache itself (n_direct > 0). A separate instantiation: the
+// per-tile source selection costs the loop 4 registers and ~7% of a config-4 full layer.
+template <bool DIRECT>
 __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const PrefillParams P, int n_qblocks) {
     // LDS: five 32-key tiles in the attention-copy order (tile t in ring[(t - t_lo) % 5])
     __shared__ f16x8 ring[PF_RING][16][64];
@@ -423,6 +427,31 @@ __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const Pref
         return;
     }
     const _Float16 *__restrict__ skv = P.sk + (size_t)kvh * (P.k_rows >> 5) * (16 * 64 * 8);
+    // Tile t (32 keys from kbase + 32 t): from the attention copy, or for t < n_direct (whole
+    // tiles of cached positions of an f16 cache, whose copy would hold the same bits) from the
+    // cache tile itself. Either way thread tid receives copy units tid (K) and 512 + tid (V):
+    // from the cache, the K unit of key pf_sigma(col), dims 16 st + 8 hh (kt_index order) and
+    // the V unit of dim 32 dt + (tid & 31), keys 16 kk + 8 hh (vt_index order). Branch-free
+    // (scalar bases, per-thread offsets), so the loads' wait counts stay static.
+    const int n_direct = DIRECT ? P.n_direct : 0;
+    const uint16_t *const ck = P.cache_k, *const cv = P.cache_v;
+    const int ctile0 = kvh * (P.n_slots >> 5), kbase = P.kbase, cmask = P.cache_mask;
+    const int dk = (int)kt_index(0, pf_sigma(tid & 31), 16 * (tid >> 6) + 8 * ((tid >> 5) & 1), 32);
+    const int dv = (int)vt_index(0, 16 * ((tid >> 6) & 1) + 8 * ((tid >> 5) & 1), 32 * (tid >> 7) + (tid & 31), 32);
+    auto gload = [&](PfTile &R, int t) {
+        if constexpr (!DIRECT) {
+            pf_gload(R, skv + (size_t)t * (PF_TILE_UNITS * 8), tid);
+            return;
+        }
+        const bool dir = t < n_direct;  // wave-uniform
+        const size_t ct = (size_t)ctile0 + (((kbase + 32 * t) & cmask) >> 5);
+        const uint16_t *kb = dir ? ck + ct * (32 * HEAD_DIM) : (const uint16_t *)skv + (size_t)t * (PF_TILE_UNITS * 8);
+        const uint16_t *vb = dir ? cv + ct * (32 * HEAD_DIM) : kb + PF_TILE_UNITS * 4;
+        const int ok = dir ? dk : 8 * tid, ov = dir ? dv : 8 * tid;
+        static_assert(PF_UNITS_PER_THREAD == 2, "one K and one V unit per thread");
+        R.u[0] = *(const u32x4 *)(kb + ok);
+        R.u[1] = *(const u32x4 *)(vb + ov);
+    };
 
     // ---- Q fragments (B operand of S^T = K Q^T): lane (col, hh) needs query row `col`,
     //      dims 16s + 8hh + e, in f16, after RMSNorm, NEOX RoPE and the scale
@@ -449,10 +478,10 @@ __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const Pref
         for (int k = 0; k < 4; k++) x[g][k] = *(const float4 *)(qp + 32 * k);
     }
     PfTile R0, R1, R2, R3;
-    pf_gload(R0, skv + (size_t)t_lo * (PF_TILE_UNITS * 8), tid);
-    if (t_lo + 1 <= t_hi) pf_gload(R1, skv + (size_t)(t_lo + 1) * (PF_TILE_UNITS * 8), tid);
-    if (t_lo + 2 <= t_hi) pf_gload(R2, skv + (size_t)(t_lo + 2) * (PF_TILE_UNITS * 8), tid);
-    if (t_lo + 3 <= t_hi) pf_gload(R3, skv + (size_t)(t_lo + 3) * (PF_TILE_UNITS * 8), tid);
+    gload(R0, t_lo);
+    if (t_lo + 1 <= t_hi) gload(R1, t_lo + 1);
+    if (t_lo + 2 <= t_hi) gload(R2, t_lo + 2);
+    if (t_lo + 3 <= t_hi) gload(R3, t_lo + 3);
 
     // After the RMSNorm |q| <= sqrt(128) |gain|, and the scale log2(e)/sqrt(128) follows: q
     // gains that could take q past f16's range, or keep it below 2^-6, make q be stored scaled
@@ -533,7 +562,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const Pref
             __syncthreads();  // every wave is done with the previous tile's LDS
             {
                 PfTile Rt;
-                pf_gload(Rt, skv + (size_t)t * (PF_TILE_UNITS * 8), tid);
+                gload(Rt, t);
                 pf_lstore(Rt, ring[0], tid);
             }
             __syncthreads();
@@ -542,7 +571,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const Pref
             for (int st = 0; st < 8; st++) kf[st] = ring[0][st][lane];
 #pragma unroll
             for (int i = 0; i < 8; i++) vf[i] = ring[0][8 + i][lane];
-            const int tx = te[t];  // wave-uniform
+            const int tx = t < n_direct ? 0 : te[t];  // wave-uniform (cache tiles: unscaled f16)
             const int eK = (int)(int16_t)(tx & 0xffff), eV = tx >> 16;
             f32x16 sc = pf_scores(kf, qf, f32x16{});
             const float ssc = __builtin_amdgcn_ldexpf(1.f, eK + eQ);
@@ -591,7 +620,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const Pref
     if (t_lo + 2 <= t_hi) pf_lstore(R2, ring[2], tid);
     if (t_lo + 3 <= t_hi) pf_lstore(R3, ring[3], tid);
     PfTile R;
-    if (t_lo + 4 <= t_hi) pf_gload(R, skv + (size_t)(t_lo + 4) * (PF_TILE_UNITS * 8), tid);
+    if (t_lo + 4 <= t_hi) gload(R, t_lo + 4);
     __syncthreads();
 
     f16x8 kf[8], vf[8];
@@ -628,7 +657,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const Pref
                 const int u = tid + PF_THREADS * g;
                 ring[sl4][u >> 6][u & 63] = __builtin_bit_cast(f16x8, R.u[g]);
             }
-            if (g == PF_UNITS_PER_THREAD && ld5) pf_gload(R, skv + (size_t)(t + 5) * (PF_TILE_UNITS * 8), tid);
+            if (g == PF_UNITS_PER_THREAD && ld5) gload(R, t + 5);
             __builtin_amdgcn_sched_barrier(0);
         }
         const f16x8 pf[2] = {__builtin_bit_cast(f16x8, u32x4{pw[0], pw[1], pw[2], pw[3]}),
@@ -733,7 +762,8 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(const PrefillParam
 }
 
 hipError_t launch_prefill(const PrefillParams &P, int dtype, hipStream_t stream) {
-    const int n_pre = (P.p0 - P.kbase + 31) >> 5;  // tiles holding cached positions (kbase 32-aligned)
+    // tiles holding cached positions (kbase 32-aligned) that the copy takes from the cache
+    const int n_pre = ((P.p0 - P.kbase + 31) >> 5) - P.n_direct;
     const int nqb = (P.T + PF_BQ - 1) / PF_BQ;
     const dim3 gp(n_pre, N_HEAD_KV), gk(((P.p0 + P.T + 31) >> 5) - (P.p0 >> 5), N_HEAD_KV);
     if (dtype == DT_F16) {
@@ -743,7 +773,11 @@ hipError_t launch_prefill(const PrefillParams &P, int dtype, hipStream_t stream)
         if (n_pre > 0) hipLaunchKernelGGL(prefix_kernel<DT_BF16>, gp, dim3(256), 0, stream, P);
         hipLaunchKernelGGL(kv_prep_kernel<DT_BF16>, gk, dim3(KP_THREADS), 0, stream, P);
     }
-    hipLaunchKernelGGL(flash_prefill_kernel, dim3(nqb * P.n_split * N_HEAD_KV), dim3(PF_THREADS), 0, stream, P, nqb);
+    const dim3 gf(nqb * P.n_split * N_HEAD_KV);
+    if (P.n_direct > 0)
+        hipLaunchKernelGGL(flash_prefill_kernel<true>, gf, dim3(PF_THREADS), 0, stream, P, nqb);
+    else
+        hipLaunchKernelGGL(flash_prefill_kernel<false>, gf, dim3(PF_THREADS), 0, stream, P, nqb);
     if (P.n_split > 1)
         hipLaunchKernelGGL(prefill_combine_kernel, dim3((P.T * N_HEAD + 3) / 4), dim3(256), 0, stream, P);
     return hipGetLastError();

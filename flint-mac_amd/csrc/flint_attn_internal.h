@@ -65,6 +65,11 @@ struct PrefillParams {
     // per kv head and 32-key tile of the copy: the power-of-two exponents its K and V values
     // were scaled by to fit f16, (eK & 0xffff) | eV << 16 ([4][k_rows / 32]; 0 = stored as is)
     int *texp;
+    // tiles 0 .. n_direct - 1 of the copy's range (whole tiles of cached positions) are read by
+    // the flash kernel from the cache itself and neither copied nor given exponents: set for f16
+    // caches, where the copy would hold the same bits, when no cache slot they read is rewritten
+    // by this call's kv_prep with a key some query still needs; 0 otherwise
+    int n_direct;
     unsigned call_id;     // nonzero id of this call (see g_scaled_call in attn_prefill.hip)
     float *att;           // [T][4096]
     // key splits (few query blocks over a long key range): each query block's tiles in n_split

@@ -291,3 +291,31 @@ def test_prefill_short_at_long_context_split_keys(cuda, store, is_swa):
     for T in Ts:
         assert_close(got[p:p + T], np.stack([want[q] for q in range(p, p + T)]), f"T={T} at p0={p}")
         p += T
+
+
+@pytest.mark.parametrize("is_swa", [False, True], ids=["full", "swa"])
+def test_prefill_f16_cached_tiles_on_scaled_path(cuda, is_swa):
+    """An f16 continuation reads its whole cached tiles from the cache itself; with q gains
+    x1e-3 (q below f16's normal range, so q is stored scaled and the tile-by-tile path runs)
+    those tiles must count as unscaled. 700 tokens, then 250 from p0 = 700 (21 cached tiles
+    read in place, the p0 tile through the copy), against the oracle."""
+    _say(f"f16 cached tiles on the scaled path swa={is_swa}")
+    rng = np.random.default_rng(91)
+    qn, kn, sk = layer_weights(rng)
+    qn = (qn * 1e-3).astype(np.float32)
+    n = 950
+    qkv = rng.standard_normal((n, QKV_DIM)).astype(np.float32)
+    kv = fa.KVLayer(is_swa=is_swa, has_rope=True, n_slots=1024, kv_dtype="f16", rope_theta=1e4,
+                    q_norm=qn, k_norm=kn, sinks=sk)
+    L = oracle_layer(kv, qn, kn, sk, "f16")
+    dq = torch.from_numpy(qkv).to(cuda)
+    att = torch.zeros((n, Q_DIM), device=cuda)
+    kv.prefill(dq[:700], att[:700], 0)
+    kv.prefill(dq[700:], att[700:], 700)
+    torch.cuda.synchronize()
+    K, V = _oracle_history(L, qkv)
+    probes = [700, 701, 731, 732, 850, 949]
+    want = _oracle_at(L, qkv, K, V, probes)
+    got = att.cpu().numpy()
+    for p in probes:
+        assert_close(got[p], want[p], f"pos {p}")
