@@ -155,35 +155,40 @@ __global__ __launch_bounds__(256) void prefix_kernel(const PrefillParams P) {
 }
 
 // ---------------------------------------------------------------------------
-// kv_prep: the new tokens' K and V. grid (32-position chunks, kv head), KP_THREADS threads.
+// kv_prep: the new tokens' K and V. grid (32-position chunks, kv head), 4 waves.
 // Chunk c holds positions 32 c0 + 32 c .. +31 (32-aligned, so it is one tile of the
-// attention copy, whose kbase is 32-aligned, and one tile of the cache). Each wave
-// normalises (+ RoPE) KP_ROWS tokens' k (lane = a NEOX pair of dims) and rounds k and v to
-// the cache dtype into LDS; the first chunk also takes the cached positions before p0
-// (from the copy, where prefix_kernel left their raw values), and positions past the last
-// new one are zero. Then every 16-byte unit
-// of the copy tile is written with one store (scaled by the tile's exponents), and the
-// new positions that the cache keeps go to the cache tile. A V unit of the cache spans 8
+// attention copy, whose kbase is 32-aligned, and one tile of the cache). Wave w owns the 8
+// consecutive rows 8w .. 8w+7 (their addresses are wave-uniform, so scalar): it normalises
+// (+ RoPE) each row's k (lane = a NEOX pair of dims), rounds k and v to the cache dtype into
+// LDS (k row-major, v transposed), then writes every 16-byte unit those rows make: the copy's
+// K units (one key, 8 dims) and V units (one dim, these 8 keys), scaled by the tile's
+// exponents, and the cache's units of the new positions it keeps. So an f16 chunk needs no
+// workgroup barrier (a bf16 chunk has one, for the tile's exponents). The first chunk also
+// takes the cached positions before p0 (from the copy, where prefix_kernel left their raw
+// values), and rows past the last new position are zero. A V unit of the cache spans the 8
 // positions: where some of them are not new (or, for the ring, not kept) its elements are
 // stored one by one, so no cache unit is read back and no two workgroups write the same bytes.
 constexpr int KP_WAVES = 4, KP_THREADS = 64 * KP_WAVES, KP_ROWS = 32 / KP_WAVES;  // rows per wave
+static_assert(KP_ROWS == 8, "a wave's rows make whole V units (8 keys)");
 template <int DT>
 __global__ __launch_bounds__(KP_THREADS) void kv_prep_kernel(const PrefillParams P) {
     typedef KvType<DT> KT;
-    __shared__ uint16_t kl[32][HEAD_DIM + 8], vl[32][HEAD_DIM + 8];  // k and v in the cache dtype
+    __shared__ __align__(16) uint16_t kl[32][HEAD_DIM + 8];  // k in the cache dtype, [row][dim]
+    __shared__ __align__(16) uint16_t vt[HEAD_DIM][32 + 8];  // v in the cache dtype, [dim][row]
     __shared__ float red[2][KP_WAVES];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, tid = threadIdx.x;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int kvh = blockIdx.y;
     const int c0 = (P.p0 >> 5) + blockIdx.x, pos0 = 32 * c0;  // first position of the chunk
     const int lo = max(P.p0, pos0), hi = min(P.p0 + P.T, pos0 + 32);  // new positions [lo, hi)
+    const int r0 = KP_ROWS * wave;  // this wave's rows r0 .. r0 + 7
     const float2 kw = make_float2(P.k_norm[lane], P.k_norm[lane + 64]);
     const float rf = P.rope_freq[lane];
-    // the wave's 8 tokens: all loads first (positions outside [lo, hi) read the chunk's
-    // first new token, in range, and are not used), then the maths
+    // the rows' k and v: all loads first (rows outside [lo, hi) read the chunk's first new
+    // token, in range, and are not used), then the maths
     float2 kx[KP_ROWS], vx[KP_ROWS];
 #pragma unroll
     for (int i = 0; i < KP_ROWS; i++) {
-        const int pos = pos0 + wave + KP_WAVES * i, t = (pos >= lo && pos < hi ? pos : lo) - P.p0;
+        const int pos = pos0 + r0 + i, t = (pos >= lo && pos < hi ? pos : lo) - P.p0;  // wave-uniform
         const float *kr = P.qkv + (size_t)t * P.q_stride + Q_DIM + kvh * HEAD_DIM;
         kx[i] = make_float2(kr[lane], kr[lane + 64]);
         vx[i] = make_float2(kr[KV_DIM + lane], kr[KV_DIM + lane + 64]);
@@ -194,33 +199,33 @@ __global__ __launch_bounds__(KP_THREADS) void kv_prep_kernel(const PrefillParams
     // interleave. Rows past the new positions are zero.
 #pragma unroll
     for (int i = 0; i < KP_ROWS; i++) {
-        const int r = wave + KP_WAVES * i, pos = pos0 + r;
+        const int r = r0 + i, pos = pos0 + r;
         const bool is_new = pos >= lo && pos < hi;
         float cs = 1.f, sn = 0.f;
         if (P.has_rope) rope_sincos((float)pos * rf, &sn, &cs);
         const float2 k2 = norm_rope_pair(kx[i], kw, P.rms_eps, P.has_rope, cs, sn);
         const uint16_t k0 = is_new ? KT::from_float(k2.x) : 0, k1 = is_new ? KT::from_float(k2.y) : 0;
         const uint16_t v0 = is_new ? KT::from_float(vx[i].x) : 0, v1 = is_new ? KT::from_float(vx[i].y) : 0;
-        kl[r][lane] = k0, kl[r][lane + 64] = k1, vl[r][lane] = v0, vl[r][lane + 64] = v1;
+        kl[r][lane] = k0, kl[r][lane + 64] = k1, vt[lane][r] = v0, vt[lane + 64][r] = v1;
         if constexpr (DT == DT_BF16) {
             mk = fmaxf(mk, fmaxf(fabsf(KT::to_float(k0)), fabsf(KT::to_float(k1))));
             mv = fmaxf(mv, fmaxf(fabsf(KT::to_float(v0)), fabsf(KT::to_float(v1))));
         }
     }
-    if (pos0 < lo) {
+    if (pos0 + r0 < lo) {  // wave-uniform
         // the first chunk of a continuation that starts inside a tile: its cached positions
         // [pos0, p0) come from the copy, where prefix_kernel left the cache's raw values
         // (kbase <= pos0, 32-aligned)
         const uint16_t *raw = (const uint16_t *)P.sk;
 #pragma unroll
         for (int i = 0; i < KP_ROWS; i++) {
-            const int r = wave + KP_WAVES * i, row = pos0 + r - P.kbase;
+            const int r = r0 + i, row = pos0 + r - P.kbase;
             if (pos0 + r < lo) {
                 const uint16_t k0 = raw[pk_index(kvh, row, lane, P.k_rows)];
                 const uint16_t k1 = raw[pk_index(kvh, row, lane + 64, P.k_rows)];
                 const uint16_t v0 = raw[pv_index(kvh, row, lane, P.k_rows)];
                 const uint16_t v1 = raw[pv_index(kvh, row, lane + 64, P.k_rows)];
-                kl[r][lane] = k0, kl[r][lane + 64] = k1, vl[r][lane] = v0, vl[r][lane + 64] = v1;
+                kl[r][lane] = k0, kl[r][lane + 64] = k1, vt[lane][r] = v0, vt[lane + 64][r] = v1;
                 if constexpr (DT == DT_BF16) {
                     mk = fmaxf(mk, fmaxf(fabsf(KT::to_float(k0)), fabsf(KT::to_float(k1))));
                     mv = fmaxf(mv, fmaxf(fabsf(KT::to_float(v0)), fabsf(KT::to_float(v1))));
@@ -228,71 +233,56 @@ __global__ __launch_bounds__(KP_THREADS) void kv_prep_kernel(const PrefillParams
             }
         }
     }
+    int eK = 0, eV = 0;
     if constexpr (DT == DT_BF16) {
         mk = wave_max(mk), mv = wave_max(mv);
         if (lane == 0) red[0][wave] = mk, red[1][wave] = mv;
-    }
-    __syncthreads();
-    int eK = 0, eV = 0;
-    if constexpr (DT == DT_BF16) {
+        __syncthreads();  // also makes every wave's rows visible (only this wave's are read)
         float xk = red[0][0], xv = red[1][0];
 #pragma unroll
         for (int w = 1; w < KP_WAVES; w++) xk = fmaxf(xk, red[0][w]), xv = fmaxf(xv, red[1][w]);
         eK = tile_exp(xk, false);
         eV = tile_exp(xv, true);
+    } else {
+        // only this wave's rows are read back
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
-    const int row0 = pos0 - P.kbase;               // attention-copy row of the chunk's first position
-    if (tid == 0) put_texp(P, kvh, row0, eK, eV);
-    const bool to_cache = hi > P.cache_from;       // some positions go to the cache
-    const int clo = max(lo, P.cache_from);         // cached positions [clo, hi)
+    const int row0 = pos0 - P.kbase;  // attention-copy row of the chunk's first position
+    if (threadIdx.x == 0) put_texp(P, kvh, row0, eK, eV);
+    const int clo = max(lo, P.cache_from);         // positions [clo, hi) go to the cache
+    const bool to_cache = hi > clo;
     const int ctile = (pos0 & P.cache_mask) >> 5;  // the cache tile (slot = pos & mask, 32-aligned)
 #pragma unroll
-    for (int i = 0; i < 512 / KP_THREADS; i++) {
-        const int u = tid + KP_THREADS * i;  // 16-byte unit of a 512-unit (8 KiB) tile
-        // K, attention copy: unit (st, hh, col) = key pf_sigma(col), dims 16 st + 8 hh .. +7
+    for (int m = 0; m < 2; m++) {
+        const int j = lane + 64 * m;  // 128 units per kind: 8 keys x 16 dim groups, 128 dims
+        // K units of key r0 + (j & 7), dims 8 (j >> 3) .. +7: the copy's (16 st + 8 hh) and the cache's
         {
-            const int st = u >> 6, hh = (u >> 5) & 1, col = u & 31, r = pf_sigma(col);
+            const int r = r0 + (j & 7), d0 = 8 * (j >> 3);
+            const u16x8 kv = *(const u16x8 *)&kl[r][d0];
             f16x8 v;
 #pragma unroll
-            for (int e = 0; e < 8; e++)
-                v[e] = (_Float16)__builtin_amdgcn_ldexpf(KT::to_float(kl[r][16 * st + 8 * hh + e]), -eK);
-            *(f16x8 *)(P.sk + pk_index(kvh, row0 + r, 16 * st + 8 * hh, P.k_rows)) = v;
+            for (int e = 0; e < 8; e++) v[e] = (_Float16)__builtin_amdgcn_ldexpf(KT::to_float(kv[e]), -eK);
+            *(f16x8 *)(P.sk + pk_index(kvh, row0 + r, d0, P.k_rows)) = v;
+            if (to_cache && pos0 + r >= clo && pos0 + r < hi)
+                *(u16x8 *)(P.cache_k + kt_index(kvh, 32 * ctile + r, d0, P.n_slots)) = kv;
         }
-        // V, attention copy: unit (dt, kk, hh, d) = dim 32 dt + d, keys 16 kk + 8 hh .. +7
+        // V units of dim j, keys r0 .. r0 + 7
         {
-            const int dt = u >> 7, kk = (u >> 6) & 1, hh = (u >> 5) & 1, d = 32 * dt + (u & 31);
-            const int r0 = 16 * kk + 8 * hh;
+            const u16x8 vv = *(const u16x8 *)&vt[j][r0];
             f16x8 v;
 #pragma unroll
-            for (int e = 0; e < 8; e++) v[e] = (_Float16)__builtin_amdgcn_ldexpf(KT::to_float(vl[r0 + e][d]), -eV);
-            *(f16x8 *)(P.sk + pv_index(kvh, row0 + r0, d, P.k_rows)) = v;
-        }
-        if (to_cache) {
-            // K, cache tile (kt_index order): unit (st, c, g, n) = key 8(n>>2) + 4st + (n&3),
-            // dims 32c + 8g .. +7
-            {
-                const int st = u >> 8, c = (u >> 6) & 3, g = (u >> 4) & 3, n = u & 15;
-                const int r = 8 * (n >> 2) + 4 * st + (n & 3), d = 32 * c + 8 * g;
-                if (pos0 + r >= clo && pos0 + r < hi) {
-                    u16x8 v;
-#pragma unroll
-                    for (int e = 0; e < 8; e++) v[e] = kl[r][d + e];
-                    *(u16x8 *)(P.cache_k + kt_index(kvh, 32 * ctile + r, d, P.n_slots)) = v;
-                }
-            }
-            // V, cache tile (vt_index order): unit (d, g) = dim d, slots 8g .. 8g+7 of the tile
-            {
-                const int d = u >> 2, r0 = 8 * (u & 3);
-                uint16_t *dst = P.cache_v + vt_index(kvh, 32 * ctile + r0, d, P.n_slots);
-                if (pos0 + r0 >= clo && pos0 + r0 + 8 <= hi) {
-                    u16x8 v;
-#pragma unroll
-                    for (int e = 0; e < 8; e++) v[e] = vl[r0 + e][d];
-                    *(u16x8 *)dst = v;
+            for (int e = 0; e < 8; e++) v[e] = (_Float16)__builtin_amdgcn_ldexpf(KT::to_float(vv[e]), -eV);
+            *(f16x8 *)(P.sk + pv_index(kvh, row0 + r0, j, P.k_rows)) = v;
+            if (to_cache) {
+                uint16_t *dst = P.cache_v + vt_index(kvh, 32 * ctile + r0, j, P.n_slots);
+                if (pos0 + r0 >= clo && pos0 + r0 + 8 <= hi) {  // wave-uniform
+                    *(u16x8 *)dst = vv;
                 } else {
 #pragma unroll
                     for (int e = 0; e < 8; e++)
-                        if (pos0 + r0 + e >= clo && pos0 + r0 + e < hi) dst[e] = vl[r0 + e][d];
+                        if (pos0 + r0 + e >= clo && pos0 + r0 + e < hi) dst[e] = vv[e];
                 }
             }
         }
