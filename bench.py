@@ -165,7 +165,7 @@ def bench_decode_swa(torch, fa, reps=200, pos=32768):
     return queued_launch_ms(torch, step, max(1, reps // n))[0] / n
 
 
-def bench_decode_step_49(torch, fa, steps=20, ctx=32768):
+def bench_decode_step_49(torch, fa, steps=6, ctx=32768):
     """A whole decode step of the attention stage at 32k, timed: Flint's 49 layers in order
     (14 full at pos 32768, each with its own 64 MiB cache, and 35 SWA layers with their rings),
     one flint_attn_decode per layer, back to back on one stream (Engine::step's attention
@@ -188,6 +188,9 @@ def bench_decode_step_49(torch, fa, steps=20, ctx=32768):
         for i, kv in enumerate(layers):
             kv.decode(qkv[i], att[i], ctx)
 
+    # 6 steps = 378 launches: more queued behind the spin kernel fill the stream's queue, and
+    # hipLaunchKernel then blocks until the GPU frees slots, so the host's per-call Python cost
+    # (~10 us) would enter the timed region (host_bound)
     ms, host_bound = queued_launch_ms(torch, step, steps, 2)
     nbytes = sum(decode_bytes(ctx) if full else decode_bytes(512) for full in FLINT_FULL_LAYERS)
     del layers
