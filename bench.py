@@ -202,7 +202,10 @@ def bench_decode_step_49(torch, fa, steps=6, ctx=32768):
 
 def bench_prefill(torch, fa, T=4000, reps=10, kinds=("full", "swa")):
     """Config 4: one prefill call of T = 4000 tokens from position 0 (kv_prep_kernel + flash_prefill_kernel),
-    bf16 KV, per layer kind; time per call from HIP events around `reps` calls on the launching stream."""
+    bf16 KV, per layer kind; time per call from HIP events around `reps` calls queued behind a spin
+    kernel, as the decode line (the events then see the GPU timeline: with the first call launched
+    onto an idle GPU right after the start event, the same 10 calls measured 78-80 instead of 71 us
+    per SWA call and 151-152 instead of 146-147 us per full-layer call)."""
     import numpy as np
     dev = torch.device("cuda:0")
     rng = np.random.default_rng(3)
@@ -214,26 +217,18 @@ def bench_prefill(torch, fa, T=4000, reps=10, kinds=("full", "swa")):
         kv = fa.KVLayer(is_swa=is_swa, has_rope=is_swa, n_slots=1024 if is_swa else T, kv_dtype="bf16",
                         q_norm=rng.uniform(0.5, 1.5, 128), k_norm=rng.uniform(0.5, 1.5, 128),
                         sinks=rng.standard_normal(32), device=dev)
-        for _ in range(2):
-            kv.prefill(qkv, att, 0)
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(reps):
-            kv.prefill(qkv, att, 0)
-        e1.record()
-        torch.cuda.synchronize()
-        ms = e0.elapsed_time(e1) / reps
+        ms, host_bound = queued_launch_ms(torch, lambda: kv.prefill(qkv, att, 0), reps)
         flops = prefill_flops(T, 513 if is_swa else None)
         tflops = flops / (ms * 1e-3) / 1e12
-        out[name] = dict(ms=ms, flops=flops, tflops=tflops, frac_of_mfma_peak=tflops / MFMA_PEAK_TFLOPS,
+        out[name] = dict(ms=ms, flops=flops, tflops=tflops, frac_of_mfma_peak=tflops / MFMA_PEAK_TFLOPS, host_bound=host_bound,
                          roofline={"bound": "mfma", "achieved": round(tflops, 1), "peak": MFMA_PEAK_TFLOPS,
                                    "unit": "TFLOP/s", "frac": round(tflops / MFMA_PEAK_TFLOPS, 4),
                                    "traffic": PREFILL_TRAFFIC_BYTES[name],
                                    "kernel": "one flint_attn_prefill call on a " + ("SWA-513" if is_swa else "full causal")
                                              + " layer = kv_prep_kernel + flash_prefill_kernel (f16 MFMA 32x32x16 on "
                                              "the exact f16 copy of the bf16 K/V); achieved = algorithmic FLOPs / "
-                                             "time per call from HIP events"})
+                                             "time per call from HIP events around calls queued behind a spin "
+                                             "kernel"})
         del kv
     return out
 
