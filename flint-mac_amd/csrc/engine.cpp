@@ -363,25 +363,28 @@ void check_tokens(int n_tok, const char *name) {
 // A batch of T tokens through one projection on the matrix cores (proj_gemm.hip): the weight
 // rows of the segments and the activation rows as f16 hi/lo planes in the device workspace, then
 // y[t][0:N] (+)= W x[t] (x RMSNorm'd with norm_w when given).
+// pl: the weights' planes, kept by the caller (then no weight prep here); T = 0 only builds them
+// into *pl
 void proj_gemm(const MatvecSeg *seg, int n_seg, int N, int K, const float *x, long long x_stride, const float *norm_w,
-               float eps, int T, float *y, long long y_stride, int add, hipStream_t stream) {
-    const int T_pad = (T + GEMM_TILE - 1) / GEMM_TILE * GEMM_TILE;
-    const size_t wbytes = (size_t)N * K * sizeof(_Float16), xbytes = (size_t)T_pad * K * sizeof(_Float16);
+               float eps, int T, float *y, long long y_stride, int add, const WeightPlanes *pl, hipStream_t stream,
+               bool build_only = false) {
+    const int T_pad = build_only ? 0 : (T + GEMM_TILE - 1) / GEMM_TILE * GEMM_TILE;
+    const size_t wbytes = pl ? 0 : (size_t)N * K * sizeof(_Float16), xbytes = (size_t)T_pad * K * sizeof(_Float16);
     size_t off = 0;
     auto take = [&](size_t b) {
         const size_t o = off;
         off += (b + 255) / 256 * 256;
         return o;
     };
-    const size_t o_wh = take(wbytes), o_wl = take(wbytes), o_f = take((size_t)N * sizeof(int));
+    const size_t o_wh = take(wbytes), o_wl = take(wbytes), o_f = take(pl ? 0 : (size_t)N * sizeof(int));
     const size_t o_xh = take(xbytes), o_xl = take(xbytes), o_e = take((size_t)T_pad * sizeof(int));
-    char *ws = (char *)scratch().gemm.get(off);
+    char *ws = off ? (char *)scratch().gemm.get(off) : nullptr;
     GemmWeightParams W{};
     for (int i = 0; i < n_seg; i++) W.seg[i] = seg[i];
     W.n_seg = n_seg;
-    W.wh = (_Float16 *)(ws + o_wh);
-    W.wl = (_Float16 *)(ws + o_wl);
-    W.fexp = (int *)(ws + o_f);
+    W.wh = pl ? pl->wh : (_Float16 *)(ws + o_wh);
+    W.wl = pl ? pl->wl : (_Float16 *)(ws + o_wl);
+    W.fexp = pl ? pl->fexp : (int *)(ws + o_f);
     GemmActParams X{};
     X.x = x;
     X.x_stride = x_stride;
@@ -400,7 +403,7 @@ void proj_gemm(const MatvecSeg *seg, int n_seg, int N, int K, const float *x, lo
     G.N = N;
     G.K = K;
     G.T = T;
-    check(launch_proj_gemm(W, X, G, stream), "projection GEMM launch");
+    check(launch_proj_gemm(W, X, G, !pl || build_only, stream), "projection GEMM launch");
 }
 
 // the GEMM takes batches of GEMM_MIN_TOKENS and more whose output rows are 16-byte aligned
@@ -408,8 +411,20 @@ bool use_gemm(int n_tok, const float *y, long long y_stride) {
     return n_tok >= GEMM_MIN_TOKENS && aligned16(y) && y_stride % 4 == 0;
 }
 
+// the q/k/v segments of a layer's weights
+void qkv_segs(const flint_weight *wq, const flint_weight *wk, const flint_weight *wv, MatvecSeg *seg) {
+    check_weight(wq, N_EMBD, "wq");
+    check_weight(wk, N_EMBD, "wk");
+    check_weight(wv, N_EMBD, "wv");
+    const flint_weight *ws[3] = {wq, wk, wv};
+    const int row0[3] = {0, Q_DIM, Q_DIM + KV_DIM};
+    for (int i = 0; i < 3; i++)
+        seg[i] = MatvecSeg{(const uint8_t *)ws[i]->data, ws[i]->type, row0[i], (int)w_row_bytes(ws[i]->type, N_EMBD)};
+}
+
 void qkv_proj_impl(const flint_weight *wq, const flint_weight *wk, const flint_weight *wv, const float *x, int n_tok,
-                   const float *attn_norm, float eps, float *qkv, int qkv_stride, hipStream_t stream) {
+                   const float *attn_norm, float eps, float *qkv, int qkv_stride, hipStream_t stream,
+                   const WeightPlanes *pl = nullptr) {
     check_weight(wq, N_EMBD, "wq");
     check_weight(wk, N_EMBD, "wk");
     check_weight(wv, N_EMBD, "wv");
@@ -435,13 +450,14 @@ void qkv_proj_impl(const flint_weight *wq, const flint_weight *wk, const flint_w
     P.y = qkv;
     P.add = 0;
     if (use_gemm(n_tok, qkv, qkv_stride)) {
-        proj_gemm(P.seg, 3, QKV_DIM, N_EMBD, x, N_EMBD, attn_norm, eps, n_tok, qkv, qkv_stride, 0, stream);
+        proj_gemm(P.seg, 3, QKV_DIM, N_EMBD, x, N_EMBD, attn_norm, eps, n_tok, qkv, qkv_stride, 0, pl, stream);
         return;
     }
     check(launch_matvec(P, N_EMBD, stream), "qkv_proj launch");
 }
 
-void o_proj_impl(const flint_weight *wo, const float *att, int n_tok, float *x, hipStream_t stream) {
+void o_proj_impl(const flint_weight *wo, const float *att, int n_tok, float *x, hipStream_t stream,
+                 const WeightPlanes *pl = nullptr) {
     check_weight(wo, Q_DIM, "wo");
     check_tokens(n_tok, "o_proj");
     if (!att || !x) throw Error("o_proj: NULL pointer");
@@ -458,13 +474,52 @@ void o_proj_impl(const flint_weight *wo, const float *att, int n_tok, float *x, 
     P.y = x;
     P.add = 1;
     if (use_gemm(n_tok, x, N_EMBD)) {
-        proj_gemm(P.seg, 1, N_EMBD, Q_DIM, att, Q_DIM, nullptr, 0.f, n_tok, x, N_EMBD, 1, stream);
+        proj_gemm(P.seg, 1, N_EMBD, Q_DIM, att, Q_DIM, nullptr, 0.f, n_tok, x, N_EMBD, 1, pl, stream);
         return;
     }
     check(launch_matvec(P, Q_DIM, stream), "o_proj launch");
 }
 
 }  // namespace
+
+size_t planes_bytes(int N, int K) {
+    const size_t w = ((size_t)N * K * sizeof(_Float16) + 255) / 256 * 256;
+    return 2 * w + ((size_t)N * sizeof(int) + 255) / 256 * 256;
+}
+
+WeightPlanes planes_at(void *mem, int N, int K) {
+    const size_t w = ((size_t)N * K * sizeof(_Float16) + 255) / 256 * 256;
+    WeightPlanes pl;
+    pl.wh = (_Float16 *)mem;
+    pl.wl = (_Float16 *)((char *)mem + w);
+    pl.fexp = (int *)((char *)mem + 2 * w);
+    return pl;
+}
+
+void build_qkv_planes(const flint_weight *wq, const flint_weight *wk, const flint_weight *wv, const WeightPlanes &pl,
+                      hipStream_t stream) {
+    MatvecSeg seg[3];
+    qkv_segs(wq, wk, wv, seg);
+    proj_gemm(seg, 3, QKV_DIM, N_EMBD, nullptr, 0, nullptr, 0.f, 0, nullptr, 0, 0, &pl, stream, true);
+}
+
+void build_o_planes(const flint_weight *wo, const WeightPlanes &pl, hipStream_t stream) {
+    check_weight(wo, Q_DIM, "wo");
+    const MatvecSeg seg{(const uint8_t *)wo->data, wo->type, 0, (int)w_row_bytes(wo->type, Q_DIM)};
+    proj_gemm(&seg, 1, N_EMBD, Q_DIM, nullptr, 0, nullptr, 0.f, 0, nullptr, 0, 0, &pl, stream, true);
+}
+
+void qkv_proj_rows_planes(const flint_weight *wq, const flint_weight *wk, const flint_weight *wv, const float *x,
+                          int n_tok, const float *attn_norm, float eps, float *qkv, int qkv_stride,
+                          const WeightPlanes *pl, hipStream_t stream) {
+    qkv_proj_impl(wq, wk, wv, x, n_tok, attn_norm, eps, qkv, qkv_stride, stream, pl);
+}
+
+void o_proj_rows_planes(const flint_weight *wo, const float *att, int n_tok, float *x, const WeightPlanes *pl,
+                        hipStream_t stream) {
+    o_proj_impl(wo, att, n_tok, x, stream, pl);
+}
+
 }  // namespace flint
 
 using namespace flint;

@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "flint_proj.h"  // flint_weight (include/, on the include path)
+
 namespace flint {
 
 constexpr int MAX_SEQ = 64;  // sequences one batched decode launch can serve
@@ -139,9 +141,30 @@ struct GemmParams {
 };
 constexpr int GEMM_TILE = 128;       // tokens and rows per gemm3 workgroup
 constexpr int GEMM_MIN_TOKENS = 16;  // batches from this size take the GEMM
-hipError_t launch_proj_gemm(const GemmWeightParams &W, const GemmActParams &X, const GemmParams &G,
+// prep_weights = false: W's planes already hold the rows (built earlier and kept by the caller)
+hipError_t launch_proj_gemm(const GemmWeightParams &W, const GemmActParams &X, const GemmParams &G, bool prep_weights,
                             hipStream_t stream);
 int matvec_row_multiple(int k);  // n_rows of a matvec launch must be a multiple of this
+
+// A projection's weight planes kept by a caller that runs many batches through the same weights
+// (the model's layer-major prefill): one device block of planes_bytes(N, K) holding wh, wl
+// [N][K] and fexp [N], built once with build_*_planes; the *_rows projections given them skip
+// their per-call weight prep (the planes are the same bits that prep would write).
+struct WeightPlanes {
+    _Float16 *wh = nullptr, *wl = nullptr;
+    int *fexp = nullptr;
+};
+size_t planes_bytes(int N, int K);
+WeightPlanes planes_at(void *mem, int N, int K);
+void build_qkv_planes(const flint_weight *wq, const flint_weight *wk, const flint_weight *wv, const WeightPlanes &pl,
+                      hipStream_t stream);
+void build_o_planes(const flint_weight *wo, const WeightPlanes &pl, hipStream_t stream);
+// flint_attn_qkv_proj_rows / flint_attn_o_proj_rows with the weights' planes (pl may be null)
+void qkv_proj_rows_planes(const flint_weight *wq, const flint_weight *wk, const flint_weight *wv, const float *x,
+                          int n_tok, const float *attn_norm, float eps, float *qkv, int qkv_stride,
+                          const WeightPlanes *pl, hipStream_t stream);
+void o_proj_rows_planes(const flint_weight *wo, const float *att, int n_tok, float *x, const WeightPlanes *pl,
+                        hipStream_t stream);
 
 }  // namespace flint
 

@@ -16,6 +16,7 @@
 #include <memory>
 #include <stdexcept>
 #include <string>
+#include <utility>
 #include <vector>
 
 #include "../../include/capi.h"
@@ -156,12 +157,39 @@ struct flint_attn_model {
     float *qkv = nullptr, *att = nullptr;
     int cap = 0;
     int32_t n_ctx = 0, pos = 0;  // the session: context length and tokens processed
+    // The prefill GEMMs' f16 hi/lo planes of every layer's q|k|v and o weights (75.5 MB a layer),
+    // one allocation made at the first prefill block that takes the GEMM; a layer's planes are built
+    // on the stream of its first such block and read by every later one.
+    void *planes = nullptr;
+    std::vector<uint8_t> planes_built;
 
     ~flint_attn_model() {
         flint_attn_engine_destroy(eng);
         if (wmem) (void)hipFree(wmem);
         if (qkv) (void)hipFree(qkv);
         if (att) (void)hipFree(att);
+        if (planes) (void)hipFree(planes);
+    }
+    static size_t layer_planes_bytes() {
+        return planes_bytes(FLINT_QKV_DIM, FLINT_N_EMBD) + planes_bytes(FLINT_N_EMBD, FLINT_Q_DIM);
+    }
+    // the layer's q|k|v and o planes, built on `stream` if this is the first use
+    std::pair<WeightPlanes, WeightPlanes> layer_planes(int il, hipStream_t stream) {
+        if (!planes) {
+            check(hipMalloc(&planes, layers.size() * layer_planes_bytes()), "hipMalloc weight planes");
+            planes_built.assign(layers.size(), 0);
+        }
+        char *base = (char *)planes + (size_t)il * layer_planes_bytes();
+        const WeightPlanes pq = planes_at(base, FLINT_QKV_DIM, FLINT_N_EMBD);
+        const WeightPlanes po =
+            planes_at(base + planes_bytes(FLINT_QKV_DIM, FLINT_N_EMBD), FLINT_N_EMBD, FLINT_Q_DIM);
+        if (!planes_built[il]) {
+            const Layer &L = layers[il];
+            build_qkv_planes(&L.q, &L.k, &L.v, pq, stream);
+            build_o_planes(&L.o, po, stream);
+            planes_built[il] = 1;
+        }
+        return {pq, po};
     }
     void reserve(int n_tok) {
         if (n_tok <= cap) return;
@@ -315,6 +343,16 @@ int32_t flint_attn_model_block_prefill(flint_attn_model *m, int32_t il, float *X
         m->reserve(T);
         float *a = att ? att : m->att;
         char e2[512] = {0};
+        const hipStream_t s = (hipStream_t)stream;
+        if (T >= GEMM_MIN_TOKENS) {
+            // the projections' GEMMs read the layer's cached weight planes
+            const auto pl = m->layer_planes(il, s);
+            qkv_proj_rows_planes(&L.q, &L.k, &L.v, X, T, L.attn_norm, m->hp.h.rms_eps, m->qkv, FLINT_QKV_DIM, &pl.first,
+                                 s);
+            call(flint_attn_engine_prefill(m->eng, il, m->qkv, p0, T, a, stream, e2, sizeof(e2)), e2);
+            o_proj_rows_planes(&L.o, a, T, X, &pl.second, s);
+            return;
+        }
         call(flint_attn_qkv_proj_rows(&L.q, &L.k, &L.v, X, T, L.attn_norm, m->hp.h.rms_eps, m->qkv, FLINT_QKV_DIM,
                                       stream, e2, sizeof(e2)),
              e2);

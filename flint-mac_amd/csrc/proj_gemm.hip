@@ -291,16 +291,17 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemm3_kernel(const GemmParams P
     }
 }
 
-hipError_t launch_proj_gemm(const GemmWeightParams &W, const GemmActParams &X, const GemmParams &G,
+hipError_t launch_proj_gemm(const GemmWeightParams &W, const GemmActParams &X, const GemmParams &G, bool prep_weights,
                             hipStream_t stream) {
     if (G.K == 2048) {
-        hipLaunchKernelGGL(wprep_kernel<2048>, dim3(G.N), dim3(64), 0, stream, W);
-        hipLaunchKernelGGL(xprep_kernel<2048>, dim3(X.T_pad), dim3(256), 0, stream, X);
+        if (prep_weights) hipLaunchKernelGGL(wprep_kernel<2048>, dim3(G.N), dim3(64), 0, stream, W);
+        if (X.T_pad > 0) hipLaunchKernelGGL(xprep_kernel<2048>, dim3(X.T_pad), dim3(256), 0, stream, X);
     } else {
-        hipLaunchKernelGGL(wprep_kernel<4096>, dim3(G.N), dim3(64), 0, stream, W);
-        hipLaunchKernelGGL(xprep_kernel<4096>, dim3(X.T_pad), dim3(256), 0, stream, X);
+        if (prep_weights) hipLaunchKernelGGL(wprep_kernel<4096>, dim3(G.N), dim3(64), 0, stream, W);
+        if (X.T_pad > 0) hipLaunchKernelGGL(xprep_kernel<4096>, dim3(X.T_pad), dim3(256), 0, stream, X);
     }
-    hipLaunchKernelGGL(gemm3_kernel, dim3(G.N / GM_TILE * (X.T_pad / GM_TILE)), dim3(GM_THREADS), 0, stream, G);
+    if (X.T_pad > 0)
+        hipLaunchKernelGGL(gemm3_kernel, dim3(G.N / GM_TILE * (X.T_pad / GM_TILE)), dim3(GM_THREADS), 0, stream, G);
     return hipGetLastError();
 }
 
