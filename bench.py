@@ -505,7 +505,7 @@ def main():
                          "frac": round(d["bytes_per_launch"] / (t_full * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                          "traffic": DECODE_TRAFFIC_BYTES,
                          "kernel": "one flint_attn_decode call = attn_decode_kernel<1, 1> (f16 KV, no V slices; 43 key "
-                                   "splits x 4 kv heads = 172 workgroups) + attn_combine_kernel (split merge); "
+                                   "splits x 4 kv heads = 172 workgroups) + attn_combine_kernel<4> (split merge, 128 workgroups); "
                                    "time per call from HIP events",
                          "bytes_per_launch": d["bytes_per_launch"], "host_bound": d["host_bound"]},
         })

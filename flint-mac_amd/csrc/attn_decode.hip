@@ -405,26 +405,42 @@ __global__ __launch_bounds__(DEC_THREADS) void attn_decode_kernel(const DecodePa
     if (lane == 0) *(float2 *)(pp + HEAD_DIM) = make_float2(M, L);
 }
 
+// The merge kernel's arguments: only what it reads (536 bytes instead of the decode kernel's
+// 1.3 KB), since a dependent launch waits for its argument block.
+struct CombineParams {
+    const float *partial, *sinks;
+    float *att;
+    int n_split[MAX_SEQ];  // key splits of sequence s
+    int split0[MAX_SEQ];   // first split record of sequence s
+};
+
 // LSE merge of the split partials plus the sink (fused.metal:331-350).
-// grid = (N_HEAD, n_seq), 256 threads. Thread (dim group dg, split group sg) sums
-// dims 4dg..4dg+3 over splits sg, sg+8, ...; thread t also holds (m, l) of splits
-// t, t+256, ... All of it is requested at once, so the merge waits on one memory
-// round trip after the kernel arguments.
-__global__ __launch_bounds__(256) void attn_combine_kernel(const DecodeParams P) {
+// grid = (N_HEAD * DP, n_seq), 256 threads: workgroup (head hh, part qd) writes the 128/DP dims
+// from (128/DP)qd of head hh. Thread (split group sg, dim group dg) sums 4 of them over splits
+// sg, sg + SG, ...; thread t also holds (m, l) of splits t, t+256, ... All of it is requested at
+// once, so the merge waits on one memory round trip after the kernel arguments. With few
+// sequences, DP = 4 spreads the partial records' reads over 4x the CUs (one CU reads ~63 GB/s).
+template <int DP>
+__global__ __launch_bounds__(256) void attn_combine_kernel(const CombineParams P) {
+    constexpr int DG = HEAD_DIM / DP / 4;  // dim groups of 4
+    constexpr int SG = 256 / DG;           // split groups
+    constexpr int NX = 64 / SG;            // accumulators per thread per 64 splits
     __shared__ float w_s[MERGE_MAX_SPLIT];
     __shared__ float red[2][4];
-    __shared__ float4 part[8][32];
-    const int hh = blockIdx.x, seq = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int ns = P.n_split[seq], split0 = P.wg_base[seq] / N_HEAD_KV;
+    __shared__ float4 part[4][DG];
+    const int hh = blockIdx.x / DP, qd = blockIdx.x % DP, seq = blockIdx.y, tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int ns = P.n_split[seq], split0 = P.split0[seq];
     const float *const partial = P.partial, *const sinks = P.sinks;
     float *const att = P.att;
     pin_sgpr(ns), pin_sgpr(split0), pin_sgpr(partial), pin_sgpr(sinks), pin_sgpr(att);
     if (ns <= 1) return;  // written directly by the decode kernel
     const float *pp = partial + ((size_t)split0 * N_HEAD + hh * ns) * PART_STRIDE;
-    const int dg = tid & 31, sg = tid >> 5;
-    float4 x[8];
+    const int dg = tid % DG, sg = tid / DG;
+    const float *px = pp + (HEAD_DIM / DP) * qd + 4 * dg;
+    float4 x[NX];
 #pragma unroll
-    for (int i = 0; i < 8; i++) x[i] = *(const float4 *)(pp + min(sg + 8 * i, ns - 1) * PART_STRIDE + 4 * dg);
+    for (int i = 0; i < NX; i++) x[i] = *(const float4 *)(px + min(sg + SG * i, ns - 1) * PART_STRIDE);
     float2 ml[MERGE_MAX_SPLIT / 256];
 #pragma unroll
     for (int j = 0; j < MERGE_MAX_SPLIT / 256; j++)
@@ -454,27 +470,33 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const DecodeParams P)
     for (int s0 = 0; s0 < ns; s0 += 64) {
         if (s0 > 0) {
 #pragma unroll
-            for (int i = 0; i < 8; i++)
-                x[i] = *(const float4 *)(pp + min(s0 + sg + 8 * i, ns - 1) * PART_STRIDE + 4 * dg);
+            for (int i = 0; i < NX; i++)
+                x[i] = *(const float4 *)(px + min(s0 + sg + SG * i, ns - 1) * PART_STRIDE);
         }
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int sp = s0 + sg + 8 * i;
+        for (int i = 0; i < NX; i++) {
+            const int sp = s0 + sg + SG * i;
             const float w = sp < ns ? w_s[sp] : 0.f;
             a.x += x[i].x * w; a.y += x[i].y * w; a.z += x[i].z * w; a.w += x[i].w * w;
         }
     }
-    part[sg][dg] = a;
-    __syncthreads();
-    if (sg == 0) {
-        float4 t = part[0][dg];
+    // sum over the wave's split groups (lanes DG apart), then over the 4 waves
 #pragma unroll
-        for (int i = 1; i < 8; i++) {
-            const float4 u = part[i][dg];
+    for (int o = DG; o < 64; o <<= 1) {
+        a.x += __shfl_xor(a.x, o, 64); a.y += __shfl_xor(a.y, o, 64);
+        a.z += __shfl_xor(a.z, o, 64); a.w += __shfl_xor(a.w, o, 64);
+    }
+    if (lane < DG) part[wave][lane] = a;
+    __syncthreads();
+    if (tid < DG) {
+        float4 t = part[0][tid];
+#pragma unroll
+        for (int i = 1; i < 4; i++) {
+            const float4 u = part[i][tid];
             t.x += u.x; t.y += u.y; t.z += u.z; t.w += u.w;
         }
         const float inv = 1.0f / L;
-        *(float4 *)(att + (size_t)seq * Q_DIM + hh * HEAD_DIM + 4 * dg) =
+        *(float4 *)(att + (size_t)seq * Q_DIM + hh * HEAD_DIM + (HEAD_DIM / DP) * qd + 4 * tid) =
             make_float4(t.x * inv, t.y * inv, t.z * inv, t.w * inv);
     }
 }
@@ -521,7 +543,19 @@ hipError_t launch_decode(const DecodeParams &P, int dtype, hipStream_t stream) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (P.max_split > 1) {
-        hipLaunchKernelGGL(attn_combine_kernel, dim3(N_HEAD, P.n_seq), dim3(256), 0, stream, P);
+        CombineParams C;
+        C.partial = P.partial;
+        C.sinks = P.sinks;
+        C.att = P.att;
+        for (int s = 0; s < MAX_SEQ; s++) {
+            C.n_split[s] = s < P.n_seq ? P.n_split[s] : 0;
+            C.split0[s] = s < P.n_seq ? P.wg_base[s] / N_HEAD_KV : 0;
+        }
+        // four workgroups per head while that keeps the grid within two per CU
+        if (P.n_seq * N_HEAD * 4 <= 512)
+            hipLaunchKernelGGL(attn_combine_kernel<4>, dim3(N_HEAD * 4, P.n_seq), dim3(256), 0, stream, C);
+        else
+            hipLaunchKernelGGL(attn_combine_kernel<1>, dim3(N_HEAD, P.n_seq), dim3(256), 0, stream, C);
         e = hipGetLastError();
     }
     return e;
