@@ -16,10 +16,12 @@ Also on the same line:
     attention): one layer of each kind, a whole decode step at 32k, and the layer-major
     prefill of 4000 tokens (flint_attn_model_prefill);
   * the CPU oracle on every core of this host (cpu_baseline; a reported baseline, not the
-    target): config-3 decode GB/s and config-4 prefill TFLOPS.
+    target): config-3 decode GB/s and config-4 prefill TFLOPS;
+  * what this GPU itself reaches, measured in the same run (measured_limits): a plain 64 MiB
+    streaming read, the f16 MFMA rate, and the GPU time of an empty and of a dependent launch.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-                       [--only decode|prefill|prefill_full|prefill_swa|config5|model]
+                       [--only decode|prefill|prefill_full|prefill_swa|config5|model|roofline]
 """
 import argparse
 import json
@@ -92,6 +94,91 @@ def queued_launch_ms(torch, step, reps, warmup=2):
     host_bound = e_spin.query()  # the spin already finished: the GPU waited for the host
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / reps, bool(host_bound)
+
+
+def bench_roofline(torch):
+    """What this GPU itself reaches, measured in the same run with the kernels of
+    flint-mac_amd/libflint_probe.so (a measurement library outside the attention library):
+      * a plain 64 MiB streaming read (16-byte non-temporal loads, one contiguous range per
+        workgroup, two sets of 4, 8 or 12 loads per thread refilled as they are consumed; the
+        best is reported) over 8 rotating buffers (512 MiB, beyond the 256 MB Infinity Cache), at
+        1024 workgroups and at the config-3 decode's 172;
+      * v_mfma_f32_32x32x16_f16 in 4 or 8 independent chains per wave, 8 waves per workgroup
+        (two per SIMD), one and four workgroups per CU (the best is reported);
+      * the GPU time per launch of an empty kernel, and of a tiny kernel that reads what the
+        launch before it wrote (the dependency of a split merge on the kernel before it).
+    Each is timed with HIP events around launches queued behind a spin kernel."""
+    import ctypes
+    path = os.path.join(ROOT, "flint-mac_amd", "libflint_probe.so")
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is missing: build with `make -C flint-mac_amd`")
+    P = ctypes.CDLL(path)
+    vp, i32, u64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_uint64
+    P.flint_probe_stream_read.argtypes = [vp, u64, i32, i32, vp, vp]
+    P.flint_probe_mfma.argtypes = [i32, i32, i32, vp, vp]
+    P.flint_probe_empty.argtypes = [vp]
+    P.flint_probe_chain.argtypes = [vp, vp, vp]
+    for f in (P.flint_probe_stream_read, P.flint_probe_mfma, P.flint_probe_empty, P.flint_probe_chain):
+        f.restype = i32
+
+    def ok(rc, what):
+        if rc != 0:
+            raise RuntimeError(f"{what} failed: {rc}")
+
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    nbytes = 64 << 20
+    bufs = [torch.randint(0, 255, (nbytes,), dtype=torch.uint8, device="cuda") for _ in range(8)]
+    sink = torch.zeros(65536, dtype=torch.float32, device="cuda")
+    out = {}
+    for n_wg in (1024, 172):
+        per = nbytes // (16 * n_wg) * 16 * n_wg  # whole 16-byte units per workgroup
+        best = None
+        for depth in (4, 8, 12):
+            it = [0]
+
+            def step(n_wg=n_wg, per=per, depth=depth, it=it):
+                b = bufs[it[0] % 8]
+                it[0] += 1
+                ok(P.flint_probe_stream_read(ctypes.c_void_p(b.data_ptr()), per, n_wg, depth,
+                                             ctypes.c_void_p(sink.data_ptr()), stream), "stream read")
+            ms, hb = queued_launch_ms(torch, step, 80, warmup=8)
+            r = {"us_per_64mib": round(ms * 1e3 * nbytes / per, 3), "gbs": round(per / (ms * 1e-3) / 1e9, 1),
+                 "loads_per_set": depth, "host_bound": hb}
+            log(f"stream read {n_wg} workgroups: {r}")
+            if best is None or r["gbs"] > best["gbs"]:
+                best = r
+        out[f"stream_read_{n_wg}wg"] = best
+    best = None
+    # (workgroups, independent chains per wave, iterations): one and four workgroups per CU
+    for n_wg, chains, iters in ((256, 4, 2000), (256, 8, 1000), (1024, 4, 500)):
+        flops = n_wg * 8 * iters * chains * 32768
+
+        def mstep(n_wg=n_wg, chains=chains, iters=iters):
+            ok(P.flint_probe_mfma(n_wg, iters, chains, ctypes.c_void_p(sink.data_ptr()), stream), "mfma")
+        ms, hb = queued_launch_ms(torch, mstep, 8, warmup=2)
+        r = {"tflops": round(flops / (ms * 1e-3) / 1e12, 1), "ms": round(ms, 4), "workgroups": n_wg,
+             "chains_per_wave": chains, "flops_per_launch": flops, "host_bound": hb}
+        log(f"mfma: {r}")
+        if best is None or r["tflops"] > best["tflops"]:
+            best = r
+    out["mfma_f16_32x32x16"] = best
+
+    def estep():
+        ok(P.flint_probe_empty(stream), "empty")
+    ms, hb = queued_launch_ms(torch, estep, 400, warmup=20)
+    out["empty_launch_us"] = round(ms * 1e3, 3)
+    a = torch.zeros(4096, dtype=torch.float32, device="cuda")
+    b = torch.zeros(4096, dtype=torch.float32, device="cuda")
+    flip = [0]
+
+    def cstep():
+        x, y = (a, b) if flip[0] % 2 == 0 else (b, a)
+        flip[0] += 1
+        ok(P.flint_probe_chain(ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(y.data_ptr()), stream), "chain")
+    ms, hb = queued_launch_ms(torch, cstep, 400, warmup=20)
+    out["dependent_launch_us"] = round(ms * 1e3, 3)
+    del bufs
+    return out
 
 
 def decode_bytes(n_keys):
@@ -431,8 +518,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["decode", "prefill", "prefill_full", "prefill_swa", "config5", "model"],
-                    default=None)
+    ap.add_argument("--only", choices=["decode", "prefill", "prefill_full", "prefill_swa", "config5", "model",
+                                       "roofline"], default=None)
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build runs on one GPU. The attention path would shard by key range (decode, "
@@ -445,6 +532,10 @@ def main():
     fa.lib()
     assert torch.cuda.is_available(), "bench needs a GPU"
     res = {}
+    if args.only in (None, "roofline"):
+        log("measured limits of this GPU (libflint_probe.so)")
+        res["roofline"] = bench_roofline(torch)
+        log(f"measured: {res['roofline']}")
     if args.only in (None, "decode"):
         log("decode 32k (config 3)")
         res["decode"] = bench_decode_32k(torch, fa, args.steps, args.warmup)
@@ -516,6 +607,8 @@ def main():
         c = res["config5"]
         line["config5_16seq_48layers"] = {"ms_per_step": round(c["ms_per_step"], 4), "tok_s": round(c["tok_s"], 1),
                                           "gbs": round(c["gbs"], 1), "bytes_per_step": c["bytes_per_step"]}
+    if "roofline" in res:
+        line["measured_limits"] = res["roofline"]
     if "model" in res:
         line["attention_blocks_q8_0_49_layers"] = {k: (round(v, 5) if isinstance(v, float) else v)
                                                    for k, v in res["model"].items()}

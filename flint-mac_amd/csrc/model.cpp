@@ -16,7 +16,6 @@
 #include <memory>
 #include <stdexcept>
 #include <string>
-#include <utility>
 #include <vector>
 
 #include "../../include/capi.h"
@@ -161,6 +160,7 @@ struct flint_attn_model {
     // one allocation made at the first prefill block that takes the GEMM; a layer's planes are built
     // on the stream of its first such block and read by every later one.
     void *planes = nullptr;
+    bool planes_failed = false;  // the allocation failed once: prefill rebuilds them per call instead
     std::vector<uint8_t> planes_built;
 
     ~flint_attn_model() {
@@ -173,10 +173,17 @@ struct flint_attn_model {
     static size_t layer_planes_bytes() {
         return planes_bytes(FLINT_QKV_DIM, FLINT_N_EMBD) + planes_bytes(FLINT_N_EMBD, FLINT_Q_DIM);
     }
-    // the layer's q|k|v and o planes, built on `stream` if this is the first use
-    std::pair<WeightPlanes, WeightPlanes> layer_planes(int il, hipStream_t stream) {
+    // the layer's q|k|v and o planes, built on `stream` if this is the first use; false when
+    // there is no memory for them
+    bool layer_planes(int il, hipStream_t stream, WeightPlanes *pq_out, WeightPlanes *po_out) {
+        if (planes_failed) return false;
         if (!planes) {
-            check(hipMalloc(&planes, layers.size() * layer_planes_bytes()), "hipMalloc weight planes");
+            if (hipMalloc(&planes, layers.size() * layer_planes_bytes()) != hipSuccess) {
+                (void)hipGetLastError();  // clear the allocation error; the projections work without planes
+                planes = nullptr;
+                planes_failed = true;
+                return false;
+            }
             planes_built.assign(layers.size(), 0);
         }
         char *base = (char *)planes + (size_t)il * layer_planes_bytes();
@@ -189,7 +196,9 @@ struct flint_attn_model {
             build_o_planes(&L.o, po, stream);
             planes_built[il] = 1;
         }
-        return {pq, po};
+        *pq_out = pq;
+        *po_out = po;
+        return true;
     }
     void reserve(int n_tok) {
         if (n_tok <= cap) return;
@@ -344,13 +353,12 @@ int32_t flint_attn_model_block_prefill(flint_attn_model *m, int32_t il, float *X
         float *a = att ? att : m->att;
         char e2[512] = {0};
         const hipStream_t s = (hipStream_t)stream;
-        if (T >= GEMM_MIN_TOKENS) {
+        WeightPlanes pq, po;
+        if (T >= GEMM_MIN_TOKENS && m->layer_planes(il, s, &pq, &po)) {
             // the projections' GEMMs read the layer's cached weight planes
-            const auto pl = m->layer_planes(il, s);
-            qkv_proj_rows_planes(&L.q, &L.k, &L.v, X, T, L.attn_norm, m->hp.h.rms_eps, m->qkv, FLINT_QKV_DIM, &pl.first,
-                                 s);
+            qkv_proj_rows_planes(&L.q, &L.k, &L.v, X, T, L.attn_norm, m->hp.h.rms_eps, m->qkv, FLINT_QKV_DIM, &pq, s);
             call(flint_attn_engine_prefill(m->eng, il, m->qkv, p0, T, a, stream, e2, sizeof(e2)), e2);
-            o_proj_rows_planes(&L.o, a, T, X, &pl.second, s);
+            o_proj_rows_planes(&L.o, a, T, X, &po, s);
             return;
         }
         call(flint_attn_qkv_proj_rows(&L.q, &L.k, &L.v, X, T, L.attn_norm, m->hp.h.rms_eps, m->qkv, FLINT_QKV_DIM,
