@@ -22,6 +22,19 @@ def test_library_exports_every_header_function():
     assert set(names) <= exported
 
 
+def test_probe_library_exports_its_entry_points():
+    """bench.py's measurement library (streaming read, MFMA rate, launch cost) is built beside the
+    attention library and exports the four functions bench_roofline binds; it is not part of the
+    attention library's C ABI."""
+    path = os.path.join(os.path.dirname(fa.LIB_PATH), "libflint_probe.so")
+    assert os.path.exists(path), "build with make -C flint-mac_amd"
+    nm = subprocess.run(["nm", "-D", "--defined-only", path], capture_output=True, text=True).stdout
+    exported = {line.split()[-1] for line in nm.splitlines() if " T " in line}
+    assert {"flint_probe_stream_read", "flint_probe_mfma", "flint_probe_empty", "flint_probe_chain"} <= exported
+    attn = subprocess.run(["nm", "-D", "--defined-only", fa.LIB_PATH], capture_output=True, text=True).stdout
+    assert "flint_probe_" not in attn
+
+
 # The Rust server's bindings, as declared at /root/reference/server/src/ffi.rs:5-11 (the
 # #[repr(C)] config) and :19-29 (the extern "C" block), kept here as text.
 RUST_FFI = """
