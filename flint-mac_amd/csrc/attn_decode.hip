@@ -415,7 +415,7 @@ struct CombineParams {
 };
 
 // LSE merge of the split partials plus the sink (fused.metal:331-350).
-// grid = (N_HEAD * DP, n_seq), 256 threads: workgroup (head hh, part qd) writes the 128/DP dims
+// grid = (N_HEAD * DP, n_seq), 256 threads: workgroup (part qd, head hh) writes the 128/DP dims
 // from (128/DP)qd of head hh. Thread (split group sg, dim group dg) sums 4 of them over splits
 // sg, sg + SG, ...; thread t also holds (m, l) of splits t, t+256, ... All of it is requested at
 // once, so the merge waits on one memory round trip after the kernel arguments. With few
@@ -428,7 +428,9 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const CombineParams P
     __shared__ float w_s[MERGE_MAX_SPLIT];
     __shared__ float red[2][4];
     __shared__ float4 part[4][DG];
-    const int hh = blockIdx.x / DP, qd = blockIdx.x % DP, seq = blockIdx.y, tid = threadIdx.x;
+    // head fastest: the DP workgroups of a head are N_HEAD ids apart, so on one XCD (the hardware
+    // deals workgroup ids to the 8 XCDs round robin) and its L2 fetches the head's records once
+    const int hh = blockIdx.x % N_HEAD, qd = blockIdx.x / N_HEAD, seq = blockIdx.y, tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int ns = P.n_split[seq], split0 = P.split0[seq];
     const float *const partial = P.partial, *const sinks = P.sinks;
