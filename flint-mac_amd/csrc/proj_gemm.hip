@@ -13,8 +13,9 @@
 //   * the GEMM accumulates hi*hi + hi*lo + lo*hi in fp32 (the lo*lo term is below 2^-22 of
 //     the product) and scales each output by 2^(e_t + f_n), which is exact.
 // Three launches: wprep (weights -> planes), xprep (activations -> planes, the RMSNorm fused
-// for q/k/v) and gemm3. The weight planes are rebuilt each call from the GGUF rows (~25 us for
-// a layer's 19M weights), so nothing is cached across calls.
+// for q/k/v) and gemm3. The stage-level calls rebuild the weight planes from the GGUF rows each
+// time (~20 us for a layer's 19M weights); a model keeps every layer's planes after building
+// them once, and its calls launch only xprep and gemm3.
 #include "common.h"
 #include "dequant.h"
 #include "flint_attn_internal.h"
