@@ -38,13 +38,24 @@ __device__ inline void split_store(float v, int e, _Float16 *hi, _Float16 *lo) {
     *lo = (_Float16)(s - (float)h);
 }
 
+// Planes are stored in the order gemm3 keeps them in LDS, so that a workgroup's chunk of a plane
+// (128 rows x 32 k) is one contiguous 8 KiB block that it copies into LDS unchanged: blocks
+// [row tile n >> 7][chunk k >> 5], and in a block the 16-byte unit of row r (n & 127), k group
+// k8 ((k >> 3) & 3) at unit ((r >> 5) * 2 + (k8 >> 1)) * 64 + (r & 31) + 32 (k8 & 1). The element
+// offset of the unit that holds elements 8 g .. 8 g + 7 of row n:
+__device__ inline size_t plane_unit(int n, int g, int K) {
+    const int r = n & 127, k8 = g & 3;
+    const int q = ((r >> 5) * 2 + (k8 >> 1)) * 64 + (r & 31) + 32 * (k8 & 1);
+    return (((size_t)(n >> 7) * (K / 32) + (g >> 2)) * 512 + q) * 8;
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------------------
 // wprep: one wave per weight row: the row's bytes staged through LDS (2-byte copies: q8_0 and
 // q6_K blocks are only 2-byte aligned), dequantised 32 elements per lane per sub-block (lane l
 // owns sub-blocks l, l + 64, ...), the row's exponent from its largest magnitude, then the
-// hi/lo planes ([n][K] f16, row-major) and f_n.
+// hi/lo planes (in gemm3's chunk order) and f_n.
 constexpr int WP_MAX_K = 4096;
 constexpr int WP_STAGE = WP_MAX_K / 32 * 34;  // largest quantised row of the batch (q8_0)
 template <int K>
@@ -68,10 +79,9 @@ __global__ __launch_bounds__(64) void wprep_kernel(const GemmWeightParams P) {
         for (int e = 0; e < 32; e++) mx = fmaxf(mx, fabsf(w[i][e]));
     }
     const int f = row_exp(wave_max(mx));
-    _Float16 *hi = P.wh + (size_t)n * K, *lo = P.wl + (size_t)n * K;
 #pragma unroll
     for (int i = 0; i < SUBS; i++) {
-        const int k0 = 32 * (lane + 64 * i);
+        const int g0 = 4 * (lane + 64 * i);  // 8-element groups of this sub-block
         f16x8 h8[4], l8[4];
 #pragma unroll
         for (int e = 0; e < 32; e++) {
@@ -82,8 +92,9 @@ __global__ __launch_bounds__(64) void wprep_kernel(const GemmWeightParams P) {
         }
 #pragma unroll
         for (int q = 0; q < 4; q++) {
-            *(f16x8 *)(hi + k0 + 8 * q) = h8[q];
-            *(f16x8 *)(lo + k0 + 8 * q) = l8[q];
+            const size_t o = plane_unit(n, g0 + q, K);
+            *(f16x8 *)(P.wh + o) = h8[q];
+            *(f16x8 *)(P.wl + o) = l8[q];
         }
     }
     if (lane == 0) P.fexp[n] = f;
@@ -93,7 +104,7 @@ __global__ __launch_bounds__(64) void wprep_kernel(const GemmWeightParams P) {
 // xprep: one 256-thread workgroup per activation row t (rows T .. T_pad - 1 are written as
 // zeros): the RMSNorm exactly as matvec_kernel computes it when gains are given (double sum
 // of squares per thread over XPT consecutive elements, then across lanes and waves in a fixed
-// order; xn = (x * scale) * g), the row's exponent, then the hi/lo planes ([t][K] f16).
+// order; xn = (x * scale) * g), the row's exponent, then the hi/lo planes (gemm3's chunk order).
 template <int K>
 __global__ __launch_bounds__(256) void xprep_kernel(const GemmActParams P) {
     constexpr int XPT = K / 256;
@@ -134,7 +145,6 @@ __global__ __launch_bounds__(256) void xprep_kernel(const GemmActParams P) {
     if (lane == 0) red[wave] = mx;
     __syncthreads();
     const int e = row_exp(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
-    _Float16 *hi = P.xh + (size_t)t * K + XPT * tid, *lo = P.xl + (size_t)t * K + XPT * tid;
 #pragma unroll
     for (int k = 0; k < XPT / 8; k++) {
         f16x8 h8, l8;
@@ -145,8 +155,9 @@ __global__ __launch_bounds__(256) void xprep_kernel(const GemmActParams P) {
             h8[j] = h;
             l8[j] = l;
         }
-        *(f16x8 *)(hi + 8 * k) = h8;
-        *(f16x8 *)(lo + 8 * k) = l8;
+        const size_t o = plane_unit(t, XPT * tid / 8 + k, K);
+        *(f16x8 *)(P.xh + o) = h8;
+        *(f16x8 *)(P.xl + o) = l8;
     }
     if (tid == 0) P.eexp[t] = e;
 }
@@ -157,8 +168,10 @@ __global__ __launch_bounds__(256) void xprep_kernel(const GemmActParams P) {
 // chunk of each operand (hi and lo planes, 128 rows x 32 k) goes into LDS in the MFMA operand
 // order: per plane, 32-row block and k-step, 1 KiB in which lane l's 16 bytes hold row l & 31,
 // k 8 (l >> 5) .. +7 (the same order for the weight rows, operand A, and for the tokens,
-// operand B), so every fragment read is one conflict-free ds_read_b128 per lane. While a chunk
-// is computed from LDS, the next one is stored there and the two after it are in flight.
+// operand B), so every fragment read is one conflict-free ds_read_b128 per lane. The planes
+// are stored in that order already (plane_unit), so the chunk's copy into LDS is contiguous on
+// both sides. While a chunk is computed from LDS, the next one is stored there and the two
+// after it are in flight.
 constexpr int GM_TILE = GEMM_TILE, GM_KC = 32, GM_THREADS = 256;
 constexpr int GM_PLANE_CHUNK = GM_TILE * GM_KC * 2;  // bytes of one plane's chunk (8 KiB)
 
@@ -183,17 +196,17 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemm3_kernel(const GemmParams P
     }
     const int n0 = nt * GM_TILE, t0 = tt * GM_TILE;
     const int K = P.K;
-    // global -> LDS: per plane, 512 units of 16 bytes (128 rows x 4 k8); thread tid takes units
-    // tid and tid + 256 (row u >> 2, k8 = u & 3: four threads read a row's 64 contiguous bytes)
+    // global -> LDS: a plane's chunk is 512 contiguous units of 16 bytes already in the LDS
+    // order (plane_unit); thread tid copies units tid and tid + 256, so a wave's load and its
+    // LDS store each cover 1 KiB contiguously (whole cache lines, no bank conflicts)
     const _Float16 *srcA[2] = {P.wh + (size_t)n0 * K, P.wl + (size_t)n0 * K};
     const _Float16 *srcB[2] = {P.xh + (size_t)t0 * K, P.xl + (size_t)t0 * K};
     int goff[2], loff[2];
 #pragma unroll
     for (int i = 0; i < 2; i++) {
-        const int u = tid + GM_THREADS * i, r = u >> 2, k8 = u & 3;
-        goff[i] = r * K + 8 * k8;
-        // LDS: block r >> 5, k-step k8 >> 1, lane slot (r & 31) + 32 (k8 & 1)
-        loff[i] = (((r >> 5) * 2 + (k8 >> 1)) * 64 + (r & 31) + 32 * (k8 & 1)) * 16;
+        const int u = tid + GM_THREADS * i;
+        goff[i] = 8 * u;
+        loff[i] = 16 * u;
     }
     // two register sets of loaded chunks, so two chunks are in flight while one is computed
     u32x4 ga[2][2][2], gb[2][2][2];  // [operand][plane][unit]
@@ -202,8 +215,8 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemm3_kernel(const GemmParams P
         for (int p = 0; p < 2; p++)
 #pragma unroll
             for (int i = 0; i < 2; i++) {
-                g[0][p][i] = *(const u32x4 *)(srcA[p] + goff[i] + kc);
-                g[1][p][i] = *(const u32x4 *)(srcB[p] + goff[i] + kc);
+                g[0][p][i] = *(const u32x4 *)(srcA[p] + goff[i] + (size_t)kc * GM_TILE);
+                g[1][p][i] = *(const u32x4 *)(srcB[p] + goff[i] + (size_t)kc * GM_TILE);
             }
     };
     auto lstore = [&](const u32x4 (&g)[2][2][2], int buf) {
@@ -294,6 +307,8 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemm3_kernel(const GemmParams P
 
 hipError_t launch_proj_gemm(const GemmWeightParams &W, const GemmActParams &X, const GemmParams &G, bool prep_weights,
                             hipStream_t stream) {
+    // the planes' chunk order and the GEMM's tiles need whole 128-row tiles of both operands
+    if (G.N % GM_TILE != 0 || X.T_pad % GM_TILE != 0 || (G.K != 2048 && G.K != 4096)) return hipErrorInvalidValue;
     if (G.K == 2048) {
         if (prep_weights) hipLaunchKernelGGL(wprep_kernel<2048>, dim3(G.N), dim3(64), 0, stream, W);
         if (X.T_pad > 0) hipLaunchKernelGGL(xprep_kernel<2048>, dim3(X.T_pad), dim3(256), 0, stream, X);
