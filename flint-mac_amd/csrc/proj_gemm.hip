@@ -101,65 +101,81 @@ __global__ __launch_bounds__(64) void wprep_kernel(const GemmWeightParams P) {
 }
 
 // ---------------------------------------------------------------------------
-// xprep: one 256-thread workgroup per activation row t (rows T .. T_pad - 1 are written as
-// zeros): the RMSNorm exactly as matvec_kernel computes it when gains are given (double sum
-// of squares per thread over XPT consecutive elements, then across lanes and waves in a fixed
-// order; xn = (x * scale) * g), the row's exponent, then the hi/lo planes (gemm3's chunk order).
+// xprep: one 512-thread workgroup per 8 activation rows t0 .. t0 + 7 (rows T .. T_pad - 1 are
+// written as zeros). Lane (row rho = lane & 7, group lane gl = lane >> 3) of wave w holds the
+// row's 8-element groups gl + 8 (w + 8 j) in registers, read once. The RMSNorm is computed as
+// matvec_kernel computes it (double sum of squares, float scale, xn = (x * scale) * g; the sum
+// runs in another order), then the row's exponent from the largest |xn|, then the hi/lo planes.
+// In the planes' chunk order the 8 rows' units of one group are one 128-byte line, so every
+// store instruction writes 8 whole lines.
 template <int K>
-__global__ __launch_bounds__(256) void xprep_kernel(const GemmActParams P) {
-    constexpr int XPT = K / 256;
-    __shared__ double part[4];
-    __shared__ float red[4];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, t = blockIdx.x;
-    float xv[XPT];
-    if (t < P.T) {
-        const float *xt = P.x + (size_t)t * P.x_stride + XPT * tid;
+__global__ __launch_bounds__(512) void xprep_kernel(const GemmActParams P) {
+    constexpr int GPJ = K / 8 / 64;  // groups per lane
+    __shared__ double red_ss[8][8];  // [wave][row]
+    __shared__ float red_mx[8][8];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, rho = lane & 7, gl = lane >> 3;
+    const int t = 8 * blockIdx.x + rho;
+    const bool live = t < P.T;
+    const float *xt = P.x + (size_t)(live ? t : 0) * P.x_stride;
+    float v[GPJ][8];
 #pragma unroll
-        for (int k = 0; k < XPT / 4; k++) {
-            const f32x4 v = *(const f32x4 *)(xt + 4 * k);
-            xv[4 * k] = v[0], xv[4 * k + 1] = v[1], xv[4 * k + 2] = v[2], xv[4 * k + 3] = v[3];
-        }
-    } else {
-#pragma unroll
-        for (int k = 0; k < XPT; k++) xv[k] = 0.f;
+    for (int j = 0; j < GPJ; j++) {
+        const int g = gl + 8 * (wave + 8 * j);
+        const f32x4 a = *(const f32x4 *)(xt + 8 * g), b = *(const f32x4 *)(xt + 8 * g + 4);
+        v[j][0] = a[0], v[j][1] = a[1], v[j][2] = a[2], v[j][3] = a[3];
+        v[j][4] = b[0], v[j][5] = b[1], v[j][6] = b[2], v[j][7] = b[3];
     }
     if (P.norm_w) {
         double ss = 0;
 #pragma unroll
-        for (int k = 0; k < XPT; k++) ss += (double)xv[k] * xv[k];
+        for (int j = 0; j < GPJ; j++)
 #pragma unroll
-        for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
-        if (lane == 0) part[wave] = ss;
+            for (int e = 0; e < 8; e++) ss += (double)v[j][e] * v[j][e];
+#pragma unroll
+        for (int m = 8; m < 64; m <<= 1) ss += __shfl_xor(ss, m, 64);
+        if (gl == 0) red_ss[wave][rho] = ss;
         __syncthreads();
         ss = 0;
 #pragma unroll
-        for (int w = 0; w < 4; w++) ss += part[w];
+        for (int w = 0; w < 8; w++) ss += red_ss[w][rho];
         const float scale = 1.0f / sqrtf((float)(ss / K) + P.eps);
 #pragma unroll
-        for (int k = 0; k < XPT; k++) xv[k] = xv[k] * scale * P.norm_w[XPT * tid + k];
+        for (int j = 0; j < GPJ; j++) {
+            const int g = gl + 8 * (wave + 8 * j);
+            const f32x4 a = *(const f32x4 *)(P.norm_w + 8 * g), b = *(const f32x4 *)(P.norm_w + 8 * g + 4);
+            const float gg[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+#pragma unroll
+            for (int e = 0; e < 8; e++) v[j][e] = v[j][e] * scale * gg[e];
+        }
     }
     float mx = 0.f;
 #pragma unroll
-    for (int k = 0; k < XPT; k++) mx = fmaxf(mx, fabsf(xv[k]));
-    mx = wave_max(mx);
-    if (lane == 0) red[wave] = mx;
-    __syncthreads();
-    const int e = row_exp(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
+    for (int j = 0; j < GPJ; j++)
 #pragma unroll
-    for (int k = 0; k < XPT / 8; k++) {
+        for (int e = 0; e < 8; e++) mx = fmaxf(mx, fabsf(v[j][e]));
+#pragma unroll
+    for (int m = 8; m < 64; m <<= 1) mx = fmaxf(mx, __shfl_xor(mx, m, 64));
+    if (gl == 0) red_mx[wave][rho] = mx;
+    __syncthreads();
+    mx = red_mx[0][rho];
+#pragma unroll
+    for (int w = 1; w < 8; w++) mx = fmaxf(mx, red_mx[w][rho]);
+    const int e = live ? row_exp(mx) : 0;
+#pragma unroll
+    for (int j = 0; j < GPJ; j++) {
         f16x8 h8, l8;
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
+        for (int i = 0; i < 8; i++) {
             _Float16 h, l;
-            split_store(xv[8 * k + j], e, &h, &l);
-            h8[j] = h;
-            l8[j] = l;
+            split_store(live ? v[j][i] : 0.f, e, &h, &l);
+            h8[i] = h;
+            l8[i] = l;
         }
-        const size_t o = plane_unit(t, XPT * tid / 8 + k, K);
+        const size_t o = plane_unit(t, gl + 8 * (wave + 8 * j), K);
         *(f16x8 *)(P.xh + o) = h8;
         *(f16x8 *)(P.xl + o) = l8;
     }
-    if (tid == 0) P.eexp[t] = e;
+    if (tid < 8) P.eexp[t] = e;  // lanes 0..7 of wave 0: rows rho = tid
 }
 
 // ---------------------------------------------------------------------------
@@ -311,10 +327,10 @@ hipError_t launch_proj_gemm(const GemmWeightParams &W, const GemmActParams &X, c
     if (G.N % GM_TILE != 0 || X.T_pad % GM_TILE != 0 || (G.K != 2048 && G.K != 4096)) return hipErrorInvalidValue;
     if (G.K == 2048) {
         if (prep_weights) hipLaunchKernelGGL(wprep_kernel<2048>, dim3(G.N), dim3(64), 0, stream, W);
-        if (X.T_pad > 0) hipLaunchKernelGGL(xprep_kernel<2048>, dim3(X.T_pad), dim3(256), 0, stream, X);
+        if (X.T_pad > 0) hipLaunchKernelGGL(xprep_kernel<2048>, dim3(X.T_pad / 8), dim3(512), 0, stream, X);
     } else {
         if (prep_weights) hipLaunchKernelGGL(wprep_kernel<4096>, dim3(G.N), dim3(64), 0, stream, W);
-        if (X.T_pad > 0) hipLaunchKernelGGL(xprep_kernel<4096>, dim3(X.T_pad), dim3(256), 0, stream, X);
+        if (X.T_pad > 0) hipLaunchKernelGGL(xprep_kernel<4096>, dim3(X.T_pad / 8), dim3(512), 0, stream, X);
     }
     if (X.T_pad > 0)
         hipLaunchKernelGGL(gemm3_kernel, dim3(G.N / GM_TILE * (X.T_pad / GM_TILE)), dim3(GM_THREADS), 0, stream, G);
