@@ -178,17 +178,19 @@ def test_decode_batch_matches_single(cuda, is_swa):
         np.testing.assert_allclose(got[s], one.cpu().numpy(), rtol=0, atol=1e-5)
 
 
-def test_decode_batch_long_contexts_auto_split(cuda):
+@pytest.mark.parametrize("positions", [[4100, 17000, 40000, 65535, 700], [9000, 33000, 700]],
+                         ids=["5seq", "3seq"])
+def test_decode_batch_long_contexts_auto_split(cuda, positions):
     """Config-5 shape: independent sequences at long, mixed contexts in one launch, with the
     automatic split plan (each sequence's key range cut into its own number of equal splits,
     so the sequences differ in split count and split length up to the grid's width; a
     sequence with one split is written directly by the decode kernel). Every sequence equals
-    the oracle."""
-    _say("decode batch, long mixed contexts, auto split")
+    the oracle. Up to four sequences, the merge runs four workgroups per head (each a quarter
+    of the head's dims); with more, one per head: the 3- and 5-sequence cases take one each."""
+    _say(f"decode batch, long mixed contexts {positions}, auto split")
     rng = np.random.default_rng(44)
     qn, kn, sk = layer_weights(rng)
-    positions = [4100, 17000, 40000, 65535, 700]
-    n_slots = 65536 + 32
+    n_slots = (max(positions) + 1 + 31) // 32 * 32 + 32
     kv = fa.KVLayer(is_swa=False, has_rope=False, n_slots=n_slots, kv_dtype="f16", q_norm=qn, k_norm=kn, sinks=sk,
                     n_seq=len(positions))
     L = oracle_layer(kv, qn, kn, sk, "f16")
