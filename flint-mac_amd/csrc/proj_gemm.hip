@@ -52,24 +52,32 @@ __device__ inline size_t plane_unit(int n, int g, int K) {
 }  // namespace
 
 // ---------------------------------------------------------------------------
-// wprep: one wave per weight row: the row's bytes staged through LDS (2-byte copies: q8_0 and
-// q6_K blocks are only 2-byte aligned), dequantised 32 elements per lane per sub-block (lane l
-// owns sub-blocks l, l + 64, ...), the row's exponent from its largest magnitude, then the
-// hi/lo planes (in gemm3's chunk order) and f_n.
-constexpr int WP_MAX_K = 4096;
-constexpr int WP_STAGE = WP_MAX_K / 32 * 34;  // largest quantised row of the batch (q8_0)
+// wprep: one 512-thread workgroup per 8 weight rows n0 .. n0 + 7, wave w on row n0 + w: the row's
+// bytes staged through its LDS area (2-byte copies: q8_0 and q6_K blocks are only 2-byte aligned),
+// dequantised 32 elements per lane per sub-block (lane l owns sub-blocks l, l + 64, ...), the
+// row's exponent f_n from its largest magnitude, then its hi/lo values written over the staged
+// bytes. After the workgroup's barrier every store writes 8 whole 128-byte lines of the planes'
+// chunk order: lane (row rho = lane & 7, group lane gl = lane >> 3) of wave w takes the 16-byte
+// units of groups gl + 8 (w + 8 j) of row n0 + rho. The wave areas are 16 bytes longer than a
+// row's values, so the 8 rows' reads of one group fall on different banks.
 template <int K>
-__global__ __launch_bounds__(64) void wprep_kernel(const GemmWeightParams P) {
+__global__ __launch_bounds__(512) void wprep_kernel(const GemmWeightParams P) {
     constexpr int SUBS = K / 32 / 64;
-    __shared__ __align__(16) uint8_t stage[WP_STAGE > K * 4 ? WP_STAGE : K * 4];
-    const int lane = threadIdx.x, n = blockIdx.x;  // plane row
+    constexpr int AREA = K * 4 + 16;  // a staged row (at most K floats), later its hi|lo values
+    static_assert(K / 32 * 34 <= K * 4, "a quantised row fits its area");
+    __shared__ __align__(16) uint8_t areas[8 * AREA];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n = 8 * blockIdx.x + wave;  // this wave's plane row
+    uint8_t *const stage = areas + wave * AREA;
     const int in2 = P.n_seg > 2 && n >= P.seg[2].row0, in1 = !in2 && P.n_seg > 1 && n >= P.seg[1].row0;
     const MatvecSeg S = in2 ? P.seg[2] : in1 ? P.seg[1] : P.seg[0];
     const uint8_t *row = S.w + (size_t)(n - S.row0) * S.row_bytes;
     const uint16_t *src = (const uint16_t *)row;
     uint16_t *dst = (uint16_t *)stage;
     for (int i = lane; i < S.row_bytes / 2; i += 64) dst[i] = src[i];
-    __syncthreads();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     float w[SUBS][32];
     float mx = 0.f;
 #pragma unroll
@@ -79,9 +87,14 @@ __global__ __launch_bounds__(64) void wprep_kernel(const GemmWeightParams P) {
         for (int e = 0; e < 32; e++) mx = fmaxf(mx, fabsf(w[i][e]));
     }
     const int f = row_exp(wave_max(mx));
+    // every lane has read the staged bytes before any lane overwrites them
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    _Float16 *const hi = (_Float16 *)stage, *const lo = hi + K;
 #pragma unroll
     for (int i = 0; i < SUBS; i++) {
-        const int g0 = 4 * (lane + 64 * i);  // 8-element groups of this sub-block
+        const int k0 = 32 * (lane + 64 * i);
         f16x8 h8[4], l8[4];
 #pragma unroll
         for (int e = 0; e < 32; e++) {
@@ -92,12 +105,21 @@ __global__ __launch_bounds__(64) void wprep_kernel(const GemmWeightParams P) {
         }
 #pragma unroll
         for (int q = 0; q < 4; q++) {
-            const size_t o = plane_unit(n, g0 + q, K);
-            *(f16x8 *)(P.wh + o) = h8[q];
-            *(f16x8 *)(P.wl + o) = l8[q];
+            *(f16x8 *)(hi + k0 + 8 * q) = h8[q];
+            *(f16x8 *)(lo + k0 + 8 * q) = l8[q];
         }
     }
     if (lane == 0) P.fexp[n] = f;
+    __syncthreads();
+    const int rho = lane & 7, gl = lane >> 3, nr = 8 * blockIdx.x + rho;
+    const _Float16 *const rh = (const _Float16 *)(areas + rho * AREA), *const rl = rh + K;
+#pragma unroll
+    for (int j = 0; j < K / 512; j++) {
+        const int g = gl + 8 * (wave + 8 * j);
+        const size_t o = plane_unit(nr, g, K);
+        *(f16x8 *)(P.wh + o) = *(const f16x8 *)(rh + 8 * g);
+        *(f16x8 *)(P.wl + o) = *(const f16x8 *)(rl + 8 * g);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -326,10 +348,10 @@ hipError_t launch_proj_gemm(const GemmWeightParams &W, const GemmActParams &X, c
     // the planes' chunk order and the GEMM's tiles need whole 128-row tiles of both operands
     if (G.N % GM_TILE != 0 || X.T_pad % GM_TILE != 0 || (G.K != 2048 && G.K != 4096)) return hipErrorInvalidValue;
     if (G.K == 2048) {
-        if (prep_weights) hipLaunchKernelGGL(wprep_kernel<2048>, dim3(G.N), dim3(64), 0, stream, W);
+        if (prep_weights) hipLaunchKernelGGL(wprep_kernel<2048>, dim3(G.N / 8), dim3(512), 0, stream, W);
         if (X.T_pad > 0) hipLaunchKernelGGL(xprep_kernel<2048>, dim3(X.T_pad / 8), dim3(512), 0, stream, X);
     } else {
-        if (prep_weights) hipLaunchKernelGGL(wprep_kernel<4096>, dim3(G.N), dim3(64), 0, stream, W);
+        if (prep_weights) hipLaunchKernelGGL(wprep_kernel<4096>, dim3(G.N / 8), dim3(512), 0, stream, W);
         if (X.T_pad > 0) hipLaunchKernelGGL(xprep_kernel<4096>, dim3(X.T_pad / 8), dim3(512), 0, stream, X);
     }
     if (X.T_pad > 0)
