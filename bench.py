@@ -231,11 +231,14 @@ def calibration_copy(torch, nbytes=64 << 20):
     del src, dst
 
 
-def bench_decode_swa(torch, fa, reps=200, pos=32768):
+def bench_decode_swa(torch, fa, reps=320, pos=32768):
+    """One SWA decode call (513 keys) per layer, cycling through 160 layers' rings (320 MiB, more
+    than the 256 MB Infinity Cache), so each call reads its ring from HBM as in a decode step,
+    where every layer's ring was last touched a whole step earlier."""
     import numpy as np
     dev = torch.device("cuda:0")
     rng = np.random.default_rng(5)
-    n = 8
+    n = 160
     layers = [fa.KVLayer(is_swa=True, has_rope=True, kv_dtype="f16", q_norm=rng.uniform(0.5, 1.5, 128),
                          k_norm=rng.uniform(0.5, 1.5, 128), sinks=rng.standard_normal(32), device=dev)
               for _ in range(n)]
@@ -358,8 +361,9 @@ def bench_model(torch, fa, reps=48, ctx=32768, T_prefill=4000):
     N(0, 1/k) rows with ggml's q8_0 rounding; one set of rows written into every layer, each layer
     its own copy in HBM) and Flint's layer pattern. The caches hold zeros: the kernels read every
     byte whatever the values.
-      * one full layer at `ctx` cached positions and one SWA layer, each block and its attention
-        stage alone timed like the decode line (the projections are the difference);
+      * the full layers' blocks at `ctx` cached positions and the SWA layers' blocks, each block
+        and its attention stage alone timed like the decode line, each call on the next layer of
+        its kind (the projections are the difference);
       * flint_attn_model_prefill of T_prefill tokens from position 0 (embedding, then layer-major
         blocks), and of the whole ctx-token prompt;
       * then flint_attn_model_step (Engine::step over the blocks) at position ctx: 8 tokens per
@@ -401,13 +405,25 @@ def bench_model(torch, fa, reps=48, ctx=32768, T_prefill=4000):
     qkv = torch.randn(5120, device=dev)
     att = torch.empty(4096, device=dev)
     out = {}
-    full_il, swa_il = FLINT_FULL_LAYERS.index(True), FLINT_FULL_LAYERS.index(False)
-    for il, name in ((full_il, "full"), (swa_il, "swa")):
-        desc = model.layer(il)
-        t_block = queued_launch_ms(torch, lambda: model.block_decode(il, x, ctx, att), reps)[0]
-        t_attn = queued_launch_ms(
-            torch, lambda: fa._call(fa.lib().flint_attn_decode, ctypes.byref(desc), fa._ptr(qkv), fa._ptr(att), ctx,
-                                    0, ctypes.c_void_p(fa._stream(None))), reps)[0]
+    # Each call takes the next layer of the kind, so every call reads weights and a cache that
+    # the calls before it did not leave in the GPU's caches (one layer's 20 MB of projection
+    # weights fits in the 256 MB Infinity Cache and would be served from there if repeated),
+    # as in a step through the model.
+    for kind_full, name in ((True, "full"), (False, "swa")):
+        ils = [il for il, f in enumerate(FLINT_FULL_LAYERS) if f == kind_full]
+        descs = [model.layer(il) for il in ils]
+        nxt = [0]
+
+        def block():
+            i = nxt[0] = (nxt[0] + 1) % len(ils)
+            model.block_decode(ils[i], x, ctx, att)
+
+        def attn():
+            i = nxt[0] = (nxt[0] + 1) % len(ils)
+            fa._call(fa.lib().flint_attn_decode, ctypes.byref(descs[i]), fa._ptr(qkv), fa._ptr(att), ctx, 0,
+                     ctypes.c_void_p(fa._stream(None)))
+        t_block = queued_launch_ms(torch, block, reps)[0]
+        t_attn = queued_launch_ms(torch, attn, reps)[0]
         out[name] = dict(block_ms=t_block, attn_ms=t_attn, proj_ms=t_block - t_attn)
     t_proj = 0.5 * (out["full"]["proj_ms"] + out["swa"]["proj_ms"])
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
