@@ -460,11 +460,24 @@ def bench_model(torch, fa, reps=48, ctx=32768, T_prefill=4000):
 
     eight_steps()
     t_step = timed(eight_steps, 3) / 8
+    # one profiled step (flint_attn_model_enable_profiling / _last_profile): GPU time per kind of
+    # stage, summed over the 49 layers (the marks between stages add a little to the total)
+    model.truncate(ctx)
+    model.enable_profiling(True)
+    model.step(17, xs[0])
+    shares = {}
+    for label, ms in model.last_profile():
+        kind = label.rsplit(".", 1)[-1]
+        shares[kind] = shares.get(kind, 0.0) + ms
+    profiled_step_ms = model.last_gpu_ms()
+    model.enable_profiling(False)
     model.close()
     return dict(full_32k_block_ms=out["full"]["block_ms"], swa_block_ms=out["swa"]["block_ms"],
                 full_32k_attn_ms=out["full"]["attn_ms"], swa_attn_ms=out["swa"]["attn_ms"],
                 proj_ms=t_proj, proj_weight_bytes=wbytes, proj_gbs=wbytes / (t_proj * 1e-3) / 1e9,
                 step_32k_ms=t_step, step_tok_s_32k=1.0 / (t_step * 1e-3),
+                step_profile_ms={k: round(v, 5) for k, v in shares.items()},
+                step_profiled_ms=profiled_step_ms,
                 prefill_4000_ms=t_prefill, prefill_4000_tok_s=T_prefill / (t_prefill * 1e-3),
                 prefill_32k_ms=t_prefill_ctx, prefill_32k_tok_s=ctx / (t_prefill_ctx * 1e-3))
 

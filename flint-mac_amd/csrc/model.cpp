@@ -12,6 +12,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cstdio>
 #include <cstring>
 #include <memory>
 #include <stdexcept>
@@ -162,8 +163,18 @@ struct flint_attn_model {
     void *planes = nullptr;
     bool planes_failed = false;  // the allocation failed once: prefill rebuilds them per call instead
     std::vector<uint8_t> planes_built;
+    // Engine::last_gpu_ms and its profiler (enable_profiling / last_profile, engine.h:54-56, 63):
+    // marks are HIP events recorded on the call's stream, mark 0 where a step or prefill starts,
+    // then one where it ends or, with profiling on, one after each stage (the embedding, then per
+    // layer its q/k/v projection, attention and o projection). labels[i] names the stage between
+    // marks i and i + 1. marks_done: the last step or prefill recorded all its marks.
+    bool profiling = false, marks_done = false;
+    std::vector<hipEvent_t> marks;
+    std::vector<std::string> labels;
+    int n_marks = 0;
 
     ~flint_attn_model() {
+        for (hipEvent_t e : marks) (void)hipEventDestroy(e);
         flint_attn_engine_destroy(eng);
         if (wmem) (void)hipFree(wmem);
         if (qkv) (void)hipFree(qkv);
@@ -211,6 +222,32 @@ struct flint_attn_model {
         check(hipMalloc((void **)&qkv, (size_t)n_tok * FLINT_QKV_DIM * sizeof(float)), "hipMalloc qkv scratch");
         check(hipMalloc((void **)&att, (size_t)n_tok * FLINT_Q_DIM * sizeof(float)), "hipMalloc att scratch");
         cap = n_tok;
+    }
+    void begin_marks(hipStream_t s) {
+        n_marks = 0;
+        marks_done = false;
+        labels.clear();
+        mark(s, nullptr);
+    }
+    // the mark after a stage (label: the stage's name; none for mark 0)
+    void mark(hipStream_t s, const char *label) {
+        if (n_marks == (int)marks.size()) {
+            // a device-scope release where each mark is recorded (the default is system scope);
+            // a mark still adds ~2.5 us to the stream, ~0.37 ms over a profiled step's 148 marks
+            hipEvent_t e;
+            check(hipEventCreateWithFlags(&e, hipEventReleaseToDevice), "hipEventCreateWithFlags");
+            marks.push_back(e);
+        }
+        check(hipEventRecord(marks[n_marks], s), "hipEventRecord");
+        if (n_marks > 0) labels.emplace_back(label);
+        n_marks++;
+    }
+    // the mark after stage `what` of layer il, when profiling
+    void stage(hipStream_t s, bool prof, int il, const char *what) {
+        if (!prof) return;
+        char label[32];
+        std::snprintf(label, sizeof(label), "blk.%d.%s", il, what);
+        mark(s, label);
     }
     const Layer &layer(int il) const {
         if (il < 0 || il >= (int)layers.size()) throw std::runtime_error("model: bad layer index");
@@ -326,47 +363,99 @@ int32_t flint_attn_model_embed(flint_attn_model *m, const int32_t *tokens, int32
     });
 }
 
+}  // extern "C"
+
+namespace {
+
+// A decode block; prof: a stage mark after each of its three stages (a profiled step).
+void block_decode(flint_attn_model *m, int il, float *x, int pos, float *att, void *stream, bool prof) {
+    if (!m) throw std::runtime_error("block_decode: no model");
+    const flint_attn_model::Layer &L = m->layer(il);
+    if (!x) throw std::runtime_error("block_decode: x is NULL");
+    m->reserve(1);
+    float *a = att ? att : m->att;
+    char e2[512] = {0};
+    const hipStream_t s = (hipStream_t)stream;
+    call(flint_attn_qkv_proj(&L.q, &L.k, &L.v, x, L.attn_norm, m->hp.h.rms_eps, m->qkv, stream, e2, sizeof(e2)), e2);
+    m->stage(s, prof, il, "qkv");
+    call(flint_attn_engine_decode(m->eng, il, m->qkv, a, pos, stream, e2, sizeof(e2)), e2);
+    m->stage(s, prof, il, "attn");
+    call(flint_attn_o_proj(&L.o, a, x, stream, e2, sizeof(e2)), e2);
+    m->stage(s, prof, il, "o");
+}
+
+// A prefill block over T tokens; prof as for block_decode.
+void block_prefill(flint_attn_model *m, int il, float *X, int p0, int T, float *att, void *stream, bool prof) {
+    if (!m) throw std::runtime_error("block_prefill: no model");
+    const flint_attn_model::Layer &L = m->layer(il);
+    if (!X) throw std::runtime_error("block_prefill: X is NULL");
+    if (T <= 0) throw std::runtime_error("prefill: empty");
+    m->reserve(T);
+    float *a = att ? att : m->att;
+    char e2[512] = {0};
+    const hipStream_t s = (hipStream_t)stream;
+    WeightPlanes pq, po;
+    if (T >= GEMM_MIN_TOKENS && m->layer_planes(il, s, &pq, &po)) {
+        // the projections' GEMMs read the layer's cached weight planes
+        qkv_proj_rows_planes(&L.q, &L.k, &L.v, X, T, L.attn_norm, m->hp.h.rms_eps, m->qkv, FLINT_QKV_DIM, &pq, s);
+        m->stage(s, prof, il, "qkv");
+        call(flint_attn_engine_prefill(m->eng, il, m->qkv, p0, T, a, stream, e2, sizeof(e2)), e2);
+        m->stage(s, prof, il, "attn");
+        o_proj_rows_planes(&L.o, a, T, X, &po, s);
+        m->stage(s, prof, il, "o");
+        return;
+    }
+    call(flint_attn_qkv_proj_rows(&L.q, &L.k, &L.v, X, T, L.attn_norm, m->hp.h.rms_eps, m->qkv, FLINT_QKV_DIM,
+                                  stream, e2, sizeof(e2)),
+         e2);
+    m->stage(s, prof, il, "qkv");
+    call(flint_attn_engine_prefill(m->eng, il, m->qkv, p0, T, a, stream, e2, sizeof(e2)), e2);
+    m->stage(s, prof, il, "attn");
+    call(flint_attn_o_proj_rows(&L.o, a, T, X, stream, e2, sizeof(e2)), e2);
+    m->stage(s, prof, il, "o");
+}
+
+}  // namespace
+
+extern "C" {
+
 int32_t flint_attn_model_block_decode(flint_attn_model *m, int32_t il, float *x, int32_t pos, float *att,
                                       void *stream, char *err, int32_t err_len) {
-    return guarded(err, err_len, [&] {
-        if (!m) throw std::runtime_error("block_decode: no model");
-        const flint_attn_model::Layer &L = m->layer(il);
-        if (!x) throw std::runtime_error("block_decode: x is NULL");
-        m->reserve(1);
-        float *a = att ? att : m->att;
-        char e2[512] = {0};
-        call(flint_attn_qkv_proj(&L.q, &L.k, &L.v, x, L.attn_norm, m->hp.h.rms_eps, m->qkv, stream, e2, sizeof(e2)),
-             e2);
-        call(flint_attn_engine_decode(m->eng, il, m->qkv, a, pos, stream, e2, sizeof(e2)), e2);
-        call(flint_attn_o_proj(&L.o, a, x, stream, e2, sizeof(e2)), e2);
-    });
+    return guarded(err, err_len, [&] { block_decode(m, il, x, pos, att, stream, false); });
 }
 
 int32_t flint_attn_model_block_prefill(flint_attn_model *m, int32_t il, float *X, int32_t p0, int32_t T,
                                        float *att, void *stream, char *err, int32_t err_len) {
-    return guarded(err, err_len, [&] {
-        if (!m) throw std::runtime_error("block_prefill: no model");
-        const flint_attn_model::Layer &L = m->layer(il);
-        if (!X) throw std::runtime_error("block_prefill: X is NULL");
-        if (T <= 0) throw std::runtime_error("prefill: empty");
-        m->reserve(T);
-        float *a = att ? att : m->att;
-        char e2[512] = {0};
-        const hipStream_t s = (hipStream_t)stream;
-        WeightPlanes pq, po;
-        if (T >= GEMM_MIN_TOKENS && m->layer_planes(il, s, &pq, &po)) {
-            // the projections' GEMMs read the layer's cached weight planes
-            qkv_proj_rows_planes(&L.q, &L.k, &L.v, X, T, L.attn_norm, m->hp.h.rms_eps, m->qkv, FLINT_QKV_DIM, &pq, s);
-            call(flint_attn_engine_prefill(m->eng, il, m->qkv, p0, T, a, stream, e2, sizeof(e2)), e2);
-            o_proj_rows_planes(&L.o, a, T, X, &po, s);
-            return;
-        }
-        call(flint_attn_qkv_proj_rows(&L.q, &L.k, &L.v, X, T, L.attn_norm, m->hp.h.rms_eps, m->qkv, FLINT_QKV_DIM,
-                                      stream, e2, sizeof(e2)),
-             e2);
-        call(flint_attn_engine_prefill(m->eng, il, m->qkv, p0, T, a, stream, e2, sizeof(e2)), e2);
-        call(flint_attn_o_proj_rows(&L.o, a, T, X, stream, e2, sizeof(e2)), e2);
-    });
+    return guarded(err, err_len, [&] { block_prefill(m, il, X, p0, T, att, stream, false); });
+}
+
+int32_t flint_attn_model_enable_profiling(flint_attn_model *m, int32_t on) {
+    if (!m) return -1;
+    m->profiling = on != 0;
+    return 0;
+}
+
+double flint_attn_model_last_gpu_ms(flint_attn_model *m) {
+    if (!m || !m->marks_done || m->n_marks < 2) return -1.0;
+    hipEvent_t e0 = m->marks[0], e1 = m->marks[m->n_marks - 1];
+    float ms = 0.f;
+    if (hipEventSynchronize(e1) != hipSuccess || hipEventElapsedTime(&ms, e0, e1) != hipSuccess) return -1.0;
+    return ms;
+}
+
+int32_t flint_attn_model_last_profile(flint_attn_model *m, char *labels, int32_t label_len, double *ms,
+                                      int32_t max_n) {
+    if (!m || !m->marks_done || m->n_marks < 2) return -1;
+    const int n = m->n_marks - 1;
+    if (!ms || max_n <= 0) return n;
+    if (hipEventSynchronize(m->marks[n]) != hipSuccess) return -1;
+    for (int i = 0; i < n && i < max_n; i++) {
+        float t = 0.f;
+        if (hipEventElapsedTime(&t, m->marks[i], m->marks[i + 1]) != hipSuccess) return -1;
+        ms[i] = t;
+        if (labels && label_len > 0) set_err(labels + (size_t)i * label_len, label_len, m->labels[i].c_str());
+    }
+    return n;
 }
 
 int32_t flint_attn_model_pos(const flint_attn_model *m) { return m ? m->pos : 0; }
@@ -384,10 +473,15 @@ int32_t flint_attn_model_step(flint_attn_model *m, int32_t token, float *x, void
         if (!m) throw std::runtime_error("step: no model");
         if (!x) throw std::runtime_error("step: x is NULL");
         if (m->pos >= m->n_ctx) throw std::runtime_error("context full");
+        const hipStream_t s = (hipStream_t)stream;
+        const bool prof = m->profiling;
         char e2[512] = {0};
+        m->begin_marks(s);
         call(flint_attn_model_embed(m, &token, 1, x, stream, e2, sizeof(e2)), e2);
-        for (int il = 0; il < (int)m->layers.size(); il++)
-            call(flint_attn_model_block_decode(m, il, x, m->pos, nullptr, stream, e2, sizeof(e2)), e2);
+        if (prof) m->mark(s, "embed");
+        for (int il = 0; il < (int)m->layers.size(); il++) block_decode(m, il, x, m->pos, nullptr, stream, prof);
+        if (!prof) m->mark(s, "step");
+        m->marks_done = true;
         m->pos++;
     });
 }
@@ -399,10 +493,15 @@ int32_t flint_attn_model_prefill(flint_attn_model *m, const int32_t *tokens, int
         if (!tokens || n <= 0) throw std::runtime_error("prefill: empty");
         if (!X) throw std::runtime_error("prefill: X is NULL");
         if ((int64_t)m->pos + n > m->n_ctx) throw std::runtime_error("prefill: context full");
+        const hipStream_t s = (hipStream_t)stream;
+        const bool prof = m->profiling;
         char e2[512] = {0};
+        m->begin_marks(s);
         call(flint_attn_model_embed(m, tokens, n, X, stream, e2, sizeof(e2)), e2);
-        for (int il = 0; il < (int)m->layers.size(); il++)
-            call(flint_attn_model_block_prefill(m, il, X, m->pos, n, nullptr, stream, e2, sizeof(e2)), e2);
+        if (prof) m->mark(s, "embed");
+        for (int il = 0; il < (int)m->layers.size(); il++) block_prefill(m, il, X, m->pos, n, nullptr, stream, prof);
+        if (!prof) m->mark(s, "prefill");
+        m->marks_done = true;
         m->pos += n;
     });
 }

@@ -101,6 +101,9 @@ _SIGS = {
     "flint_attn_model_truncate": (_i32, [_vp, _i32]),
     "flint_attn_model_step": (_i32, [_vp, _i32, _vp, _vp, _cp, _i32]),
     "flint_attn_model_prefill": (_i32, [_vp, _i32p, _i32, _vp, _vp, _cp, _i32]),
+    "flint_attn_model_enable_profiling": (_i32, [_vp, _i32]),
+    "flint_attn_model_last_gpu_ms": (ctypes.c_double, [_vp]),
+    "flint_attn_model_last_profile": (_i32, [_vp, _cp, _i32, ctypes.POINTER(ctypes.c_double), _i32]),
     "flint_open": (_vp, [_vp, _cp, _i32]),
     "flint_close": (None, [_vp]),
     "flint_n_ctx": (_i32, [_vp]),
@@ -298,11 +301,36 @@ class Model:
         self.h = ctypes.c_void_p(h)
 
     def close(self):
-        if getattr(self, "h", None):
+        if getattr(self, "h", None) and lib is not None:  # lib is None while the interpreter exits
             lib().flint_attn_model_close(self.h)
             self.h = None
 
     __del__ = close
+
+    def enable_profiling(self, on=True):
+        """Later steps and prefills time each stage (Engine::enable_profiling;
+        flint_attn_model_enable_profiling)."""
+        lib().flint_attn_model_enable_profiling(self.h, 1 if on else 0)
+
+    def last_gpu_ms(self):
+        """GPU time of the last step or prefill in ms, or None before any (Engine::last_gpu_ms;
+        flint_attn_model_last_gpu_ms). Waits for that call's work."""
+        t = lib().flint_attn_model_last_gpu_ms(self.h)
+        return None if t < 0 else t
+
+    def last_profile(self):
+        """[(stage, ms)] of the last step or prefill in order (Engine::last_profile;
+        flint_attn_model_last_profile). Waits for that call's work."""
+        n = lib().flint_attn_model_last_profile(self.h, None, 0, None, 0)
+        if n < 0:
+            return []
+        width = 32
+        labels = ctypes.create_string_buffer(n * width)
+        ms = (ctypes.c_double * n)()
+        if lib().flint_attn_model_last_profile(self.h, labels, width, ms, n) != n:
+            raise FlintAttnError("flint_attn_model_last_profile failed")
+        raw = labels.raw
+        return [(raw[i * width:(i + 1) * width].split(b"\0")[0].decode(), ms[i]) for i in range(n)]
 
     def hparams(self):
         """(HParams, is_swa list, has_rope list)."""

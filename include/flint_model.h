@@ -124,6 +124,36 @@ int32_t flint_attn_model_step(flint_attn_model *m, int32_t token, float *x, void
 int32_t flint_attn_model_prefill(flint_attn_model *m, const int32_t *tokens, int32_t n, float *X, void *stream,
                                  char *err, int32_t err_len);
 
+/*
+ * Engine::enable_profiling (engine.h:54-55, engine.mm:948-951): with `on` set, every later
+ * step and prefill also records a HIP event after each of its stages on the call's stream (the
+ * embedding "embed", then per layer L "blk.L.qkv", "blk.L.attn" and "blk.L.o"), which
+ * flint_attn_model_last_profile reads. The events between stages order nothing, but they add
+ * work to the stream, so profiled times are for relative shares, as the reference's are.
+ * `on` = 0 turns it off. 0, or -1 without a model.
+ */
+int32_t flint_attn_model_enable_profiling(flint_attn_model *m, int32_t on);
+
+/*
+ * Engine::last_gpu_ms (engine.h:63; engine.mm:931, the command buffer's GPU start to end): the
+ * GPU time of the last flint_attn_model_step or _prefill, from HIP events recorded on its stream
+ * where it started and ended. Waits for that call's work to finish. -1 when no step or prefill
+ * has completed its launches yet.
+ */
+double flint_attn_model_last_gpu_ms(flint_attn_model *m);
+
+/*
+ * Engine::last_profile (engine.h:56, engine.mm:953-966): the stages of the last step or
+ * prefill in order, each with its GPU time in ms (consecutive event marks, so the times sum to
+ * flint_attn_model_last_gpu_ms). Unprofiled calls have one stage, "step" or "prefill". Writes
+ * min(n, max_n) entries: ms[i], and when labels is given the i-th label, NUL-terminated and cut
+ * to label_len - 1 bytes, at labels + i * label_len. Returns n, the number of stages (with ms
+ * NULL or max_n <= 0: only n, without waiting), or -1 when there is none (or on a HIP error).
+ * Waits for that call's work to finish.
+ */
+int32_t flint_attn_model_last_profile(flint_attn_model *m, char *labels, int32_t label_len, double *ms,
+                                      int32_t max_n);
+
 #ifdef __cplusplus
 }
 #endif

@@ -158,6 +158,10 @@ def test_capi_null_handle_paths():
     assert L.flint_decode(None, 1, err, len(err)) == -1 and err.value
     assert L.flint_prefill(None, None, 0, err, len(err)) == -1
     assert not L.flint_logits(None)
+    # the model session's timing calls (Engine::last_gpu_ms / enable_profiling / last_profile)
+    assert L.flint_attn_model_enable_profiling(None, 1) == -1
+    assert L.flint_attn_model_last_gpu_ms(None) == -1.0
+    assert L.flint_attn_model_last_profile(None, None, 0, None, 0) == -1
 
 
 def _layer(**kw):

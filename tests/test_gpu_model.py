@@ -195,6 +195,59 @@ def test_session_step_prefill_truncate(setup, cuda):
     m2.close()
 
 
+def test_session_gpu_time_and_profile(setup, cuda):
+    """Engine::last_gpu_ms / enable_profiling / last_profile (/root/reference/src/engine.h:54-56,
+    63) over the session: the GPU time of the last step or prefill, and with profiling on its
+    stages in order (the embedding, then per layer the q/k/v projection, attention and o
+    projection), whose times sum to it. Profiling changes no result: the same calls after a
+    rollback give the same hidden states bit for bit."""
+    import torch
+    m = fa.Model(setup[0], n_ctx=256)
+    assert m.last_gpu_ms() is None and m.last_profile() == []
+    n_layer = m.hparams()[0].n_layer
+    stages = ["embed"] + [f"blk.{il}.{s}" for il in range(n_layer) for s in ("qkv", "attn", "o")]
+    X = torch.zeros((33, 2048), device=cuda)
+    m.prefill(list(range(32)), X[:32])
+    t = m.last_gpu_ms()
+    prof = m.last_profile()
+    assert t is not None and t > 0
+    assert [s for s, _ in prof] == ["prefill"] and abs(prof[0][1] - t) <= 1e-6 + 1e-6 * t
+    m.step(32, X[32])
+    assert [s for s, _ in m.last_profile()] == ["step"] and m.last_gpu_ms() > 0
+    torch.cuda.synchronize()
+    want = X.cpu().numpy()
+
+    m.enable_profiling(True)
+    assert m.truncate(0) == 0
+    Y = torch.zeros((33, 2048), device=cuda)
+    m.prefill(list(range(32)), Y[:32])
+    prof = m.last_profile()
+    t = m.last_gpu_ms()
+    assert [s for s, _ in prof] == stages
+    assert all(ms >= 0 for _, ms in prof)
+    assert abs(sum(ms for _, ms in prof) - t) <= 1e-3 + 1e-4 * t
+    m.step(32, Y[32])
+    prof = m.last_profile()
+    t = m.last_gpu_ms()
+    assert [s for s, _ in prof] == stages
+    assert abs(sum(ms for _, ms in prof) - t) <= 1e-3 + 1e-4 * t
+    torch.cuda.synchronize()
+    assert np.array_equal(Y.cpu().numpy(), want), "profiling changed the hidden states"
+
+    m.enable_profiling(False)
+    assert m.truncate(32) == 0
+    m.step(32, Y[32])
+    assert [s for s, _ in m.last_profile()] == ["step"]
+    # a failed call leaves no timing behind
+    with pytest.raises(fa.FlintAttnError, match="prefill: empty"):
+        m.prefill([], Y)
+    assert m.last_gpu_ms() is not None  # the check fails before the call starts its marks
+    with pytest.raises(fa.FlintAttnError, match="out of range"):
+        m.step(1 << 20, Y[32])
+    assert m.last_gpu_ms() is None and m.last_profile() == []
+    m.close()
+
+
 def test_session_errors(setup, cuda):
     import torch
     m = fa.Model(setup[0], n_ctx=64)
