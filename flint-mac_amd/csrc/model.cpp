@@ -12,6 +12,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <chrono>
 #include <cstdio>
 #include <cstring>
 #include <memory>
@@ -169,6 +170,7 @@ struct flint_attn_model {
     // layer its q/k/v projection, attention and o projection). labels[i] names the stage between
     // marks i and i + 1. marks_done: the last step or prefill recorded all its marks.
     bool profiling = false, marks_done = false;
+    double encode_ms = -1.0;  // host time the last step / prefill took to enqueue its work (Engine::last_encode_ms)
     std::vector<hipEvent_t> marks;
     std::vector<std::string> labels;
     int n_marks = 0;
@@ -226,6 +228,7 @@ struct flint_attn_model {
     void begin_marks(hipStream_t s) {
         n_marks = 0;
         marks_done = false;
+        encode_ms = -1.0;
         labels.clear();
         mark(s, nullptr);
     }
@@ -443,6 +446,10 @@ double flint_attn_model_last_gpu_ms(flint_attn_model *m) {
     return ms;
 }
 
+double flint_attn_model_last_encode_ms(const flint_attn_model *m) {
+    return m && m->marks_done ? m->encode_ms : -1.0;
+}
+
 int32_t flint_attn_model_last_profile(flint_attn_model *m, char *labels, int32_t label_len, double *ms,
                                       int32_t max_n) {
     if (!m || !m->marks_done || m->n_marks < 2) return -1;
@@ -475,6 +482,7 @@ int32_t flint_attn_model_step(flint_attn_model *m, int32_t token, float *x, void
         if (m->pos >= m->n_ctx) throw std::runtime_error("context full");
         const hipStream_t s = (hipStream_t)stream;
         const bool prof = m->profiling;
+        const auto t0 = std::chrono::steady_clock::now();
         char e2[512] = {0};
         m->begin_marks(s);
         call(flint_attn_model_embed(m, &token, 1, x, stream, e2, sizeof(e2)), e2);
@@ -482,6 +490,7 @@ int32_t flint_attn_model_step(flint_attn_model *m, int32_t token, float *x, void
         for (int il = 0; il < (int)m->layers.size(); il++) block_decode(m, il, x, m->pos, nullptr, stream, prof);
         if (!prof) m->mark(s, "step");
         m->marks_done = true;
+        m->encode_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
         m->pos++;
     });
 }
@@ -495,6 +504,7 @@ int32_t flint_attn_model_prefill(flint_attn_model *m, const int32_t *tokens, int
         if ((int64_t)m->pos + n > m->n_ctx) throw std::runtime_error("prefill: context full");
         const hipStream_t s = (hipStream_t)stream;
         const bool prof = m->profiling;
+        const auto t0 = std::chrono::steady_clock::now();
         char e2[512] = {0};
         m->begin_marks(s);
         call(flint_attn_model_embed(m, tokens, n, X, stream, e2, sizeof(e2)), e2);
@@ -502,6 +512,7 @@ int32_t flint_attn_model_prefill(flint_attn_model *m, const int32_t *tokens, int
         for (int il = 0; il < (int)m->layers.size(); il++) block_prefill(m, il, X, m->pos, n, nullptr, stream, prof);
         if (!prof) m->mark(s, "prefill");
         m->marks_done = true;
+        m->encode_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
         m->pos += n;
     });
 }

@@ -103,6 +103,7 @@ _SIGS = {
     "flint_attn_model_prefill": (_i32, [_vp, _i32p, _i32, _vp, _vp, _cp, _i32]),
     "flint_attn_model_enable_profiling": (_i32, [_vp, _i32]),
     "flint_attn_model_last_gpu_ms": (ctypes.c_double, [_vp]),
+    "flint_attn_model_last_encode_ms": (ctypes.c_double, [_vp]),
     "flint_attn_model_last_profile": (_i32, [_vp, _cp, _i32, ctypes.POINTER(ctypes.c_double), _i32]),
     "flint_open": (_vp, [_vp, _cp, _i32]),
     "flint_close": (None, [_vp]),
@@ -316,6 +317,12 @@ class Model:
         """GPU time of the last step or prefill in ms, or None before any (Engine::last_gpu_ms;
         flint_attn_model_last_gpu_ms). Waits for that call's work."""
         t = lib().flint_attn_model_last_gpu_ms(self.h)
+        return None if t < 0 else t
+
+    def last_encode_ms(self):
+        """Host time the last step or prefill took to enqueue its launches, in ms, or None
+        (Engine::last_encode_ms; flint_attn_model_last_encode_ms)."""
+        t = lib().flint_attn_model_last_encode_ms(self.h)
         return None if t < 0 else t
 
     def last_profile(self):

@@ -143,6 +143,13 @@ int32_t flint_attn_model_enable_profiling(flint_attn_model *m, int32_t on);
 double flint_attn_model_last_gpu_ms(flint_attn_model *m);
 
 /*
+ * Engine::last_encode_ms (engine.h:63; engine.mm:906-915, the host's encoding time): the host
+ * time the last flint_attn_model_step or _prefill took to check its arguments and enqueue its
+ * launches, in ms. -1 when no step or prefill has completed its launches yet.
+ */
+double flint_attn_model_last_encode_ms(const flint_attn_model *m);
+
+/*
  * Engine::last_profile (engine.h:56, engine.mm:953-966): the stages of the last step or
  * prefill in order, each with its GPU time in ms (consecutive event marks, so the times sum to
  * flint_attn_model_last_gpu_ms). Unprofiled calls have one stage, "step" or "prefill". Writes

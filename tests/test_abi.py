@@ -161,6 +161,7 @@ def test_capi_null_handle_paths():
     # the model session's timing calls (Engine::last_gpu_ms / enable_profiling / last_profile)
     assert L.flint_attn_model_enable_profiling(None, 1) == -1
     assert L.flint_attn_model_last_gpu_ms(None) == -1.0
+    assert L.flint_attn_model_last_encode_ms(None) == -1.0
     assert L.flint_attn_model_last_profile(None, None, 0, None, 0) == -1
 
 

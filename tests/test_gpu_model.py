@@ -203,14 +203,14 @@ def test_session_gpu_time_and_profile(setup, cuda):
     rollback give the same hidden states bit for bit."""
     import torch
     m = fa.Model(setup[0], n_ctx=256)
-    assert m.last_gpu_ms() is None and m.last_profile() == []
+    assert m.last_gpu_ms() is None and m.last_profile() == [] and m.last_encode_ms() is None
     n_layer = m.hparams()[0].n_layer
     stages = ["embed"] + [f"blk.{il}.{s}" for il in range(n_layer) for s in ("qkv", "attn", "o")]
     X = torch.zeros((33, 2048), device=cuda)
     m.prefill(list(range(32)), X[:32])
     t = m.last_gpu_ms()
     prof = m.last_profile()
-    assert t is not None and t > 0
+    assert t is not None and t > 0 and m.last_encode_ms() > 0
     assert [s for s, _ in prof] == ["prefill"] and abs(prof[0][1] - t) <= 1e-6 + 1e-6 * t
     m.step(32, X[32])
     assert [s for s, _ in m.last_profile()] == ["step"] and m.last_gpu_ms() > 0
@@ -244,7 +244,7 @@ def test_session_gpu_time_and_profile(setup, cuda):
     assert m.last_gpu_ms() is not None  # the check fails before the call starts its marks
     with pytest.raises(fa.FlintAttnError, match="out of range"):
         m.step(1 << 20, Y[32])
-    assert m.last_gpu_ms() is None and m.last_profile() == []
+    assert m.last_gpu_ms() is None and m.last_profile() == [] and m.last_encode_ms() is None
     m.close()
 
 
