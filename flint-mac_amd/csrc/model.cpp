@@ -236,7 +236,8 @@ struct flint_attn_model {
     void mark(hipStream_t s, const char *label) {
         if (n_marks == (int)marks.size()) {
             // a device-scope release where each mark is recorded (the default is system scope);
-            // a mark still adds ~2.5 us to the stream, ~0.37 ms over a profiled step's 148 marks
+            // a mark still adds a few microseconds to the stream (0.4-0.9 ms over a profiled
+            // step's 148 marks)
             hipEvent_t e;
             check(hipEventCreateWithFlags(&e, hipEventReleaseToDevice), "hipEventCreateWithFlags");
             marks.push_back(e);
