@@ -50,7 +50,6 @@ namespace flint {
 constexpr int PART_STRIDE = 132;
 constexpr int DEC_WAVES = 8;
 constexpr int DEC_THREADS = DEC_WAVES * 64;
-constexpr int MERGE_MAX_SPLIT = 1024;
 // LDS row of a wave's partial accumulator for one head: 128 floats + 4 of padding, so the
 // 32 lanes that write 16 bytes each spread evenly over the banks
 constexpr int ACC_ROW = HEAD_DIM + 4;
@@ -72,20 +71,22 @@ struct KvTile {
 template <int VS>
 __device__ inline void load_tile(KvTile<VS> &T, const uint16_t *__restrict__ kc, const uint16_t *__restrict__ vc,
                                  int t, int lane, int slot_mask, bool live, int slice) {
-    const uint32_t base = ((uint32_t)(t * 32) & (uint32_t)slot_mask) * HEAD_DIM;
+    // byte offsets in 32 bits (the host bounds a kv head's cache below 2^31 bytes)
+    const uint32_t base = ((uint32_t)(t * 32) & (uint32_t)slot_mask) * (HEAD_DIM * 2);
+    const char *kb = (const char *)kc, *vb = (const char *)vc;
     // K: instruction (st, c) reads units (st*4 + c)*64 + lane: MFMA row n = lane & 15 holds
     // key 8(n>>2) + 4st + (n&3) of the tile, dims 32c + 8(lane>>4) .. +7
-    const uint32_t ko = base + (live ? lane * 8 : 0);
+    const uint32_t ko = base + (live ? lane * 16 : 0);
 #pragma unroll
     for (int st = 0; st < 2; st++)
 #pragma unroll
         for (int c = 0; c < 4; c++)
-            T.k[st][c] = __builtin_nontemporal_load((const u32x4 *)(kc + ko + (st * 4 + c) * 512));
+            T.k[st][c] = __builtin_nontemporal_load((const u32x4 *)(kb + (ko + (st * 4 + c) * 1024)));
     // V^T tile (8 KiB): row = dim 16d + n, keys 8g .. 8g+7 of the tile
-    const uint32_t vo = base + (live ? (lane & 15) * 32 + 8 * (lane >> 4) : 0);
+    const uint32_t vo = base + (live ? (lane & 15) * 64 + 16 * (lane >> 4) : 0);
 #pragma unroll
     for (int d = 0; d < 8 / VS; d++)
-        T.v[d] = __builtin_nontemporal_load((const u32x4 *)(vc + vo + 16 * (8 / VS * slice + d) * 32));
+        T.v[d] = __builtin_nontemporal_load((const u32x4 *)(vb + (vo + (8 / VS * slice + d) * 1024)));
 }
 
 template <int DT, int VS>
@@ -139,14 +140,18 @@ __device__ inline void consume_tile(DecodeState<DT, VS> &S, KvTile<VS> &T, const
     if (kb < k_begin || kb + 32 > pos) {  // wave-uniform: a tile at either end of the key range
         // keys outside [k_begin, pos) get score -inf and V = 0 (their slots may hold
         // stale data, and 0 * inf is nan); V words hold keys (2w, 2w+1)
+        // (-inf is made here, in a register of its own, rather than hoisted out of the
+        // stream loop by the compiler, where it would hold a register for the whole loop)
+        float ninf;
+        asm volatile("v_mov_b32 %0, 0xff800000" : "=v"(ninf));
         uint32_t vmask[4];
 #pragma unroll
         for (int w = 0; w < 4; w++) {
             const int key = kb + 8 * g + 2 * w;
             const bool ok0 = (key >= k_begin) & (key < pos), ok1 = (key + 1 >= k_begin) & (key + 1 < pos);
-            sc[2 * w] = ok0 ? sc[2 * w] : -INFINITY;
-            sc[2 * w + 1] = ok1 ? sc[2 * w + 1] : -INFINITY;
-            vmask[w] = (ok0 ? 0x0000ffffu : 0u) | (ok1 ? 0xffff0000u : 0u);
+            sc[2 * w] = ok0 ? sc[2 * w] : ninf;
+            sc[2 * w + 1] = ok1 ? sc[2 * w + 1] : ninf;
+            vmask[w] = ((uint32_t)-(int)ok0 >> 16) | ((uint32_t)-(int)ok1 << 16);
         }
 #pragma unroll
         for (int d = 0; d < 8 / VS; d++)
@@ -178,8 +183,10 @@ template <int DT, int VS>
 __global__ __launch_bounds__(DEC_THREADS) void attn_decode_kernel(const DecodeParams P) {
     typedef KvType<DT> KT;
     typedef typename KT::vec8 vec8;
+    constexpr int W = DEC_WAVES;
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // the wave index is made scalar, so everything derived from it lives in SGPRs
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int n = lane & 15, g = lane >> 4;   // MFMA column (q head x hi/lo) and k-group
     const int hloc = n & 7, hl = n >> 3;      // head within the GQA group, 0 = hi half, 1 = lo half
     static_assert(MAX_SEQ == 64, "one per-sequence table entry per lane");
@@ -212,7 +219,8 @@ __global__ __launch_bounds__(DEC_THREADS) void attn_decode_kernel(const DecodePa
     const int seq = __builtin_popcountll(__builtin_amdgcn_ballot_w64(lane < n_seq && wid >= t_base)) - 1;
     const int n_split = __builtin_amdgcn_readlane(t_ns, seq), pos = __builtin_amdgcn_readlane(t_pos, seq);
     const int tps = __builtin_amdgcn_readlane(t_tps, seq);
-    const int local = wid - __builtin_amdgcn_readlane(t_base, seq);
+    const int seq_base = __builtin_amdgcn_readlane(t_base, seq);
+    const int local = wid - seq_base;
     const int kvh = local & (N_HEAD_KV - 1), slice = (local / N_HEAD_KV) % VS, split = local / (N_HEAD_KV * VS);
     if (seq < 0 || split >= n_split) return;  // not reached: the host sizes the grid exactly
     const bool last_split = split == n_split - 1;
@@ -229,18 +237,20 @@ __global__ __launch_bounds__(DEC_THREADS) void attn_decode_kernel(const DecodePa
     __shared__ uint16_t sm_qh[2][GQA][HEAD_DIM];   // [hi/lo][head][dim]
     __shared__ float sm_q[GQA][HEAD_DIM];          // log2(e)/sqrt(D)-scaled q (for the current token)
     __shared__ float sm_kv[2][HEAD_DIM];           // current token: k and v as the cache holds them
-    __shared__ float sm_acc[DEC_WAVES][GQA][ACC_ROW];  // wave partial accumulators (padded rows)
-    __shared__ float sm_m[DEC_WAVES + 1][GQA], sm_l[DEC_WAVES + 1][GQA];
+    __shared__ float sm_acc[W][GQA][ACC_ROW];      // wave partial accumulators (padded rows)
+    __shared__ float sm_m[W + 1][GQA], sm_l[W + 1][GQA];
 
-    // ---- the prologue's inputs first, then this wave's first two tiles: vmcnt counts
+    // ---- the prologue's inputs first, then this wave's first tiles: vmcnt counts
     //      completions in issue order, so the prologue can wait for its own small loads
-    //      while the tiles stay in flight ----
-    const bool cur_wave = last_split && wave == DEC_WAVES - 1;  // also handles the current token
+    //      while the tiles stay in flight. Wave w normalises q head w; the last split's last
+    //      wave also handles the current token ----
+    const bool cur_wave = last_split && wave == W - 1;
     const float *qr = row + (kvh * GQA + wave) * HEAD_DIM;
     const float2 qx = make_float2(qr[lane], qr[lane + 64]);
     const float2 qw = make_float2(q_norm[lane], q_norm[lane + 64]);
     const float rfreq = P.rope_freq[lane];
-    const float sink = sinks[kvh * GQA + wave] * LOG2E;  // head `wave` of the group, for the final merge
+    // head `wave` of the group, for the final merge: wave-uniform, kept in an SGPR
+    const float sink = __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(sinks[kvh * GQA + wave]))) * LOG2E;
     float2 kx = {0.f, 0.f}, kw = {0.f, 0.f}, vx = {0.f, 0.f};
     if (cur_wave) {
         const float *kr = row + Q_DIM + kvh * HEAD_DIM, *vr = row + Q_DIM + KV_DIM + kvh * HEAD_DIM;
@@ -257,7 +267,7 @@ __global__ __launch_bounds__(DEC_THREADS) void attn_decode_kernel(const DecodePa
     // contexts the prologue ends only as the stream does; the tiles land no earlier when
     // the prologue goes first, so nothing is gained by reordering.)
     KvTile<VS> ta, tb;
-    int t_a = t_begin + wave, t_b = t_a + DEC_WAVES;
+    int t_a = t_begin + wave, t_b = t_a + W;
     load_tile(ta, kc, vc, t_a < t_end ? t_a : t_begin, lane, slot_mask, t_a < t_end, slice);
     load_tile(tb, kc, vc, t_b < t_end ? t_b : t_begin, lane, slot_mask, t_b < t_end, slice);
     __builtin_amdgcn_sched_barrier(0);
@@ -289,12 +299,12 @@ __global__ __launch_bounds__(DEC_THREADS) void attn_decode_kernel(const DecodePa
             sm_kv[1][lane + 64] = KT::to_float(v1);
             const int slot = pos & slot_mask;
             if (slice == 0) {  // one V slice writes the token's K/V (every slice computes them)
-            uint16_t *kw_ = k_cache + (size_t)seq * seq_stride;
-            kw_[kt_index(kvh, slot, lane, n_slots)] = k0;
-            kw_[kt_index(kvh, slot, lane + 64, n_slots)] = k1;
-            uint16_t *vw = v_cache + (size_t)seq * seq_stride;
-            vw[vt_index(kvh, slot, lane, n_slots)] = v0;
-            vw[vt_index(kvh, slot, lane + 64, n_slots)] = v1;
+                uint16_t *kw_ = k_cache + (size_t)seq * seq_stride;
+                kw_[kt_index(kvh, slot, lane, n_slots)] = k0;
+                kw_[kt_index(kvh, slot, lane + 64, n_slots)] = k1;
+                uint16_t *vw = v_cache + (size_t)seq * seq_stride;
+                vw[vt_index(kvh, slot, lane, n_slots)] = v0;
+                vw[vt_index(kvh, slot, lane + 64, n_slots)] = v1;
             }
         }
     }
@@ -308,8 +318,8 @@ __global__ __launch_bounds__(DEC_THREADS) void attn_decode_kernel(const DecodePa
         float dot = sm_q[wave][lane] * sm_kv[0][lane] + sm_q[wave][lane + 64] * sm_kv[0][lane + 64];
         dot = wave_sum(dot);
         if (lane == 0) {
-            sm_m[DEC_WAVES][wave] = dot;
-            sm_l[DEC_WAVES][wave] = 1.f;
+            sm_m[W][wave] = dot;
+            sm_l[W][wave] = 1.f;
         }
     }
 
@@ -324,17 +334,17 @@ __global__ __launch_bounds__(DEC_THREADS) void attn_decode_kernel(const DecodePa
     // are unconditional and the wait counts static (consuming a tile waits for its own
     // 16 loads only); the drain then handles the last two or three tiles, issuing no
     // load that will not be consumed except in the three-tile case.
-    while (t_b + 2 * DEC_WAVES < t_end) {
+    while (t_b + 2 * W < t_end) {
         consume_tile<DT, VS>(S, ta, qb, t_a, k_begin, pos, g, hl);
-        t_a += 2 * DEC_WAVES;
+        t_a += 2 * W;
         load_tile(ta, kc, vc, t_a, lane, slot_mask, true, slice);
         consume_tile<DT, VS>(S, tb, qb, t_b, k_begin, pos, g, hl);
-        t_b += 2 * DEC_WAVES;
+        t_b += 2 * W;
         load_tile(tb, kc, vc, t_b, lane, slot_mask, true, slice);
     }
     if (t_a < t_end) {
         consume_tile<DT, VS>(S, ta, qb, t_a, k_begin, pos, g, hl);
-        t_a += 2 * DEC_WAVES;
+        t_a += 2 * W;
         const bool third = t_a < t_end;
         // unconditional (16 bytes per load when there is no third tile): tile b's wait
         // stays exact while the third tile streams in
@@ -344,38 +354,43 @@ __global__ __launch_bounds__(DEC_THREADS) void attn_decode_kernel(const DecodePa
     }
 
     // ---- merge hi/lo columns and the waves (and the current token) through LDS ----
+    // (the lane's MFMA column and k-group are derived again here from the lane id, so that
+    // they hold no register during the stream)
+    const int lane2 = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+    asm volatile("" ::"v"(lane2));
+    const int n2 = lane2 & 15, g2 = lane2 >> 4, hloc2 = n2 & 7, hl2 = n2 >> 3;
     S.l = xor32_sum(xor16_sum(S.l));
 #pragma unroll
     for (int d = 0; d < 8 / VS; d++) {
         f32x4 v;
 #pragma unroll
         for (int r = 0; r < 4; r++) v[r] = S.acc[d][r] + lane_xor8(S.acc[d][r]);
-        if (hl == 0) *(f32x4 *)&sm_acc[wave][hloc][16 * d + 4 * g] = v;
+        if (hl2 == 0) *(f32x4 *)&sm_acc[wave][hloc2][16 * d + 4 * g2] = v;
     }
-    if (hl == 0 && g == 0) {
-        sm_m[wave][hloc] = S.m;
-        sm_l[wave][hloc] = S.l;
+    if (hl2 == 0 && g2 == 0) {
+        sm_m[wave][hloc2] = S.m;
+        sm_l[wave][hloc2] = S.l;
     }
     lds_barrier();
 
     // wave th merges head th: 8 wave partials + the current token, branch-free (a wave
     // without keys has m = -1e30 and l = 0, so its weight is 0). Lane pairs of dims d2, d2+1
     // of this V slice's 128/VS dims (with VS > 1 the upper lanes read unused LDS and store nothing)
-    const int th = wave, d2 = lane * 2, dg = HEAD_DIM / VS * slice + d2;
-    float mw[DEC_WAVES + 1], lw[DEC_WAVES + 1];
+    const int th = wave, d2 = lane2 * 2, dg = HEAD_DIM / VS * slice + d2;
+    float mw[W + 1], lw[W + 1];
 #pragma unroll
-    for (int w = 0; w < DEC_WAVES; w++) {
+    for (int w = 0; w < W; w++) {
         mw[w] = sm_m[w][th];
         lw[w] = sm_l[w][th];
     }
-    mw[DEC_WAVES] = last_split ? sm_m[DEC_WAVES][th] : -1e30f;
-    lw[DEC_WAVES] = last_split ? 1.f : 0.f;
+    mw[W] = last_split ? sm_m[W][th] : -1e30f;
+    lw[W] = last_split ? 1.f : 0.f;
     float M = mw[0];
 #pragma unroll
-    for (int w = 1; w <= DEC_WAVES; w++) M = fmaxf(M, mw[w]);
+    for (int w = 1; w <= W; w++) M = fmaxf(M, mw[w]);
     float L = 0.f, A0 = 0.f, A1 = 0.f;
 #pragma unroll
-    for (int w = 0; w < DEC_WAVES; w++) {
+    for (int w = 0; w < W; w++) {
         const float c = __builtin_amdgcn_exp2f(mw[w] - M);
         const float2 a = *(const float2 *)&sm_acc[w][th][d2];
         L += lw[w] * c;
@@ -383,8 +398,8 @@ __global__ __launch_bounds__(DEC_THREADS) void attn_decode_kernel(const DecodePa
         A1 += a.y * c;
     }
     if (last_split) {  // sm_kv is written only in the last split: elsewhere it is stale LDS
-        const float c = __builtin_amdgcn_exp2f(mw[DEC_WAVES] - M);
-        L += lw[DEC_WAVES] * c;
+        const float c = __builtin_amdgcn_exp2f(mw[W] - M);
+        L += lw[W] * c;
         A0 += sm_kv[1][dg & (HEAD_DIM - 1)] * c;
         A1 += sm_kv[1][(dg + 1) & (HEAD_DIM - 1)] * c;
     }
@@ -399,10 +414,10 @@ __global__ __launch_bounds__(DEC_THREADS) void attn_decode_kernel(const DecodePa
     if constexpr (VS > 1) return;  // not reached: V slices are planned for one split per sequence
     // partials of a launch: sequence s's splits start at split wg_base[s] / 4 of the launch,
     // and each head's splits are consecutive records
-    const int split0 = __builtin_amdgcn_readlane(t_base, seq) / N_HEAD_KV;
+    const int split0 = seq_base / N_HEAD_KV;
     float *pp = partial + ((size_t)split0 * N_HEAD + hout * n_split + split) * PART_STRIDE;
     *(float2 *)(pp + d2) = make_float2(A0, A1);
-    if (lane == 0) *(float2 *)(pp + HEAD_DIM) = make_float2(M, L);
+    if (lane2 == 0) *(float2 *)(pp + HEAD_DIM) = make_float2(M, L);
 }
 
 // The merge kernel's arguments: only what it reads (536 bytes instead of the decode kernel's
@@ -414,93 +429,75 @@ struct CombineParams {
     int split0[MAX_SEQ];   // first split record of sequence s
 };
 
-// LSE merge of the split partials plus the sink (fused.metal:331-350).
-// grid = (N_HEAD * DP, n_seq), 256 threads: workgroup (part qd, head hh) writes the 128/DP dims
-// from (128/DP)qd of head hh. Thread (split group sg, dim group dg) sums 4 of them over splits
-// sg, sg + SG, ...; thread t also holds (m, l) of splits t, t+256, ... All of it is requested at
-// once, so the merge waits on one memory round trip after the kernel arguments. With few
-// sequences, DP = 4 spreads the partial records' reads over 4x the CUs (one CU reads ~63 GB/s).
-template <int DP>
+// LSE merge of the split partials plus the sink (fused.metal:331-350), with no LDS and no
+// workgroup barrier. grid = (N_HEAD, n_seq), 4 waves: wave q writes dims 32q .. 32q + 31 of head
+// hh. Lane s takes split s of each chunk of 64 (its (m, l) and its 32 accumulators, all requested
+// at once, so the merge waits on one memory round trip after the kernel arguments); the chunk's
+// weights 2^(m_s - M) come from a wave max (splits with l = 0 are skipped, as in fused.metal), and
+// the 64 lanes' 32 weighted sums are reduced by a reduce-scatter over lane pairs (swaps across
+// the wave halves and rows, DPP within rows), which leaves dim lane / 2 in lanes 2d and 2d + 1.
+// (A 256-thread workgroup per head quarter, reducing through LDS with three barriers, measured
+// ~0.25 us slower per config-3 call.)
+__device__ inline float dpp_half_mirror(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), DPP_HALF_MIRROR, 0xf, 0xf, false));
+}
 __global__ __launch_bounds__(256) void attn_combine_kernel(const CombineParams P) {
-    constexpr int DG = HEAD_DIM / DP / 4;  // dim groups of 4
-    constexpr int SG = 256 / DG;           // split groups
-    constexpr int NX = 64 / SG;            // accumulators per thread per 64 splits
-    __shared__ float w_s[MERGE_MAX_SPLIT];
-    __shared__ float red[2][4];
-    __shared__ float4 part[4][DG];
-    // head fastest: the DP workgroups of a head are N_HEAD ids apart, so on one XCD (the hardware
-    // deals workgroup ids to the 8 XCDs round robin) and its L2 fetches the head's records once
-    const int hh = blockIdx.x % N_HEAD, qd = blockIdx.x / N_HEAD, seq = blockIdx.y, tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
+    const int hh = blockIdx.x, seq = blockIdx.y, lane = threadIdx.x & 63;
+    const int q = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int ns = P.n_split[seq], split0 = P.split0[seq];
     const float *const partial = P.partial, *const sinks = P.sinks;
     float *const att = P.att;
     pin_sgpr(ns), pin_sgpr(split0), pin_sgpr(partial), pin_sgpr(sinks), pin_sgpr(att);
     if (ns <= 1) return;  // written directly by the decode kernel
     const float *pp = partial + ((size_t)split0 * N_HEAD + hh * ns) * PART_STRIDE;
-    const int dg = tid % DG, sg = tid / DG;
-    const float *px = pp + (HEAD_DIM / DP) * qd + 4 * dg;
-    float4 x[NX];
-#pragma unroll
-    for (int i = 0; i < NX; i++) x[i] = *(const float4 *)(px + min(sg + SG * i, ns - 1) * PART_STRIDE);
-    float2 ml[MERGE_MAX_SPLIT / 256];
-#pragma unroll
-    for (int j = 0; j < MERGE_MAX_SPLIT / 256; j++)
-        ml[j] = *(const float2 *)(pp + min(tid + 256 * j, ns - 1) * PART_STRIDE + HEAD_DIM);
     const float sink = sinks[hh] * LOG2E;
-    float M = sink;
+    float M = sink, lsum = 0.f, acc[32];
 #pragma unroll
-    for (int j = 0; j < MERGE_MAX_SPLIT / 256; j++)
-        if (tid + 256 * j < ns && ml[j].y != 0.f) M = fmaxf(M, ml[j].x);
-    M = wave_max(M);
-    if (lane == 0) red[0][wave] = M;
-    __syncthreads();
-    M = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
-    float L = 0.f;
-#pragma unroll
-    for (int j = 0; j < MERGE_MAX_SPLIT / 256; j++) {
-        const int s = tid + 256 * j;
-        const float w = (s < ns && ml[j].y != 0.f) ? exp2f(ml[j].x - M) : 0.f;
-        if (s < ns) w_s[s] = w;
-        L += ml[j].y * w;
-    }
-    L = wave_sum(L);
-    if (lane == 0) red[1][wave] = L;
-    __syncthreads();
-    L = red[1][0] + red[1][1] + red[1][2] + red[1][3] + exp2f(sink - M);
-    float4 a = {0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < 32; j++) acc[j] = 0.f;
     for (int s0 = 0; s0 < ns; s0 += 64) {
-        if (s0 > 0) {
+        const bool live = s0 + lane < ns;
+        const float *rec = pp + (size_t)min(s0 + lane, ns - 1) * PART_STRIDE;
+        f32x4 a[8];
 #pragma unroll
-            for (int i = 0; i < NX; i++)
-                x[i] = *(const float4 *)(px + min(s0 + sg + SG * i, ns - 1) * PART_STRIDE);
-        }
+        for (int i = 0; i < 8; i++) a[i] = *(const f32x4 *)(rec + 32 * q + 4 * i);
+        const float2 ml = *(const float2 *)(rec + HEAD_DIM);
+        const bool use = live && ml.y != 0.f;  // splits without keys carry no weight
+        const float Mn = fmaxf(M, wave_max(use ? ml.x : -INFINITY));
+        const float scale = exp2f(M - Mn), w = use ? exp2f(ml.x - Mn) : 0.f;
+        lsum = lsum * scale + ml.y * w;
 #pragma unroll
-        for (int i = 0; i < NX; i++) {
-            const int sp = s0 + sg + SG * i;
-            const float w = sp < ns ? w_s[sp] : 0.f;
-            a.x += x[i].x * w; a.y += x[i].y * w; a.z += x[i].z * w; a.w += x[i].w * w;
-        }
+        for (int j = 0; j < 32; j++) acc[j] = acc[j] * scale + a[j >> 2][j & 3] * w;
+        M = Mn;
     }
-    // sum over the wave's split groups (lanes DG apart), then over the 4 waves
+    const float L = wave_sum(lsum) + exp2f(sink - M);
+    // reduce-scatter: 32 values per lane -> one dim per lane pair
 #pragma unroll
-    for (int o = DG; o < 64; o <<= 1) {
-        a.x += __shfl_xor(a.x, o, 64); a.y += __shfl_xor(a.y, o, 64);
-        a.z += __shfl_xor(a.z, o, 64); a.w += __shfl_xor(a.w, o, 64);
+    for (int j = 0; j < 16; j++) {  // lanes l and l ^ 32: dims j (lower half), j + 16 (upper)
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[j]), __float_as_uint(acc[j + 16]), false, false);
+        acc[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
     }
-    if (lane < DG) part[wave][lane] = a;
-    __syncthreads();
-    if (tid < DG) {
-        float4 t = part[0][tid];
 #pragma unroll
-        for (int i = 1; i < 4; i++) {
-            const float4 u = part[i][tid];
-            t.x += u.x; t.y += u.y; t.z += u.z; t.w += u.w;
-        }
-        const float inv = 1.0f / L;
-        *(float4 *)(att + (size_t)seq * Q_DIM + hh * HEAD_DIM + (HEAD_DIM / DP) * qd + 4 * tid) =
-            make_float4(t.x * inv, t.y * inv, t.z * inv, t.w * inv);
+    for (int j = 0; j < 8; j++) {  // lanes l and l ^ 16
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(acc[j]), __float_as_uint(acc[j + 8]), false, false);
+        acc[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
     }
+    const bool b3 = lane & 8, b2 = lane & 4, b1 = lane & 2;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {  // lanes l and l ^ 8 (rotation by 8 within a row of 16)
+        const float t0 = acc[j] + dpp<DPP_ROR8>(acc[j]), t1 = acc[j + 4] + dpp<DPP_ROR8>(acc[j + 4]);
+        acc[j] = b3 ? t1 : t0;
+    }
+#pragma unroll
+    for (int j = 0; j < 2; j++) {  // lanes l and 7 - l within each 8 (they differ in bit 2)
+        const float t0 = acc[j] + dpp_half_mirror(acc[j]), t1 = acc[j + 2] + dpp_half_mirror(acc[j + 2]);
+        acc[j] = b2 ? t1 : t0;
+    }
+    {  // lanes l and l ^ 2, then l ^ 1
+        const float t0 = acc[0] + dpp<DPP_QUAD_XOR2>(acc[0]), t1 = acc[1] + dpp<DPP_QUAD_XOR2>(acc[1]);
+        acc[0] = b1 ? t1 : t0;
+        acc[0] += dpp<DPP_QUAD_XOR1>(acc[0]);
+    }
+    if ((lane & 1) == 0) att[(size_t)seq * Q_DIM + hh * HEAD_DIM + 32 * q + (lane >> 1)] = acc[0] / L;
 }
 
 // Split partials of the entry point that allocates nothing (flint_attn_decode_batch_noalloc):
@@ -553,11 +550,7 @@ hipError_t launch_decode(const DecodeParams &P, int dtype, hipStream_t stream) {
             C.n_split[s] = s < P.n_seq ? P.n_split[s] : 0;
             C.split0[s] = s < P.n_seq ? P.wg_base[s] / N_HEAD_KV : 0;
         }
-        // four workgroups per head while that keeps the grid within two per CU
-        if (P.n_seq * N_HEAD * 4 <= 512)
-            hipLaunchKernelGGL(attn_combine_kernel<4>, dim3(N_HEAD * 4, P.n_seq), dim3(256), 0, stream, C);
-        else
-            hipLaunchKernelGGL(attn_combine_kernel<1>, dim3(N_HEAD, P.n_seq), dim3(256), 0, stream, C);
+        hipLaunchKernelGGL(attn_combine_kernel, dim3(N_HEAD, P.n_seq), dim3(256), 0, stream, C);
         e = hipGetLastError();
     }
     return e;

@@ -98,6 +98,8 @@ void validate_layer(const flint_attn_layer *L) {
     if (!L->q_norm || !L->k_norm || !L->sinks) throw Error("layer q_norm/k_norm/sinks pointer is NULL");
     if (L->kv_dtype != FLINT_KV_F16 && L->kv_dtype != FLINT_KV_BF16) throw Error("kv_dtype must be F16 or BF16");
     if (L->n_slots <= 0 || L->n_slots % 32 != 0) throw Error("n_slots must be a positive multiple of 32");
+    if (L->n_slots > FLINT_MAX_SLOTS)
+        throw Error("n_slots must be at most " + std::to_string(FLINT_MAX_SLOTS) + " (32-bit cache offsets)");
     if (L->window < 1) throw Error("window must be >= 1");
     if (((uintptr_t)L->q_norm | (uintptr_t)L->k_norm) & 15) throw Error("q_norm/k_norm must be 16-byte aligned");
     if (L->is_swa) {
@@ -627,6 +629,8 @@ flint_attn_engine *flint_attn_engine_create(int32_t n_layer, const uint8_t *is_s
     try {
         if (n_layer <= 0 || !is_swa || !has_rope) throw Error("engine: n_layer > 0 and the layer flags are required");
         if (n_ctx <= 0) throw Error("engine: n_ctx must be > 0");
+        if (n_ctx > FLINT_MAX_SLOTS)
+            throw Error("engine: n_ctx must be at most " + std::to_string(FLINT_MAX_SLOTS) + " (32-bit cache offsets)");
         if (kv_dtype != FLINT_KV_F16 && kv_dtype != FLINT_KV_BF16) throw Error("engine: kv_dtype must be F16 or BF16");
         auto e = std::make_unique<flint_attn_engine>();
         e->layers.resize(n_layer);

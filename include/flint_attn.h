@@ -21,6 +21,9 @@
  *   V: [N_HEAD_KV][n_slots/32][HEAD_DIM][32]   (V transposed within the tile)
  * SWA layers: n_slots is a power of two >= window (1024 for Flint) and
  * position p lives in slot p & (n_slots-1); full-attention layers: slot = p.
+ * n_slots is at most FLINT_MAX_SLOTS, so a kv head's K (or V) cache stays below 2^31 bytes
+ * and the kernels address it with 32-bit offsets (the reference's n_ctx bound,
+ * /root/reference/src/metal/flint_config.h:29-31, is far below it).
  * (The reference keeps position-major [slot][kv_head][128] for both,
  * /root/reference/src/engine.mm:509-511, fused.metal:275.)
  */
@@ -43,6 +46,7 @@ extern "C" {
 #define FLINT_QKV_DIM 5120 /* one raw q|k|v row: q 0..4095, k 4096..4607, v 4608..5119 */
 #define FLINT_N_SWA 513    /* SWA window, current token included */
 #define FLINT_SWA_RING 1024
+#define FLINT_MAX_SLOTS (1 << 23) /* slots per layer and kv head */
 
 /* KV cache element types. */
 #define FLINT_KV_F16 1
@@ -59,7 +63,7 @@ extern "C" {
 typedef struct {
     void *k_cache;        /* device, layout above (tiled K) */
     void *v_cache;        /* device, layout above (element (h, slot, d) at ((h*n_slots/32 + slot/32)*128 + d)*32 + slot%32) */
-    int32_t n_slots;      /* multiple of 32; SWA: power of two >= window */
+    int32_t n_slots;      /* multiple of 32, at most FLINT_MAX_SLOTS; SWA: power of two >= window */
     int32_t kv_dtype;     /* FLINT_KV_F16 or FLINT_KV_BF16 */
     int32_t is_swa;
     int32_t has_rope;

@@ -176,6 +176,9 @@ def _layer(**kw):
     (dict(n_slots=1000), "multiple of 32"),
     (dict(n_slots=992), "power of two"),
     (dict(n_slots=256), "must hold the window"),
+    # one slot past FLINT_MAX_SLOTS (a kv head's cache would reach 2^31 bytes), rejected before
+    # any launch: the pointers here are not device memory
+    (dict(is_swa=0, n_slots=(1 << 23) + 32), "at most 8388608"),
     (dict(kv_dtype=7), "kv_dtype"),
     (dict(k_cache=0), "KV cache pointer"),
     (dict(sinks=0), "sinks"),
@@ -227,6 +230,8 @@ def test_engine_create_rejects_bad_arguments():
     assert not L.flint_attn_engine_create(2, flags, flags, 0, 1, 1e4, err, len(err))
     assert not L.flint_attn_engine_create(2, flags, flags, 4096, 3, 1e4, err, len(err))
     assert b"kv_dtype" in err.value
+    assert not L.flint_attn_engine_create(2, flags, flags, (1 << 23) + 1, 1, 1e4, err, len(err))
+    assert b"at most 8388608" in err.value
     assert L.flint_attn_engine_n_layer(None) == 0
     assert not L.flint_attn_engine_layer(None, 0)
 
