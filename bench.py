@@ -10,7 +10,9 @@ Also on the same line:
   * a whole decode step of the attention stage at 32k, timed: Flint's 14 full (pos 32768)
     + 35 SWA layers back to back, each with its own cache (decode_step_49_layers_32k);
   * prefill attention at 4000 tokens (config 4, bf16 KV, full causal and SWA-513), with a
-    roofline object per layer kind;
+    roofline object per layer kind for the larger of its two floors (MFMA on the full layer,
+    HBM on the SWA layer, whose fp32 q in and output out outweigh its FLOPs), the other
+    fraction beside it;
   * the 16-sequence mixed-context decode (config 5);
   * the attention blocks read from a 49-layer GGUF model (q8_0 q/k/v/o projections +
     attention): one layer of each kind, a whole decode step at 32k, and the layer-major
@@ -190,6 +192,15 @@ def prefill_flops(T, window=None):
     return 4 * 32 * 128 * keys
 
 
+def prefill_bytes(T, ring=None, kv_bytes=2):
+    """Algorithmic HBM bytes of one prefill call from position 0: the fp32 q|k|v rows read
+    (q 4096 + k, v 512 + 512 floats per token), the fp32 attention output written, and the K/V
+    rows the cache keeps (all T on a full layer, the last `ring` on an SWA layer) in the cache
+    dtype."""
+    kept = min(T, ring) if ring else T
+    return T * (4096 + 1024) * 4 + T * 4096 * 4 + kept * 1024 * kv_bytes
+
+
 def bench_decode_32k(torch, fa, steps, warmup, n_layers=8, ctx=32768):
     import numpy as np
     dev = torch.device("cuda:0")
@@ -309,16 +320,27 @@ def bench_prefill(torch, fa, T=4000, reps=10, kinds=("full", "swa")):
                         sinks=rng.standard_normal(32), device=dev)
         ms, host_bound = queued_launch_ms(torch, lambda: kv.prefill(qkv, att, 0), reps)
         flops = prefill_flops(T, 513 if is_swa else None)
+        nbytes = prefill_bytes(T, 1024 if is_swa else None)
         tflops = flops / (ms * 1e-3) / 1e12
-        out[name] = dict(ms=ms, flops=flops, tflops=tflops, frac_of_mfma_peak=tflops / MFMA_PEAK_TFLOPS, host_bound=host_bound,
-                         roofline={"bound": "mfma", "achieved": round(tflops, 1), "peak": MFMA_PEAK_TFLOPS,
-                                   "unit": "TFLOP/s", "frac": round(tflops / MFMA_PEAK_TFLOPS, 4),
-                                   "traffic": PREFILL_TRAFFIC_BYTES[name],
-                                   "kernel": "one flint_attn_prefill call on a " + ("SWA-513" if is_swa else "full causal")
-                                             + " layer = kv_prep_kernel + flash_prefill_kernel (f16 MFMA 32x32x16 on "
-                                             "the exact f16 copy of the bf16 K/V); achieved = algorithmic FLOPs / "
-                                             "time per call from HIP events around calls queued behind a spin "
-                                             "kernel"})
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        # the call's two floors at the published peaks; the roofline object is the one of the larger
+        # floor (MFMA on a full causal layer, HBM on an SWA-513 layer), with the other fraction beside it
+        floor_us = {"mfma": flops / (MFMA_PEAK_TFLOPS * 1e12) * 1e6, "hbm": nbytes / (HBM_PEAK_GBS * 1e9) * 1e6}
+        mfma_frac, hbm_frac = tflops / MFMA_PEAK_TFLOPS, gbs / HBM_PEAK_GBS
+        kernel = ("one flint_attn_prefill call on a " + ("SWA-513" if is_swa else "full causal")
+                  + " layer = kv_prep_kernel + flash_prefill_kernel (f16 MFMA 32x32x16 on the exact f16 copy of "
+                  "the bf16 K/V); achieved = algorithmic FLOPs or bytes / time per call from HIP events around "
+                  "calls queued behind a spin kernel")
+        if floor_us["mfma"] >= floor_us["hbm"]:
+            roof = {"bound": "mfma", "achieved": round(tflops, 1), "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                    "frac": round(mfma_frac, 4), "hbm_frac": round(hbm_frac, 4)}
+        else:
+            roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(hbm_frac, 4), "mfma_frac": round(mfma_frac, 4)}
+        roof.update({"traffic": PREFILL_TRAFFIC_BYTES[name], "bytes_per_launch": nbytes, "flops_per_launch": flops,
+                     "floor_us": {k: round(v, 2) for k, v in floor_us.items()}, "kernel": kernel})
+        out[name] = dict(ms=ms, flops=flops, tflops=tflops, frac_of_mfma_peak=mfma_frac, gbs=gbs,
+                         frac_of_hbm_peak=hbm_frac, host_bound=host_bound, roofline=roof)
         del kv
     return out
 
