@@ -158,9 +158,10 @@ __global__ __launch_bounds__(256) void prefix_kernel(const PrefillParams P) {
 // kv_prep: the new tokens' K and V. grid (32-position chunks, kv head), 4 waves.
 // Chunk c holds positions 32 c0 + 32 c .. +31 (32-aligned, so it is one tile of the
 // attention copy, whose kbase is 32-aligned, and one tile of the cache). Wave w owns the 8
-// consecutive rows 8w .. 8w+7 (their addresses are wave-uniform, so scalar): it normalises
-// (+ RoPE) each row's k (lane = a NEOX pair of dims), rounds k and v to the cache dtype into
-// LDS (k row-major, v transposed), then writes every 16-byte unit those rows make: the copy's
+// consecutive rows 8w .. 8w+7, 8 lanes a row (16 dims a lane, so one RMSNorm scale per lane
+// serves 16 dims; the row-per-wave layout before it spent ~1 us more per call on per-row
+// reductions and divisions): it normalises (+ RoPE) each row's k, rounds k and v to the cache
+// dtype into LDS (k row-major, v transposed), then writes every 16-byte unit those rows make: the copy's
 // K units (one key, 8 dims) and V units (one dim, these 8 keys), scaled by the tile's
 // exponents, and the cache's units of the new positions it keeps. So an f16 chunk needs no
 // workgroup barrier (a bf16 chunk has one, for the tile's exponents). The first chunk also
@@ -181,36 +182,64 @@ __global__ __launch_bounds__(KP_THREADS) void kv_prep_kernel(const PrefillParams
     const int c0 = (P.p0 >> 5) + blockIdx.x, pos0 = 32 * c0;  // first position of the chunk
     const int lo = max(P.p0, pos0), hi = min(P.p0 + P.T, pos0 + 32);  // new positions [lo, hi)
     const int r0 = KP_ROWS * wave;  // this wave's rows r0 .. r0 + 7
-    const float2 kw = make_float2(P.k_norm[lane], P.k_norm[lane + 64]);
-    const float rf = P.rope_freq[lane];
-    // the rows' k and v: all loads first (rows outside [lo, hi) read the chunk's first new
-    // token, in range, and are not used), then the maths
-    float2 kx[KP_ROWS], vx[KP_ROWS];
+    // Lane (rr, q8) takes row r0 + rr, dims 32k + 4 q8 + j (k, j < 4): a row's sum of squares is a
+    // sum over its 8 lanes, each lane's RMSNorm scale serves its 16 dims, and a NEOX pair
+    // (d, d + 64) is (k, k + 2) of one lane. All loads first (rows outside [lo, hi) read the chunk's
+    // first new token, in range, and are zeroed), then the maths.
+    const int rr = lane >> 3, q8 = lane & 7, r = r0 + rr, pos = pos0 + r;
+    const bool is_new = pos >= lo && pos < hi;
+    const float *kr = P.qkv + (size_t)((is_new ? pos : lo) - P.p0) * P.q_stride + Q_DIM + kvh * HEAD_DIM + 4 * q8;
+    float4 kx[4], vx[4], kw[4], rf[2];
 #pragma unroll
-    for (int i = 0; i < KP_ROWS; i++) {
-        const int pos = pos0 + r0 + i, t = (pos >= lo && pos < hi ? pos : lo) - P.p0;  // wave-uniform
-        const float *kr = P.qkv + (size_t)t * P.q_stride + Q_DIM + kvh * HEAD_DIM;
-        kx[i] = make_float2(kr[lane], kr[lane + 64]);
-        vx[i] = make_float2(kr[KV_DIM + lane], kr[KV_DIM + lane + 64]);
+    for (int k = 0; k < 4; k++) kw[k] = *(const float4 *)(P.k_norm + 32 * k + 4 * q8);
+#pragma unroll
+    for (int k = 0; k < 2; k++) rf[k] = *(const float4 *)&P.rope_freq[32 * k + 4 * q8];
+#pragma unroll
+    for (int k = 0; k < 4; k++) kx[k] = *(const float4 *)(kr + 32 * k);
+#pragma unroll
+    for (int k = 0; k < 4; k++) vx[k] = *(const float4 *)(kr + KV_DIM + 32 * k);
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; k++) ss += kx[k].x * kx[k].x + kx[k].y * kx[k].y + kx[k].z * kx[k].z + kx[k].w * kx[k].w;
+    ss = lane8_sum(ss);
+    const float scale = 1.0f / sqrtf(ss / HEAD_DIM + P.rms_eps);  // as norm_rope_pair
+    float y[4][4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const float *x = &kx[k].x, *w = &kw[k].x;
+#pragma unroll
+        for (int j = 0; j < 4; j++) y[k][j] = x[j] * scale * w[j];
+    }
+    if (P.has_rope) {
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            const float *f = &rf[k].x;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                float cs, sn;
+                rope_sincos((float)pos * f[j], &sn, &cs);
+                const float x0 = y[k][j], x1 = y[k + 2][j];
+                y[k][j] = x0 * cs - x1 * sn;
+                y[k + 2][j] = x0 * sn + x1 * cs;
+            }
+        }
     }
     float mk = 0.f, mv = 0.f;  // this lane's largest |k| and |v| (bf16: they set the tile's exponents)
-    // Every row is computed as if new (rows outside [lo, hi) from the chunk's first new token)
-    // and selected afterwards: no branch between the rows, so their norm and RoPE chains
-    // interleave. Rows past the new positions are zero.
 #pragma unroll
-    for (int i = 0; i < KP_ROWS; i++) {
-        const int r = r0 + i, pos = pos0 + r;
-        const bool is_new = pos >= lo && pos < hi;
-        float cs = 1.f, sn = 0.f;
-        if (P.has_rope) rope_sincos((float)pos * rf, &sn, &cs);
-        const float2 k2 = norm_rope_pair(kx[i], kw, P.rms_eps, P.has_rope, cs, sn);
-        const uint16_t k0 = is_new ? KT::from_float(k2.x) : 0, k1 = is_new ? KT::from_float(k2.y) : 0;
-        const uint16_t v0 = is_new ? KT::from_float(vx[i].x) : 0, v1 = is_new ? KT::from_float(vx[i].y) : 0;
-        kl[r][lane] = k0, kl[r][lane + 64] = k1, vt[lane][r] = v0, vt[lane + 64][r] = v1;
-        if constexpr (DT == DT_BF16) {
-            mk = fmaxf(mk, fmaxf(fabsf(KT::to_float(k0)), fabsf(KT::to_float(k1))));
-            mv = fmaxf(mv, fmaxf(fabsf(KT::to_float(v0)), fabsf(KT::to_float(v1))));
+    for (int k = 0; k < 4; k++) {
+        const float *v = &vx[k].x;
+        uint16_t kh[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            kh[j] = is_new ? KT::from_float(y[k][j]) : 0;
+            const uint16_t vh = is_new ? KT::from_float(v[j]) : 0;
+            vt[32 * k + 4 * q8 + j][r] = vh;
+            if constexpr (DT == DT_BF16) {
+                mk = fmaxf(mk, fabsf(KT::to_float(kh[j])));
+                mv = fmaxf(mv, fabsf(KT::to_float(vh)));
+            }
         }
+        *(uint2 *)&kl[r][32 * k + 4 * q8] = make_uint2(pack2(kh[0], kh[1]), pack2(kh[2], kh[3]));
     }
     if (pos0 + r0 < lo) {  // wave-uniform
         // the first chunk of a continuation that starts inside a tile: its cached positions
