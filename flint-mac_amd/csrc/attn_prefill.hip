@@ -743,7 +743,10 @@ __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const Pref
             const float4 v = ob[r * 16 + (c ^ (r & 15))];
             if (t0 + r < P.T) {
                 float *dst = n_split == 1 ? P.att + (size_t)(t0 + r) * Q_DIM + hq * HEAD_DIM : part_row(t0 + r);
-                *(float4 *)(dst + 64 * half + 4 * c) = v;
+                // streaming stores: the output is not read again here, and left in the caches it
+                // would evict the K/V tiles the other workgroups of the XCD still read (measured
+                // 1.5-2.5 us faster per call on both layer kinds; q read the same way was slower)
+                __builtin_nontemporal_store(f32x4{v.x, v.y, v.z, v.w}, (f32x4 *)(dst + 64 * half + 4 * c));
             }
         }
     }
