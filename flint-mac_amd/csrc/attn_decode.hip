@@ -196,6 +196,7 @@ __global__ __launch_bounds__(DEC_THREADS) void attn_decode_kernel(const DecodePa
     //      more memory round trip on the critical path). The per-sequence tables arrive one
     //      entry per lane, so finding this workgroup's sequence costs no second round trip ----
     const int t_base = P.wg_base[lane], t_pos = P.pos[lane], t_tps = P.tps[lane], t_ns = P.n_split[lane];
+    const int t_s0 = P.split0[lane];
     const int n_seq = P.n_seq;
     const int is_swa = P.is_swa, has_rope = P.has_rope, window = P.window;
     const int n_slots = P.n_slots, slot_mask = P.slot_mask;
@@ -208,7 +209,7 @@ __global__ __launch_bounds__(DEC_THREADS) void attn_decode_kernel(const DecodePa
     pin_sgpr(n_slots), pin_sgpr(slot_mask), pin_sgpr(rms_eps), pin_sgpr(seq_stride);
     pin_sgpr(qkv), pin_sgpr(q_norm), pin_sgpr(k_norm), pin_sgpr(sinks), pin_sgpr(k_cache), pin_sgpr(v_cache);
     pin_sgpr(att), pin_sgpr(partial);
-    asm volatile("" ::"v"(t_base), "v"(t_pos), "v"(t_tps), "v"(t_ns));
+    asm volatile("" ::"v"(t_base), "v"(t_pos), "v"(t_tps), "v"(t_ns), "v"(t_s0));
 
     // The grid is flat and holds exactly the launch's work units: sequence s owns workgroups
     // wg_base[s] .. wg_base[s] + 4 VS n_split[s] - 1 (kv head fastest, then V slice, then
@@ -219,8 +220,8 @@ __global__ __launch_bounds__(DEC_THREADS) void attn_decode_kernel(const DecodePa
     const int seq = __builtin_popcountll(__builtin_amdgcn_ballot_w64(lane < n_seq && wid >= t_base)) - 1;
     const int n_split = __builtin_amdgcn_readlane(t_ns, seq), pos = __builtin_amdgcn_readlane(t_pos, seq);
     const int tps = __builtin_amdgcn_readlane(t_tps, seq);
-    const int seq_base = __builtin_amdgcn_readlane(t_base, seq);
-    const int local = wid - seq_base;
+    const int local = wid - __builtin_amdgcn_readlane(t_base, seq);
+    const int split0 = __builtin_amdgcn_readlane(t_s0, seq);  // this sequence's first partial record
     const int kvh = local & (N_HEAD_KV - 1), slice = (local / N_HEAD_KV) % VS, split = local / (N_HEAD_KV * VS);
     if (seq < 0 || split >= n_split) return;  // not reached: the host sizes the grid exactly
     const bool last_split = split == n_split - 1;
@@ -412,9 +413,8 @@ __global__ __launch_bounds__(DEC_THREADS) void attn_decode_kernel(const DecodePa
         return;
     }
     if constexpr (VS > 1) return;  // not reached: V slices are planned for one split per sequence
-    // partials of a launch: sequence s's splits start at split wg_base[s] / 4 of the launch,
-    // and each head's splits are consecutive records
-    const int split0 = seq_base / N_HEAD_KV;
+    // partials of a launch: sequence s's records start at split0[s], and each head's splits are
+    // consecutive records
     float *pp = partial + ((size_t)split0 * N_HEAD + hout * n_split + split) * PART_STRIDE;
     *(float2 *)(pp + d2) = make_float2(A0, A1);
     if (lane2 == 0) *(float2 *)(pp + HEAD_DIM) = make_float2(M, L);
@@ -548,7 +548,7 @@ hipError_t launch_decode(const DecodeParams &P, int dtype, hipStream_t stream) {
         C.att = P.att;
         for (int s = 0; s < MAX_SEQ; s++) {
             C.n_split[s] = s < P.n_seq ? P.n_split[s] : 0;
-            C.split0[s] = s < P.n_seq ? P.wg_base[s] / N_HEAD_KV : 0;
+            C.split0[s] = s < P.n_seq ? P.split0[s] : 0;
         }
         hipLaunchKernelGGL(attn_combine_kernel, dim3(N_HEAD, P.n_seq), dim3(256), 0, stream, C);
         e = hipGetLastError();

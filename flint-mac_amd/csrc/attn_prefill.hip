@@ -86,7 +86,7 @@ __device__ inline float block_max256(float x, float *red) {
 
 // A tile's exponents into the table, and the call's flag when the tile is scaled.
 __device__ inline void put_texp(const PrefillParams &P, int kvh, int row0, int eK, int eV) {
-    P.texp[kvh * (P.k_rows >> 5) + (row0 >> 5)] = (eK & 0xffff) | (eV << 16);
+    P.texp[kvh * (P.k_rows >> 5) + ((row0 - 32 * P.n_direct) >> 5)] = (eK & 0xffff) | (eV << 16);
     if (eK | eV) __hip_atomic_store(&g_scaled_call, P.call_id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -106,12 +106,13 @@ __global__ __launch_bounds__(256) void prefix_kernel(const PrefillParams P) {
     __shared__ float red[2][4];
     const int kvh = blockIdx.y, tid = threadIdx.x;
     const int row0 = 32 * (P.n_direct + (int)blockIdx.x), pos0 = P.kbase + row0;  // the tile's first position
+    const int crow = row0 - 32 * P.n_direct;  // its row in the copy, which starts at tile n_direct
     if (pos0 + 32 > P.p0) {  // the tile holding p0: raw values of positions [pos0, p0)
         uint16_t *raw = (uint16_t *)P.sk;
         for (int i = tid; i < (P.p0 - pos0) * HEAD_DIM; i += 256) {
             const int r = i >> 7, d = i & 127, slot = (pos0 + r) & P.cache_mask;
-            raw[pk_index(kvh, row0 + r, d, P.k_rows)] = P.cache_k[kt_index(kvh, slot, d, P.n_slots)];
-            raw[pv_index(kvh, row0 + r, d, P.k_rows)] = P.cache_v[vt_index(kvh, slot, d, P.n_slots)];
+            raw[pk_index(kvh, crow + r, d, P.k_rows)] = P.cache_k[kt_index(kvh, slot, d, P.n_slots)];
+            raw[pv_index(kvh, crow + r, d, P.k_rows)] = P.cache_v[vt_index(kvh, slot, d, P.n_slots)];
         }
         return;
     }
@@ -148,9 +149,9 @@ __global__ __launch_bounds__(256) void prefix_kernel(const PrefillParams P) {
         // K cache unit (st*4 + c)*64 + 16g + n: key 8(n>>2) + 4st + (n&3), dims 32c + 8g .. +7
         const int st = u >> 8, c = (u >> 6) & 3, g = (u >> 4) & 3, n = u & 15;
         const int r = 8 * (n >> 2) + 4 * st + (n & 3);
-        *(f16x8 *)(P.sk + pk_index(kvh, row0 + r, 32 * c + 8 * g, P.k_rows)) = k8;
+        *(f16x8 *)(P.sk + pk_index(kvh, crow + r, 32 * c + 8 * g, P.k_rows)) = k8;
         // V cache unit 4d + g: dim d, keys 8g .. 8g+7
-        *(f16x8 *)(P.sk + pv_index(kvh, row0 + 8 * (u & 3), u >> 2, P.k_rows)) = v8;
+        *(f16x8 *)(P.sk + pv_index(kvh, crow + 8 * (u & 3), u >> 2, P.k_rows)) = v8;
     }
 }
 
@@ -248,7 +249,7 @@ __global__ __launch_bounds__(KP_THREADS) void kv_prep_kernel(const PrefillParams
         const uint16_t *raw = (const uint16_t *)P.sk;
 #pragma unroll
         for (int i = 0; i < KP_ROWS; i++) {
-            const int r = r0 + i, row = pos0 + r - P.kbase;
+            const int r = r0 + i, row = pos0 + r - P.kbase - 32 * P.n_direct;  // the copy starts at tile n_direct
             if (pos0 + r < lo) {
                 const uint16_t k0 = raw[pk_index(kvh, row, lane, P.k_rows)];
                 const uint16_t k1 = raw[pk_index(kvh, row, lane + 64, P.k_rows)];
@@ -278,7 +279,8 @@ __global__ __launch_bounds__(KP_THREADS) void kv_prep_kernel(const PrefillParams
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
-    const int row0 = pos0 - P.kbase;  // attention-copy row of the chunk's first position
+    const int row0 = pos0 - P.kbase;  // the chunk's first position, from kbase
+    const int crow = row0 - 32 * P.n_direct;  // its attention-copy row (the copy starts at tile n_direct)
     if (threadIdx.x == 0) put_texp(P, kvh, row0, eK, eV);
     const int clo = max(lo, P.cache_from);         // positions [clo, hi) go to the cache
     const bool to_cache = hi > clo;
@@ -293,7 +295,7 @@ __global__ __launch_bounds__(KP_THREADS) void kv_prep_kernel(const PrefillParams
             f16x8 v;
 #pragma unroll
             for (int e = 0; e < 8; e++) v[e] = (_Float16)__builtin_amdgcn_ldexpf(KT::to_float(kv[e]), -eK);
-            *(f16x8 *)(P.sk + pk_index(kvh, row0 + r, d0, P.k_rows)) = v;
+            *(f16x8 *)(P.sk + pk_index(kvh, crow + r, d0, P.k_rows)) = v;
             if (to_cache && pos0 + r >= clo && pos0 + r < hi)
                 *(u16x8 *)(P.cache_k + kt_index(kvh, 32 * ctile + r, d0, P.n_slots)) = kv;
         }
@@ -303,7 +305,7 @@ __global__ __launch_bounds__(KP_THREADS) void kv_prep_kernel(const PrefillParams
             f16x8 v;
 #pragma unroll
             for (int e = 0; e < 8; e++) v[e] = (_Float16)__builtin_amdgcn_ldexpf(KT::to_float(vv[e]), -eV);
-            *(f16x8 *)(P.sk + pv_index(kvh, row0 + r0, j, P.k_rows)) = v;
+            *(f16x8 *)(P.sk + pv_index(kvh, crow + r0, j, P.k_rows)) = v;
             if (to_cache) {
                 uint16_t *dst = P.cache_v + vt_index(kvh, 32 * ctile + r0, j, P.n_slots);
                 if (pos0 + r0 >= clo && pos0 + r0 + 8 <= hi) {  // wave-uniform
@@ -464,7 +466,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const Pref
         }
         const bool dir = t < n_direct;  // wave-uniform
         const size_t ct = (size_t)ctile0 + (((kbase + 32 * t) & cmask) >> 5);
-        const uint16_t *kb = dir ? ck + ct * (32 * HEAD_DIM) : (const uint16_t *)skv + (size_t)t * (PF_TILE_UNITS * 8);
+        const uint16_t *kb = dir ? ck + ct * (32 * HEAD_DIM) : (const uint16_t *)skv + (size_t)(t - n_direct) * (PF_TILE_UNITS * 8);
         const uint16_t *vb = dir ? cv + ct * (32 * HEAD_DIM) : kb + PF_TILE_UNITS * 4;
         const int ok = dir ? dk : 8 * tid, ov = dir ? dv : 8 * tid;
         static_assert(PF_UNITS_PER_THREAD == 2, "one K and one V unit per thread");
@@ -590,7 +592,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const Pref
             for (int st = 0; st < 8; st++) kf[st] = ring[0][st][lane];
 #pragma unroll
             for (int i = 0; i < 8; i++) vf[i] = ring[0][8 + i][lane];
-            const int tx = t < n_direct ? 0 : te[t];  // wave-uniform (cache tiles: unscaled f16)
+            const int tx = t < n_direct ? 0 : te[t - n_direct];  // wave-uniform (cache tiles: unscaled f16)
             const int eK = (int)(int16_t)(tx & 0xffff), eV = tx >> 16;
             f32x16 sc = pf_scores(kf, qf, f32x16{});
             const float ssc = __builtin_amdgcn_ldexpf(1.f, eK + eQ);

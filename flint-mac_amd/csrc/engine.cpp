@@ -197,23 +197,27 @@ void decode_impl(const flint_attn_layer *L, int n_seq, int64_t seq_stride, const
     // workgroup per kv head, 6.3 with 2, 5.7 with 4; 16 sequences: 9.8, 9.6, 9.1 us.
     P.v_slices = max_split > 1 ? 1 : n_seq * N_HEAD_KV * 4 <= 256 ? 4 : n_seq * N_HEAD_KV * 2 <= 256 ? 2 : 1;
     P.wg_base[0] = 0;
+    int n_records = 0;  // partial records (in splits) of the launch: sequences of more than one split
     for (int s = 0; s < n_seq; s++) {
         P.pos[s] = pos[s];
         P.wg_base[s + 1] = P.wg_base[s] + N_HEAD_KV * P.v_slices * P.n_split[s];
+        P.split0[s] = n_records;
+        if (P.n_split[s] > 1) n_records += P.n_split[s];
     }
     for (int s = n_seq + 1; s <= MAX_SEQ; s++) P.wg_base[s] = P.wg_base[n_seq];
     P.max_split = max_split;
     if (max_split > 1024) throw Error("too many key splits (max 1024): raise keys_per_split");
     if (max_split > 1) {
-        // one record per (split, head) of the launch (v_slices is 1 here: 4 workgroups a split)
-        const size_t need = (size_t)(P.wg_base[n_seq] / N_HEAD_KV) * N_HEAD * PART_STRIDE * sizeof(float);
+        // one record per (split, head) of the sequences with more than one split
+        const size_t need = (size_t)n_records * N_HEAD * PART_STRIDE * sizeof(float);
         if (no_alloc) {
             if (need > DECODE_SCRATCH_BYTES)
                 throw Error("flint_attn_decode_batch_noalloc: the split plan needs " + std::to_string(need) +
                             " bytes of partials, more than the " + std::to_string(DECODE_SCRATCH_BYTES) +
                             " bytes this entry point holds (" +
                             std::to_string(DECODE_SCRATCH_BYTES / (N_HEAD * PART_STRIDE * sizeof(float))) +
-                            " key splits over the batch): use fewer sequences or a larger keys_per_split");
+                            " key splits over the batch's sequences of more than one split): use fewer "
+                            "sequences or a larger keys_per_split");
             check(decode_scratch(&P.partial), "decode scratch address");
         } else {
             P.partial = (float *)scratch().partial.get(need);
@@ -256,13 +260,6 @@ void prefill_impl(const flint_attn_layer *L, const float *qkv, int q_stride, int
         P.cache_from = p0;
         P.kbase = 0;
     }
-    P.k_rows = ((p0 + T - P.kbase) + PREFILL_ROW_ALIGN - 1) / PREFILL_ROW_ALIGN * PREFILL_ROW_ALIGN;
-    // the attention copy, then its table of per-tile exponents (every tile the flash kernel reads
-    // is written in this call, padding rows included)
-    const size_t copy_bytes = (size_t)N_HEAD_KV * P.k_rows * 2 * HEAD_DIM * sizeof(_Float16);
-    char *ws = (char *)scratch().kv.get(copy_bytes + (size_t)N_HEAD_KV * (P.k_rows / 32) * sizeof(int));
-    P.sk = (_Float16 *)ws;
-    P.texp = (int *)(ws + copy_bytes);
     // f16 caches: whole tiles of cached positions are read in place instead of converted into the
     // copy, for short calls (T <= 256). The flash kernel that can read cache tiles runs its loop
     // ~7% slower, which at 32768 cached positions equals the conversion it saves at T ~ 512
@@ -272,6 +269,14 @@ void prefill_impl(const flint_attn_layer *L, const float *qkv, int q_stride, int
     // window (masked keys).
     if (L->kv_dtype == FLINT_KV_F16 && T <= 256 && (!L->is_swa || T <= L->n_slots - L->window + 1))
         P.n_direct = (p0 - P.kbase) >> 5;
+    // the attention copy holds the positions from tile n_direct on, then its table of per-tile
+    // exponents (every tile the flash kernel reads from it is written in this call, padding
+    // rows included): a short call at a long context needs only its own few tiles
+    P.k_rows = ((p0 + T - P.kbase - 32 * P.n_direct) + PREFILL_ROW_ALIGN - 1) / PREFILL_ROW_ALIGN * PREFILL_ROW_ALIGN;
+    const size_t copy_bytes = (size_t)N_HEAD_KV * P.k_rows * 2 * HEAD_DIM * sizeof(_Float16);
+    char *ws = (char *)scratch().kv.get(copy_bytes + (size_t)N_HEAD_KV * (P.k_rows / 32) * sizeof(int));
+    P.sk = (_Float16 *)ws;
+    P.texp = (int *)(ws + copy_bytes);
     // a nonzero id per call: the kernels flag a call that stored scaled tiles with its id
     static std::atomic<uint32_t> next_call{0};
     uint32_t id = ++next_call;
@@ -364,13 +369,16 @@ void check_tokens(int n_tok, const char *name) {
 
 // A batch of T tokens through one projection on the matrix cores (proj_gemm.hip): the weight
 // rows of the segments and the activation rows as f16 hi/lo planes in the device workspace, then
-// y[t][0:N] (+)= W x[t] (x RMSNorm'd with norm_w when given).
-// pl: the weights' planes, kept by the caller (then no weight prep here); T = 0 only builds them
-// into *pl
+// y[t][0:N] (+)= W x[t] (x RMSNorm'd with norm_w when given). The tokens go through in passes of
+// at most GEMM_PASS_TOKENS, so the workspace has a fixed ceiling (the weight planes once, built in
+// the first pass, and one pass's activation planes).
+// pl: the weights' planes, kept by the caller (then no weight prep here); build_only: only build
+// them into *pl
 void proj_gemm(const MatvecSeg *seg, int n_seg, int N, int K, const float *x, long long x_stride, const float *norm_w,
                float eps, int T, float *y, long long y_stride, int add, const WeightPlanes *pl, hipStream_t stream,
                bool build_only = false) {
-    const int T_pad = build_only ? 0 : (T + GEMM_TILE - 1) / GEMM_TILE * GEMM_TILE;
+    const int T_pass = build_only ? 0 : std::min(T, GEMM_PASS_TOKENS);
+    const int T_pad = (T_pass + GEMM_TILE - 1) / GEMM_TILE * GEMM_TILE;
     const size_t wbytes = pl ? 0 : (size_t)N * K * sizeof(_Float16), xbytes = (size_t)T_pad * K * sizeof(_Float16);
     size_t off = 0;
     auto take = [&](size_t b) {
@@ -388,24 +396,34 @@ void proj_gemm(const MatvecSeg *seg, int n_seg, int N, int K, const float *x, lo
     W.wl = pl ? pl->wl : (_Float16 *)(ws + o_wl);
     W.fexp = pl ? pl->fexp : (int *)(ws + o_f);
     GemmActParams X{};
-    X.x = x;
-    X.x_stride = x_stride;
     X.norm_w = norm_w;
     X.eps = eps;
-    X.T = T;
-    X.T_pad = T_pad;
     X.xh = (_Float16 *)(ws + o_xh);
     X.xl = (_Float16 *)(ws + o_xl);
     X.eexp = (int *)(ws + o_e);
     GemmParams G{};
     G.wh = W.wh, G.wl = W.wl, G.fexp = W.fexp, G.xh = X.xh, G.xl = X.xl, G.eexp = X.eexp;
-    G.y = y;
-    G.y_stride = y_stride;
     G.add = add;
     G.N = N;
     G.K = K;
-    G.T = T;
-    check(launch_proj_gemm(W, X, G, !pl || build_only, stream), "projection GEMM launch");
+    if (build_only) {
+        X.x = x, X.x_stride = x_stride, X.T = 0, X.T_pad = 0;
+        G.y = y, G.y_stride = y_stride, G.T = 0;
+        check(launch_proj_gemm(W, X, G, true, stream), "projection GEMM launch");
+        return;
+    }
+    for (int t0 = 0; t0 < T; t0 += GEMM_PASS_TOKENS) {
+        const int n = std::min(GEMM_PASS_TOKENS, T - t0);
+        X.x = x + (size_t)t0 * x_stride;
+        X.x_stride = x_stride;
+        X.T = n;
+        X.T_pad = (n + GEMM_TILE - 1) / GEMM_TILE * GEMM_TILE;
+        G.y = y + (size_t)t0 * y_stride;
+        G.y_stride = y_stride;
+        G.T = n;
+        // the weight planes are built once, in the first pass, unless the caller keeps them
+        check(launch_proj_gemm(W, X, G, !pl && t0 == 0, stream), "projection GEMM launch");
+    }
 }
 
 // the GEMM takes batches of GEMM_MIN_TOKENS and more whose output rows are 16-byte aligned

@@ -23,8 +23,8 @@ struct DecodeParams {
     uint16_t *v_cache;          // sequence 0: [4][n_slots/32][128][32] (V^T in 32-slot tiles)
     long long seq_stride;       // elements between two sequences' K (and V) caches
     float *att;                 // [n_seq][4096]
-    float *partial;             // [sum of n_split][32][132]: sequence s's splits start at split
-                                // wg_base[s] / 4, and each head's splits are consecutive records
+    float *partial;             // [sum of n_split over sequences of more than one split][32][132]:
+                                // sequence s's records start at split0[s], each head's consecutive
     int n_slots;                // slots per kv head
     int slot_mask;              // SWA: n_slots - 1 (power of two); full: all ones
     int is_swa, has_rope, window, max_split;
@@ -35,6 +35,8 @@ struct DecodeParams {
     int n_split[MAX_SEQ];       // key splits of sequence s
     int tps[MAX_SEQ];           // 32-key tiles per split of sequence s
     int wg_base[MAX_SEQ + 1];   // first workgroup of sequence s (4 x v_slices per split); [n_seq] = grid size
+    int split0[MAX_SEQ];        // first partial record (in splits) of sequence s: the splits of the
+                                // sequences before it that have more than one (one split needs none)
     int v_slices;               // 1, or 2 / 4 when every sequence has one split: a head's 128 output
                                 // dims in that many workgroups (each reads all of K and its part of V)
 };
@@ -61,11 +63,13 @@ struct PrefillParams {
     uint16_t *cache_k, *cache_v;
     int n_slots, cache_mask, cache_from;
     // attention copy (f16, pk_index / pv_index layouts) of key positions
-    // kbase .. p0 + T - 1 at rows 0 .., k_rows rows per kv head (multiple of PREFILL_ROW_ALIGN)
+    // kbase + 32 n_direct .. p0 + T - 1 at rows 0 .., k_rows rows per kv head (multiple of
+    // PREFILL_ROW_ALIGN): position p is copy row p - kbase - 32 n_direct
     _Float16 *sk;
     int k_rows, kbase;
     // per kv head and 32-key tile of the copy: the power-of-two exponents its K and V values
-    // were scaled by to fit f16, (eK & 0xffff) | eV << 16 ([4][k_rows / 32]; 0 = stored as is)
+    // were scaled by to fit f16, (eK & 0xffff) | eV << 16 ([4][k_rows / 32], indexed like the
+    // copy's tiles; 0 = stored as is)
     int *texp;
     // tiles 0 .. n_direct - 1 of the copy's range (whole tiles of cached positions) are read by
     // the flash kernel from the cache itself and neither copied nor given exponents: set for f16
@@ -141,6 +145,7 @@ struct GemmParams {
 };
 constexpr int GEMM_TILE = 128;       // tokens and rows per gemm3 workgroup
 constexpr int GEMM_MIN_TOKENS = 16;  // batches from this size take the GEMM
+constexpr int GEMM_PASS_TOKENS = 8192;  // tokens per GEMM pass (a multiple of GEMM_TILE): bounds the workspace
 // prep_weights = false: W's planes already hold the rows (built earlier and kept by the caller)
 hipError_t launch_proj_gemm(const GemmWeightParams &W, const GemmActParams &X, const GemmParams &G, bool prep_weights,
                             hipStream_t stream);

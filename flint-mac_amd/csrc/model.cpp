@@ -160,9 +160,13 @@ struct flint_attn_model {
     int32_t n_ctx = 0, pos = 0;  // the session: context length and tokens processed
     // The prefill GEMMs' f16 hi/lo planes of every layer's q|k|v and o weights (75.5 MB a layer),
     // one allocation made at the first prefill block that takes the GEMM; a layer's planes are built
-    // on the stream of its first such block and read by every later one.
+    // on the stream of its first such block and read by every later one. planes_on: the caller's
+    // switch (flint_attn_model_set_weight_planes). A failed allocation is tried once per prefill
+    // call (planes_failed_call: the call it failed in), and the projections rebuild the planes in
+    // the workspace meanwhile.
     void *planes = nullptr;
-    bool planes_failed = false;  // the allocation failed once: prefill rebuilds them per call instead
+    bool planes_on = true;
+    uint64_t prefill_call = 0, planes_failed_call = 0;
     std::vector<uint8_t> planes_built;
     // Engine::last_gpu_ms and its profiler (enable_profiling / last_profile, engine.h:54-56, 63):
     // marks are HIP events recorded on the call's stream, mark 0 where a step or prefill starts,
@@ -189,14 +193,16 @@ struct flint_attn_model {
     // the layer's q|k|v and o planes, built on `stream` if this is the first use; false when
     // there is no memory for them
     bool layer_planes(int il, hipStream_t stream, WeightPlanes *pq_out, WeightPlanes *po_out) {
-        if (planes_failed) return false;
+        if (!planes_on) return false;
         if (!planes) {
+            if (planes_failed_call == prefill_call) return false;  // already failed in this call
             if (hipMalloc(&planes, layers.size() * layer_planes_bytes()) != hipSuccess) {
                 (void)hipGetLastError();  // clear the allocation error; the projections work without planes
                 planes = nullptr;
-                planes_failed = true;
+                planes_failed_call = prefill_call;
                 return false;
             }
+            planes_failed_call = 0;
             planes_built.assign(layers.size(), 0);
         }
         char *base = (char *)planes + (size_t)il * layer_planes_bytes();
@@ -430,7 +436,32 @@ int32_t flint_attn_model_block_decode(flint_attn_model *m, int32_t il, float *x,
 
 int32_t flint_attn_model_block_prefill(flint_attn_model *m, int32_t il, float *X, int32_t p0, int32_t T,
                                        float *att, void *stream, char *err, int32_t err_len) {
-    return guarded(err, err_len, [&] { block_prefill(m, il, X, p0, T, att, stream, false); });
+    return guarded(err, err_len, [&] {
+        if (m) m->prefill_call++;
+        block_prefill(m, il, X, p0, T, att, stream, false);
+    });
+}
+
+int32_t flint_attn_model_set_weight_planes(flint_attn_model *m, int32_t on, char *err, int32_t err_len) {
+    return guarded(err, err_len, [&] {
+        if (!m) throw std::runtime_error("set_weight_planes: no model");
+        m->planes_on = on != 0;
+        m->planes_failed_call = 0;
+        if (!m->planes_on && m->planes) {
+            // the planes may still be read by work queued on any stream
+            check(hipDeviceSynchronize(), "set_weight_planes: device synchronize");
+            check(hipFree(m->planes), "set_weight_planes: free");
+            m->planes = nullptr;
+            m->planes_built.clear();
+        }
+    });
+}
+
+int32_t flint_attn_model_weight_planes(const flint_attn_model *m) {
+    if (!m) return -2;
+    if (!m->planes_on) return 0;
+    if (m->planes) return 1;
+    return m->planes_failed_call ? -1 : 2;
 }
 
 int32_t flint_attn_model_enable_profiling(flint_attn_model *m, int32_t on) {
@@ -503,6 +534,7 @@ int32_t flint_attn_model_prefill(flint_attn_model *m, const int32_t *tokens, int
         if (!tokens || n <= 0) throw std::runtime_error("prefill: empty");
         if (!X) throw std::runtime_error("prefill: X is NULL");
         if ((int64_t)m->pos + n > m->n_ctx) throw std::runtime_error("prefill: context full");
+        m->prefill_call++;
         const hipStream_t s = (hipStream_t)stream;
         const bool prof = m->profiling;
         const auto t0 = std::chrono::steady_clock::now();

@@ -102,6 +102,8 @@ _SIGS = {
     "flint_attn_model_step": (_i32, [_vp, _i32, _vp, _vp, _cp, _i32]),
     "flint_attn_model_prefill": (_i32, [_vp, _i32p, _i32, _vp, _vp, _cp, _i32]),
     "flint_attn_model_enable_profiling": (_i32, [_vp, _i32]),
+    "flint_attn_model_set_weight_planes": (_i32, [_vp, _i32, _cp, _i32]),
+    "flint_attn_model_weight_planes": (_i32, [_vp]),
     "flint_attn_model_last_gpu_ms": (ctypes.c_double, [_vp]),
     "flint_attn_model_last_encode_ms": (ctypes.c_double, [_vp]),
     "flint_attn_model_last_profile": (_i32, [_vp, _cp, _i32, ctypes.POINTER(ctypes.c_double), _i32]),
@@ -307,6 +309,16 @@ class Model:
             self.h = None
 
     __del__ = close
+
+    def set_weight_planes(self, on=True):
+        """Keep the prefill projections' weight planes (the default) or free them
+        (flint_attn_model_set_weight_planes)."""
+        _call(lib().flint_attn_model_set_weight_planes, self.h, 1 if on else 0)
+
+    def weight_planes(self):
+        """1 kept, 2 allowed and not allocated yet, 0 off, -1 the last allocation failed
+        (flint_attn_model_weight_planes)."""
+        return lib().flint_attn_model_weight_planes(self.h)
 
     def enable_profiling(self, on=True):
         """Later steps and prefills time each stage (Engine::enable_profiling;

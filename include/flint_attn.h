@@ -105,9 +105,10 @@ int32_t flint_attn_decode_batch(const flint_attn_layer *layer, int32_t n_seq, in
  * graph capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in
  * the reference. It takes the same arguments and launches the same kernels, and allocates
  * nothing: the key-split partials live in a static 4 MiB device array of the library, one
- * per GPU, held until the process ends. That holds 248 key splits over the batch (the
- * built-in plan uses about 48 over all sequences; one split needs no partials); a plan that
- * needs more is rejected with an error before any launch. Every call on a GPU shares that
+ * per GPU, held until the process ends. That holds 248 key splits, counted over the batch's
+ * sequences that take more than one (the built-in plan uses about 48 over all sequences; a
+ * sequence of one split needs no partials); a plan that needs more is rejected with an error
+ * before any launch. Every call on a GPU shares that
  * GPU's array, so calls that overlap on one GPU (on two streams, or from two threads) race.
  */
 int32_t flint_attn_decode_batch_noalloc(const flint_attn_layer *layer, int32_t n_seq, int64_t seq_stride,

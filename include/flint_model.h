@@ -88,6 +88,20 @@ int32_t flint_attn_model_block_prefill(flint_attn_model *m, int32_t il, float *X
                                        float *att, void *stream, char *err, int32_t err_len);
 
 /*
+ * The prefill projections' kept weight planes (no counterpart in the reference): from the first
+ * prefill block of 16 or more tokens, a model keeps every layer's q|k|v and o weights as f16
+ * hi/lo planes in one device allocation (75.5 MB a layer, 3.7 GB for Flint's 49), so later
+ * prefill blocks skip their per-call weight prep. on = 0 frees them (after a device
+ * synchronize) and prefill rebuilds the planes in its workspace on every call; on = 1 (the
+ * default) allows them again. When the allocation fails, prefill goes on without them and
+ * tries again in its next call. 0 / -1.
+ */
+int32_t flint_attn_model_set_weight_planes(flint_attn_model *m, int32_t on, char *err, int32_t err_len);
+/* 1: planes kept; 2: allowed, not allocated yet; 0: switched off; -1: allowed, but the last
+ * allocation failed (the projections rebuild the planes per call); -2: no model. */
+int32_t flint_attn_model_weight_planes(const flint_attn_model *m);
+
+/*
  * The model as one session over its attention blocks, as the reference's Engine drives its
  * layers (/root/reference/src/engine.h:24-79). The position is the number of tokens processed.
  * With the FFN half outside this library, the hidden state these calls return is that of the

@@ -160,6 +160,8 @@ def test_capi_null_handle_paths():
     assert not L.flint_logits(None)
     # the model session's timing calls (Engine::last_gpu_ms / enable_profiling / last_profile)
     assert L.flint_attn_model_enable_profiling(None, 1) == -1
+    assert L.flint_attn_model_set_weight_planes(None, 0, None, 0) == -1
+    assert L.flint_attn_model_weight_planes(None) == -2
     assert L.flint_attn_model_last_gpu_ms(None) == -1.0
     assert L.flint_attn_model_last_encode_ms(None) == -1.0
     assert L.flint_attn_model_last_profile(None, None, 0, None, 0) == -1

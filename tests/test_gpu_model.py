@@ -141,6 +141,57 @@ def test_block_prefill_matches_oracle_and_decode(setup, cuda):
     model2.close()
 
 
+def test_block_prefill_600_tokens(cuda, tmp_path):
+    """A longer layer-major prefill (a model of the same layers with 600 positions): 600 tokens
+    through layer 0 and then layer 1 in one call each, so the projections run over five
+    128-token tiles and the flash kernel over 19 query blocks (and the 100-token window slides
+    over many). Each layer within the bars on its own input, and the hidden state end to end."""
+    import torch
+    m = mb.make_model(n_pos=600)
+    path = str(tmp_path / "blocks600.gguf")
+    mb.write_model(path, m)
+    embd = m["embd"].astype(np.float32)
+    blocks = mb.oracle_blocks(m, "f16")
+    n = embd.shape[0]
+    model = fa.Model(path, n_ctx=1024)
+    X = torch.zeros((n, 2048), device=cuda)
+    A = torch.zeros((2, n, 4096), device=cuda)
+    model.embed(list(range(n)), X)
+    for il in range(2):
+        x_in = X.cpu().numpy()
+        model.block_prefill(il, X, 0, A[il])
+        torch.cuda.synchronize()
+        _check_layer(blocks[il], x_in, X.cpu().numpy(), A[il].cpu().numpy(), f"600-token prefill layer {il}")
+    hidden, _ = fo.block_forward(blocks, embd, "f16")
+    _close(X.cpu().numpy(), hidden, "600-token prefill hidden, end to end")
+    model.close()
+
+
+def test_weight_planes_switch(setup, cuda):
+    """The prefill projections' kept weight planes hold the bits the per-call weight prep writes:
+    prefill blocks with the planes kept, switched off (freed) and on again give bit-identical
+    hidden states, and the accessor reports each state."""
+    import torch
+    path, embd, hidden, att, blocks = setup
+    n = embd.shape[0]
+    toks = list(range(n))
+    model = fa.Model(path, n_ctx=256)
+    assert model.weight_planes() == 2  # allowed, not allocated before the first prefill block
+    outs = []
+    for state in (1, 0, 1):
+        model.set_weight_planes(state == 1)
+        X = torch.zeros((n, 2048), device=cuda)
+        model.embed(toks, X)
+        for il in range(2):
+            model.block_prefill(il, X, 0)
+        torch.cuda.synchronize()
+        assert model.weight_planes() == state
+        outs.append(X.cpu().numpy())
+    assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
+    _close(outs[0], hidden, "prefill hidden with kept planes, end to end")
+    model.close()
+
+
 def test_block_errors(setup, cuda):
     import torch
     model = fa.Model(setup[0], n_ctx=64)

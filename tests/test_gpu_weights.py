@@ -255,3 +255,39 @@ def test_projection_rows_gemm_row_ranges(cuda):
     scales = 10.0 ** np.linspace(4, -6, T)
     att_scales = 10.0 ** np.linspace(6, -7, T)
     _gemm_case(cuda, rng, ("q8_0", "q6_K", "f16"), "q8_0", T, x_scale=scales, att_scale=att_scales)
+
+
+def test_projection_rows_gemm_1000_tokens(cuda):
+    """1000 tokens: eight 128-token tiles and a partial one, dealt over the XCDs tile by tile as a
+    long prefill's are, every output within the bound of the oracle."""
+    _gemm_case(cuda, np.random.default_rng(61), ("q8_0", "q6_K", "q5_K"), "q8_0", 1000)
+
+
+def test_projection_rows_gemm_passes_bit_identical(cuda):
+    """Beyond 8192 tokens the projections run in passes of 8192 (the workspace's ceiling): each
+    token's output does not depend on the batch it came in, so the 8300-token call's rows equal,
+    bit for bit, the same rows computed as batches of their own (the first pass's first rows, the
+    rows across the pass boundary, the second pass's last rows)."""
+    import torch
+    rng = np.random.default_rng(67)
+    E, T = fa.N_EMBD, 8300
+    wq, wk, wv = (oracle.random_blocks("q8_0", n, E, rng) for n in (4096, 512, 512))
+    wo = oracle.random_blocks("q6_K", E, 4096, rng)
+    ws = [(_dev(w, cuda), "q8_0") for w in (wq, wk, wv)]
+    wo_d = (_dev(wo, cuda), "q6_K")
+    x = torch.randn((T, E), device=cuda)
+    g = torch.rand(E, device=cuda) + 0.5
+    att = torch.randn((T, 4096), device=cuda)
+    x0 = torch.randn((T, E), device=cuda)
+    qkv = torch.empty((T, 5120), device=cuda)
+    fa.qkv_proj_rows(ws[0], ws[1], ws[2], x, g, qkv)
+    y = x0.clone()
+    fa.o_proj_rows(wo_d, att, y)
+    for a, b in ((0, 40), (8150, 8250), (8260, 8300)):
+        q_part = torch.empty((b - a, 5120), device=cuda)
+        fa.qkv_proj_rows(ws[0], ws[1], ws[2], x[a:b].contiguous(), g, q_part)
+        y_part = x0[a:b].clone()
+        fa.o_proj_rows(wo_d, att[a:b].contiguous(), y_part)
+        torch.cuda.synchronize()
+        assert torch.equal(qkv[a:b], q_part), ("qkv", a, b)
+        assert torch.equal(y[a:b], y_part), ("o", a, b)
