@@ -29,10 +29,10 @@
 //    and hands the MFMA operands over through LDS, and the current token
 //    joins the block merge as one more partial.
 //  * Every split writes its partial (m, l, acc); a second, short kernel merges
-//    them (fused.metal:331-350), 8 split groups x 32 dim groups per head. (A
-//    last-block merge inside the streaming kernel needs an agent-scope
-//    release/acquire per block and funnels every partial through one CU, which
-//    measured slower than the kernel boundary.)
+//    them (fused.metal:331-350): one workgroup per head, one wave per 32 dims,
+//    one lane per split. (A last-block merge inside the streaming kernel needs
+//    coherent stores and a ticket per block and funnels every partial through
+//    one CU, which measured slower than the kernel boundary.)
 //  * Batched entry: one launch serves many independent sequences (one token each).
 //    The grid is flat: sequence s owns 4 x n_split[s] consecutive workgroups (kv head
 //    fastest), so no workgroup is idle and the XCDs, dealt workgroups in id order, get
