@@ -39,11 +39,11 @@ MFMA_PEAK_TFLOPS = 2500.0   # MI355X dense bf16/f16 MFMA
 # HBM bytes per decode call (attn_decode_kernel + attn_combine_kernel) at 32k, from rocprofv3
 # --pmc FETCH_SIZE and WRITE_SIZE runs of `bench.py --only decode --no-cpu`, each scaled by the
 # counter's reading for the 64 MiB calibration copy (profiles/decode_32k_f16.md).
-DECODE_TRAFFIC_BYTES = 68886565
+DECODE_TRAFFIC_BYTES = 68876235
 # HBM bytes per prefill call (kv_prep_kernel + flash_prefill_kernel) at T = 4000, bf16 KV, from
 # rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs of `bench.py --only prefill_full|prefill_swa
 # --no-cpu`, scaled like the decode figure (profiles/prefill_4000_bf16.md); None = not measured.
-PREFILL_TRAFFIC_BYTES = {"full": 187099779, "swa": 176743121}
+PREFILL_TRAFFIC_BYTES = {"full": 184742384, "swa": 176713704}
 # Flint's 49 layers: full attention (no RoPE) at layers 0, 48 and i % 4 == 1, SWA + RoPE elsewhere
 # (/root/reference/src/metal/flint_config.h:37-38): 14 full, 35 SWA
 FLINT_FULL_LAYERS = [i == 0 or i == 48 or i % 4 == 1 for i in range(49)]
@@ -647,7 +647,7 @@ def main():
                          "frac": round(d["bytes_per_launch"] / (t_full * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                          "traffic": DECODE_TRAFFIC_BYTES,
                          "kernel": "one flint_attn_decode call = attn_decode_kernel<1, 1> (f16 KV, no V slices; 43 key "
-                                   "splits x 4 kv heads = 172 workgroups) + attn_combine_kernel<4> (split merge, 128 workgroups); "
+                                   "splits x 4 kv heads = 172 workgroups) + attn_combine_kernel (split merge, 32 workgroups of 4 waves, one lane per split); "
                                    "time per call from HIP events",
                          "bytes_per_launch": d["bytes_per_launch"], "host_bound": d["host_bound"]},
         })
