@@ -418,6 +418,17 @@ __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const Pref
     // LDS: 8 KiB per wave that hands q over to the operand order, and later the output
     __shared__ f16x8 q_lds[PF_WAVES][8][64];
 
+    // SWA layers of two or more rounds of workgroups (every block the same length): the second
+    // half of the first round starts ~4 us late. Otherwise all workgroups of a round load q
+    // together, loop together (memory idle) and store together, and the next round's q loads meet
+    // the stores; offset by about one q load, half the CUs move data while the other half loop,
+    // which stays so in the later rounds (2.0-2.4 us less per T = 4000 call; on full layers the
+    // longest-first order already spreads the workgroups out, and the offset measured slower).
+    // Workgroups are dealt to CUs in id order, so ids 128 .. 255 are half of the first round.
+    if (P.is_swa && P.n_split == 1 && gridDim.x >= 384 && blockIdx.x >= 128 && blockIdx.x < 256) {
+        const unsigned long long t_end = __builtin_amdgcn_s_memrealtime() + 400;  // 100 MHz ticks
+        while (__builtin_amdgcn_s_memrealtime() < t_end) __builtin_amdgcn_s_sleep(4);
+    }
     // Did this call store some tile of the copy scaled (prefix / kv_prep set the flag before this
     // launch)? A plain read of a uniform address is a scalar load; it is issued here, with the
     // kernel arguments the wave waits for anyway (left alone, the compiler sinks it to its use
