@@ -250,8 +250,11 @@ __global__ __launch_bounds__(DEC_THREADS) void attn_decode_kernel(const DecodePa
     const float2 qx = make_float2(qr[lane], qr[lane + 64]);
     const float2 qw = make_float2(q_norm[lane], q_norm[lane + 64]);
     const float rfreq = P.rope_freq[lane];
-    // head `wave` of the group, for the final merge: wave-uniform, kept in an SGPR
-    const float sink = __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(sinks[kvh * GQA + wave]))) * LOG2E;
+    // head `wave` of the group, for the final merge: a wave-uniform address read through the
+    // constant address space, so it is a scalar load into an SGPR that nothing waits for until
+    // the merge (the kernel never writes the sinks). A vector load moved into an SGPR here made
+    // every wave wait for its round trip before it issued its first tile loads.
+    const float sink = *(const __attribute__((address_space(4))) float *)(sinks + kvh * GQA + wave) * LOG2E;
     float2 kx = {0.f, 0.f}, kw = {0.f, 0.f}, vx = {0.f, 0.f};
     if (cur_wave) {
         const float *kr = row + Q_DIM + kvh * HEAD_DIM, *vr = row + Q_DIM + KV_DIM + kvh * HEAD_DIM;
@@ -272,6 +275,10 @@ __global__ __launch_bounds__(DEC_THREADS) void attn_decode_kernel(const DecodePa
     load_tile(ta, kc, vc, t_a < t_end ? t_a : t_begin, lane, slot_mask, t_a < t_end, slice);
     load_tile(tb, kc, vc, t_b < t_end ? t_b : t_begin, lane, slot_mask, t_b < t_end, slice);
     __builtin_amdgcn_sched_barrier(0);
+    // The current token's rows are handed to the prologue here, after the tile loads: left
+    // alone, the compiler rounds v to the cache dtype right after its load, in the branch
+    // above, and that wave then waits for the load before it issues its tiles.
+    asm volatile("" : "+v"(kx.x), "+v"(kx.y), "+v"(kw.x), "+v"(kw.y), "+v"(vx.x), "+v"(vx.y));
 
     // ---- prologue: wave w normalises q head w (+ RoPE), the last split's last wave also
     //      the current token's k and v (rounded to the cache dtype, written to slot(pos)) ----

@@ -430,10 +430,12 @@ __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const Pref
         while (__builtin_amdgcn_s_memrealtime() < t_end) __builtin_amdgcn_s_sleep(4);
     }
     // Did this call store some tile of the copy scaled (prefix / kv_prep set the flag before this
-    // launch)? A plain read of a uniform address is a scalar load; it is issued here, with the
-    // kernel arguments the wave waits for anyway (left alone, the compiler sinks it to its use
-    // after the q prologue, one more memory round trip per workgroup).
-    const uint32_t scaled_call = g_scaled_call;
+    // launch)? Read through the constant address space, so that it is a scalar load issued with
+    // the kernel arguments, which the wave waits for anyway: this kernel never writes the flag,
+    // and the launch's acquire makes the earlier kernels' store visible. (A plain read of the
+    // variable is a vector load, and holding its value in an SGPR from here made every wave wait
+    // for that load's round trip before it could issue its q loads.)
+    const uint32_t scaled_call = *(const __attribute__((address_space(4))) uint32_t *)&g_scaled_call;
     pin_sgpr(scaled_call);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int col = lane & 31, hh = lane >> 5;
