@@ -448,7 +448,10 @@ struct CombineParams {
 __device__ inline float dpp_half_mirror(float x) {
     return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), DPP_HALF_MIRROR, 0xf, 0xf, false));
 }
-__global__ __launch_bounds__(256) void attn_combine_kernel(const CombineParams P) {
+// At most 2 waves per SIMD (one workgroup per CU is all the grid needs), so the register
+// allocator keeps a lane's 8 accumulator loads and its (m, l) load in flight together instead
+// of reusing registers for the last loads after a wait (a second memory round trip).
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void attn_combine_kernel(const CombineParams P) {
     const int hh = blockIdx.x, seq = blockIdx.y, lane = threadIdx.x & 63;
     const int q = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int ns = P.n_split[seq], split0 = P.split0[seq];
@@ -457,8 +460,11 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const CombineParams P
     pin_sgpr(ns), pin_sgpr(split0), pin_sgpr(partial), pin_sgpr(sinks), pin_sgpr(att);
     if (ns <= 1) return;  // written directly by the decode kernel
     const float *pp = partial + ((size_t)split0 * N_HEAD + hh * ns) * PART_STRIDE;
-    const float sink = sinks[hh] * LOG2E;
-    float M = sink, lsum = 0.f, acc[32];
+    // a scalar load (constant address space: the kernel never writes the sinks), first used
+    // after the records' loop, so the records are requested without waiting for it
+    const float sink = *(const __attribute__((address_space(4))) float *)(sinks + hh) * LOG2E;
+    // M starts finite, so a chunk whose splits all lack keys keeps scale 1 and weight 0
+    float M = -1e30f, lsum = 0.f, acc[32];
 #pragma unroll
     for (int j = 0; j < 32; j++) acc[j] = 0.f;
     for (int s0 = 0; s0 < ns; s0 += 64) {
@@ -476,7 +482,10 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const CombineParams P
         for (int j = 0; j < 32; j++) acc[j] = acc[j] * scale + a[j >> 2][j & 3] * w;
         M = Mn;
     }
-    const float L = wave_sum(lsum) + exp2f(sink - M);
+    // the sink joins last: Mf = max(M, sink), the sums rescaled by 2^(M - Mf) (folded into the
+    // final division, c and L being the same in every lane)
+    const float Mf = fmaxf(M, sink), c = exp2f(M - Mf);
+    const float L = wave_sum(lsum) * c + exp2f(sink - Mf), cl = c / L;
     // reduce-scatter: 32 values per lane -> one dim per lane pair
 #pragma unroll
     for (int j = 0; j < 16; j++) {  // lanes l and l ^ 32: dims j (lower half), j + 16 (upper)
@@ -504,7 +513,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const CombineParams P
         acc[0] = b1 ? t1 : t0;
         acc[0] += dpp<DPP_QUAD_XOR1>(acc[0]);
     }
-    if ((lane & 1) == 0) att[(size_t)seq * Q_DIM + hh * HEAD_DIM + 32 * q + (lane >> 1)] = acc[0] / L;
+    if ((lane & 1) == 0) att[(size_t)seq * Q_DIM + hh * HEAD_DIM + 32 * q + (lane >> 1)] = acc[0] * cl;
 }
 
 // Split partials of the entry point that allocates nothing (flint_attn_decode_batch_noalloc):
