@@ -411,7 +411,9 @@ __device__ __forceinline__ void pf_pv(f32x16 (&acc)[4], const f16x8 (&vf)[8], co
 // instructions the other can issue MFMAs.
 // DIRECT: some tiles come from the cache itself (n_direct > 0). A separate instantiation: the
 // per-tile source selection costs the loop 4 registers and ~7% of a config-4 full layer.
-template <bool DIRECT>
+// SWA_DEAL: an SWA layer without key splits (every query block the same length), whose work is
+// dealt as described at the block index below.
+template <bool DIRECT, bool SWA_DEAL = false>
 __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const PrefillParams P, int n_qblocks) {
     // LDS: five 32-key tiles in the attention-copy order (tile t in ring[(t - t_lo) % 5])
     __shared__ f16x8 ring[PF_RING][16][64];
@@ -425,9 +427,11 @@ __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const Pref
     // which stays so in the later rounds (2.0-2.4 us less per T = 4000 call; on full layers the
     // longest-first order already spreads the workgroups out, and the offset measured slower).
     // Workgroups are dealt to CUs in id order, so ids 128 .. 255 are half of the first round.
-    if (P.is_swa && P.n_split == 1 && gridDim.x >= 384 && blockIdx.x >= 128 && blockIdx.x < 256) {
-        const unsigned long long t_end = __builtin_amdgcn_s_memrealtime() + 400;  // 100 MHz ticks
-        while (__builtin_amdgcn_s_memrealtime() < t_end) __builtin_amdgcn_s_sleep(4);
+    if constexpr (SWA_DEAL) {
+        if (gridDim.x >= 384 && blockIdx.x >= 128 && blockIdx.x < 256) {
+            const unsigned long long t_end = __builtin_amdgcn_s_memrealtime() + 400;  // 100 MHz ticks
+            while (__builtin_amdgcn_s_memrealtime() < t_end) __builtin_amdgcn_s_sleep(4);
+        }
     }
     // Did this call store some tile of the copy scaled (prefix / kv_prep set the flag before this
     // launch)? Read through the constant address space, so that it is a scalar load issued with
@@ -444,7 +448,19 @@ __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const Pref
     const int n_split = P.n_split;
     const int kvh = blockIdx.x & 3, hq = kvh * GQA + wave;
     const int rest = (int)(blockIdx.x >> 2), split = rest % n_split;
-    const int qb = n_qblocks - 1 - rest / n_split;
+    // Longest-first (causal blocks grow with qb). SWA_DEAL: kv head h's workgroups land on XCDs
+    // h and h + 4 (the hardware deals workgroup ids to the 8 XCDs in turn); each of the two takes a
+    // contiguous half of the head's query blocks, longest first, so that its L2 fetches only its
+    // half's copy tiles (a tile is read by the 17 blocks after it): the flash kernel's fetch falls
+    // from 1.15x to 1.04x of q plus the copy.
+    int qb;
+    if constexpr (SWA_DEAL) {
+        const int half_blocks = (n_qblocks + 1) >> 1;
+        qb = (rest & 1) * half_blocks + (half_blocks - 1 - (rest >> 1));
+        if (qb >= n_qblocks) return;  // the second half's first slot when n_qblocks is odd
+    } else {
+        qb = n_qblocks - 1 - rest / n_split;
+    }
     const int t0 = qb * PF_BQ;
     const int q_first = P.p0 + t0, q_last = P.p0 + min(t0 + PF_BQ, P.T) - 1;
     const int my_t = t0 + col, my_qp = P.p0 + my_t;
@@ -810,11 +826,13 @@ hipError_t launch_prefill(const PrefillParams &P, int dtype, hipStream_t stream)
         if (n_pre > 0) hipLaunchKernelGGL(prefix_kernel<DT_BF16>, gp, dim3(256), 0, stream, P);
         hipLaunchKernelGGL(kv_prep_kernel<DT_BF16>, gk, dim3(KP_THREADS), 0, stream, P);
     }
-    const dim3 gf(nqb * P.n_split * N_HEAD_KV);
     if (P.n_direct > 0)
-        hipLaunchKernelGGL(flash_prefill_kernel<true>, gf, dim3(PF_THREADS), 0, stream, P, nqb);
+        hipLaunchKernelGGL(flash_prefill_kernel<true>, dim3(nqb * P.n_split * N_HEAD_KV), dim3(PF_THREADS), 0, stream, P, nqb);
+    else if (P.is_swa && P.n_split == 1)  // both halves of every kv head's blocks: an even count
+        hipLaunchKernelGGL((flash_prefill_kernel<false, true>), dim3(2 * ((nqb + 1) >> 1) * N_HEAD_KV), dim3(PF_THREADS), 0,
+                           stream, P, nqb);
     else
-        hipLaunchKernelGGL(flash_prefill_kernel<false>, gf, dim3(PF_THREADS), 0, stream, P, nqb);
+        hipLaunchKernelGGL(flash_prefill_kernel<false>, dim3(nqb * P.n_split * N_HEAD_KV), dim3(PF_THREADS), 0, stream, P, nqb);
     if (P.n_split > 1)
         hipLaunchKernelGGL(prefill_combine_kernel, dim3((P.T * N_HEAD + 3) / 4), dim3(256), 0, stream, P);
     return hipGetLastError();
