@@ -76,10 +76,29 @@ __device__ inline int xs_index(int e) {
     return s * 32 + 4 * (c ^ ((s >> 1) & 7)) + (e & 3);
 }
 
+// Sum over the 64 lanes in double, on VALU lane permutes (each 32-bit half moved by DPP within
+// rows of 16, then v_permlane16/32_swap across rows): no LDS round trips (a __shfl_xor chain
+// costs six dependent ds_bpermute pairs).
+template <int CTRL>
+__device__ inline double dpp_f64(double v) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, CTRL, 0xf, 0xf, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), CTRL, 0xf, 0xf, false);
+    return __builtin_bit_cast(double, ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
+}
 __device__ inline double wave_sum_f64(double v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
-    return v;
+    v += dpp_f64<DPP_ROR8>(v);
+    v += dpp_f64<DPP_ROR4>(v);
+    v += dpp_f64<DPP_ROR2>(v);
+    v += dpp_f64<DPP_ROR1>(v);  // every lane of a row of 16 holds the row's sum
+    uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const auto l16 = __builtin_amdgcn_permlane16_swap((uint32_t)b, (uint32_t)b, false, false);
+    const auto h16 = __builtin_amdgcn_permlane16_swap((uint32_t)(b >> 32), (uint32_t)(b >> 32), false, false);
+    v = __builtin_bit_cast(double, ((uint64_t)h16[0] << 32) | l16[0]) + __builtin_bit_cast(double, ((uint64_t)h16[1] << 32) | l16[1]);
+    b = __builtin_bit_cast(uint64_t, v);
+    const auto l32 = __builtin_amdgcn_permlane32_swap((uint32_t)b, (uint32_t)b, false, false);
+    const auto h32 = __builtin_amdgcn_permlane32_swap((uint32_t)(b >> 32), (uint32_t)(b >> 32), false, false);
+    return __builtin_bit_cast(double, ((uint64_t)h32[0] << 32) | l32[0]) + __builtin_bit_cast(double, ((uint64_t)h32[1] << 32) | l32[1]);
 }
 
 template <int K, int R>
