@@ -16,10 +16,11 @@
 //
 // Matvec layout (HBM-bound on the weight bytes): a wave takes R consecutive rows. It requests
 // their bytes at kernel start (16-byte loads, coalesced) while the workgroup reads x once
-// into LDS (normalised there when the RMSNorm is fused). Row by row, the bytes go into an
-// LDS area of the wave's own; each lane then reads the bytes of its sub-block from LDS at the
-// alignment the format gives (q8_0 and q6_K blocks are only 2-byte aligned), decodes 32
-// weights and accumulates their products with x in fp32; a wave-wide sum gives y[row].
+// into LDS (normalised there when the RMSNorm is fused). The rows' bytes then go into an
+// LDS area of the wave's own; each lane reads the bytes of its sub-block from LDS at the
+// alignment the format gives (q8_0 and q6_K blocks are only 2-byte aligned: q8_0 as aligned
+// words realigned in registers), decodes 32 weights and accumulates their products with x in
+// fp32; a wave-wide sum gives y[row].
 // f32/f16/bf16 rows are read straight from HBM (64- or 128-byte sub-blocks, aligned).
 #include <hip/hip_runtime.h>
 
@@ -108,7 +109,8 @@ __global__ __launch_bounds__(64 * MV_WAVES) void matvec_kernel(const MatvecParam
     constexpr int UNITS = (QBYTES / 16 + 63) / 64;  // 16-byte loads per lane for it
     constexpr int XPT = K / (64 * MV_WAVES);        // x elements per thread in the shared pass
     __shared__ __align__(16) float xs[K];           // the (normalised) x row
-    __shared__ __align__(16) uint8_t stage[MV_WAVES][QBYTES];
+    constexpr int QROW = (QBYTES + 4 + 15) / 16 * 16;  // a staged row, + 4 bytes read past a q8_0 row's end
+    __shared__ __align__(16) uint8_t stage[MV_WAVES][R][QROW];
     __shared__ double part[MV_WAVES];
     // wave index made scalar: the row segment, its type and its row pointer are then known
     // to be wave-uniform (scalar branches for the format, scalar load bases)
@@ -196,43 +198,68 @@ __global__ __launch_bounds__(64 * MV_WAVES) void matvec_kernel(const MatvecParam
     // rows (one pointer that may be either compiles to generic flat loads, several times slower).
     float acc[R];
     if (!fl) {
+        // every row of the wave staged at once, then the dots
 #pragma unroll
-        for (int r = 0; r < R; r++) {
-            if (r > 0) __builtin_amdgcn_wave_barrier();  // every lane done with the previous row
+        for (int r = 0; r < R; r++)
 #pragma unroll
             for (int k = 0; k < UNITS; k++) {
                 const int idx = lane + 64 * k;
-                if (idx < n_units) ((u32x4 *)stage[wave])[idx] = u[r][k];
+                if (idx < n_units) ((u32x4 *)stage[wave][r])[idx] = u[r][k];
             }
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            float a = 0.f;
-            if (S.type == W_Q8_0) {
-                // d * sum(q x) per block: the dot needs no dequantised weights (one multiply
-                // per block instead of one per weight)
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (S.type == W_Q8_0) {
+            // d * sum(q x) per block. The block (2-byte scale, 32 int8) sits at 34 L bytes, 2-byte
+            // aligned: it is read as 9 aligned words and realigned (alignbit); the int8 weights are
+            // converted with the byte-to-float instructions after flipping their sign bits
+            // (u = q + 128), and sum(q x) = sum(u x) - 128 sum(x), sum(x) per sub-block computed once.
+            float xsum[SUBS];
 #pragma unroll
-                for (int i = 0; i < SUBS; i++) {
-                    const uint16_t *p = (const uint16_t *)(stage[wave] + 34 * (lane + 64 * i));
-                    float b = 0.f;
+            for (int i = 0; i < SUBS; i++) {
+                float t = 0.f;
 #pragma unroll
-                    for (int e = 0; e < 16; e++) {
-                        const uint32_t v = p[1 + e];
-                        b = fmaf((float)(int8_t)(v & 0xff), xl[i][2 * e], b);
-                        b = fmaf((float)(int8_t)(v >> 8), xl[i][2 * e + 1], b);
+                for (int e = 0; e < 32; e++) t += xl[i][e];
+                xsum[i] = t;
+            }
+#pragma unroll
+            for (int r = 0; r < R; r++) acc[r] = 0.f;
+#pragma unroll
+            for (int i = 0; i < SUBS; i++) {
+                const int base = 34 * (lane + 64 * i);
+                const bool odd = base & 2;  // the block starts 2 bytes into a word
+#pragma unroll
+                for (int r = 0; r < R; r++) {
+                    const uint32_t *dw = (const uint32_t *)(stage[wave][r] + (base & ~3));
+                    uint32_t d[9];
+#pragma unroll
+                    for (int j = 0; j < 9; j++) d[j] = dw[j];
+                    const uint32_t sc = odd ? d[0] >> 16 : d[0] & 0xffffu;
+                    float b0 = 0.f, b1 = 0.f;
+#pragma unroll
+                    for (int j = 0; j < 8; j++) {
+                        const uint32_t q = (odd ? d[j + 1] : __builtin_amdgcn_alignbit(d[j + 1], d[j], 16)) ^ 0x80808080u;
+                        b0 = fmaf((float)(q & 0xffu), xl[i][4 * j], b0);
+                        b1 = fmaf((float)((q >> 8) & 0xffu), xl[i][4 * j + 1], b1);
+                        b0 = fmaf((float)((q >> 16) & 0xffu), xl[i][4 * j + 2], b0);
+                        b1 = fmaf((float)(q >> 24), xl[i][4 * j + 3], b1);
                     }
-                    a = fmaf(h2f(p[0]), b, a);
+                    acc[r] = fmaf(h2f(sc), (b0 + b1) - 128.f * xsum[i], acc[r]);
                 }
-            } else {
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                float a = 0.f;
 #pragma unroll
                 for (int i = 0; i < SUBS; i++) {
                     float w[32];
-                    deq32(S.type, stage[wave], lane + 64 * i, w);
+                    deq32(S.type, stage[wave][r], lane + 64 * i, w);
 #pragma unroll
                     for (int e = 0; e < 32; e++) a = fmaf(w[e], xl[i][e], a);
                 }
+                acc[r] = a;
             }
-            acc[r] = a;
         }
     } else {
 #pragma unroll
@@ -265,9 +292,10 @@ hipError_t launch_get_rows(const RowsParams &P, hipStream_t stream) {
     return hipGetLastError();
 }
 
-// Rows per wave: 2 for the 2048-element rows (q/k/v: 640 workgroups per token) and for the
-// 4096-element rows (o: 256 workgroups); measured best of 1, 2, 4 and 8.
-constexpr int MV_ROWS_2048 = 2, MV_ROWS_4096 = 2;
+// Rows per wave: 2 for the 2048-element rows (q/k/v: 640 workgroups per token) and 1 for the
+// 4096-element rows (o: 512 workgroups, two waves per SIMD: with one, each row's LDS reads and
+// FMA chain were exposed); measured best of 1, 2, 4 and 8 for either.
+constexpr int MV_ROWS_2048 = 2, MV_ROWS_4096 = 1;
 
 int matvec_row_multiple(int k) { return MV_WAVES * (k == 2048 ? MV_ROWS_2048 : MV_ROWS_4096); }
 
