@@ -63,9 +63,9 @@ __global__ __launch_bounds__(64) void get_rows_kernel(const RowsParams P) {
 
 // ---------------------------------------------------------------------------
 // matvec: a workgroup of MV_WAVES waves serves MV_WAVES * R consecutive rows of one token.
-// x (RMS-normalised and scaled by the gains first, when norm_w is given) is read from HBM
-// once per workgroup into LDS; each wave then takes R rows, whose bytes it requested at
-// kernel start, and reads its lanes' 32-element slices of x from LDS.
+// x (times the RMSNorm gains, when norm_w is given; the norm's scale multiplies the row sums)
+// is read from HBM once per workgroup into LDS; each wave then takes R rows, whose bytes it
+// requested at kernel start, and reads its lanes' 32-element slices of x from LDS.
 constexpr int MV_WAVES = 4;
 
 // x in LDS: float4 column c (elements 4c .. 4c+3) of sub-block s at s * 32 + 4 (c ^ ((s >> 1) & 7)).
@@ -162,7 +162,10 @@ __global__ __launch_bounds__(64 * MV_WAVES) void matvec_kernel(const MatvecParam
         }
     if (norm_w) {
         // RMSNorm as the CPU reference (ref_model.cpp:45-50): double sum of squares, float
-        // scale, (x * scale) * g
+        // scale = 1 / sqrt(ss / K + eps). The scale is one number per token, so W (x scale g) =
+        // scale (W (x g)): x g goes to LDS at once and the scale multiplies each row's sum at the
+        // end (within a few ulp of scaling x first), so the reduction and its barrier are off the
+        // path to the dots (one workgroup barrier instead of two).
         double ss = 0;
 #pragma unroll
         for (int k = 0; k < XPT / 4; k++)
@@ -170,19 +173,21 @@ __global__ __launch_bounds__(64 * MV_WAVES) void matvec_kernel(const MatvecParam
             for (int e = 0; e < 4; e++) ss += (double)xv[k][e] * xv[k][e];
         ss = wave_sum_f64(ss);
         if (lane == 0) part[wave] = ss;
-        __syncthreads();
-        ss = 0;
-#pragma unroll
-        for (int w = 0; w < MV_WAVES; w++) ss += part[w];
-        const float scale = 1.0f / sqrtf((float)(ss / K) + eps);
 #pragma unroll
         for (int k = 0; k < XPT / 4; k++)
 #pragma unroll
-            for (int e = 0; e < 4; e++) xv[k][e] = xv[k][e] * scale * gv[k][e];
+            for (int e = 0; e < 4; e++) xv[k][e] = xv[k][e] * gv[k][e];
     }
 #pragma unroll
     for (int k = 0; k < XPT / 4; k++) *(f32x4 *)&xs[xs_index(XPT * tid + 4 * k)] = xv[k];
     __syncthreads();
+    float scale = 1.f;
+    if (norm_w) {
+        double ss = 0;
+#pragma unroll
+        for (int w = 0; w < MV_WAVES; w++) ss += part[w];
+        scale = 1.0f / sqrtf((float)(ss / K) + eps);
+    }
 
     // this lane's slices of x: sub-blocks lane + 64 i
     float xl[SUBS][32];
@@ -282,6 +287,7 @@ __global__ __launch_bounds__(64 * MV_WAVES) void matvec_kernel(const MatvecParam
         float a = acc[0];
 #pragma unroll
         for (int r = 1; r < R; r++) a = lane == r ? acc[r] : a;
+        a *= scale;
         const int row = row0 + lane;
         yt[row] = add ? yt[row] + a : a;
     }
