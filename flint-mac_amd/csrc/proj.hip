@@ -216,17 +216,10 @@ __global__ __launch_bounds__(64 * MV_WAVES) void matvec_kernel(const MatvecParam
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         if (S.type == W_Q8_0) {
             // d * sum(q x) per block. The block (2-byte scale, 32 int8) sits at 34 L bytes, 2-byte
-            // aligned: it is read as 9 aligned words and realigned (alignbit); the int8 weights are
-            // converted with the byte-to-float instructions after flipping their sign bits
-            // (u = q + 128), and sum(q x) = sum(u x) - 128 sum(x), sum(x) per sub-block computed once.
-            float xsum[SUBS];
-#pragma unroll
-            for (int i = 0; i < SUBS; i++) {
-                float t = 0.f;
-#pragma unroll
-                for (int e = 0; e < 32; e++) t += xl[i][e];
-                xsum[i] = t;
-            }
+            // aligned: it is read as 9 aligned words and realigned (alignbit); each int8 weight is one
+            // sign-extending byte convert (SDWA) and an FMA, in two interleaved chains. (Converting
+            // unsigned bytes after a sign flip, with 128 sum(x) subtracted per block, measured slower
+            // and loses exactness on blocks of small quantised values.)
 #pragma unroll
             for (int r = 0; r < R; r++) acc[r] = 0.f;
 #pragma unroll
@@ -243,13 +236,13 @@ __global__ __launch_bounds__(64 * MV_WAVES) void matvec_kernel(const MatvecParam
                     float b0 = 0.f, b1 = 0.f;
 #pragma unroll
                     for (int j = 0; j < 8; j++) {
-                        const uint32_t q = (odd ? d[j + 1] : __builtin_amdgcn_alignbit(d[j + 1], d[j], 16)) ^ 0x80808080u;
-                        b0 = fmaf((float)(q & 0xffu), xl[i][4 * j], b0);
-                        b1 = fmaf((float)((q >> 8) & 0xffu), xl[i][4 * j + 1], b1);
-                        b0 = fmaf((float)((q >> 16) & 0xffu), xl[i][4 * j + 2], b0);
-                        b1 = fmaf((float)(q >> 24), xl[i][4 * j + 3], b1);
+                        const uint32_t q = odd ? d[j + 1] : __builtin_amdgcn_alignbit(d[j + 1], d[j], 16);
+                        b0 = fmaf((float)(int8_t)(q & 0xffu), xl[i][4 * j], b0);
+                        b1 = fmaf((float)(int8_t)((q >> 8) & 0xffu), xl[i][4 * j + 1], b1);
+                        b0 = fmaf((float)(int8_t)((q >> 16) & 0xffu), xl[i][4 * j + 2], b0);
+                        b1 = fmaf((float)(int8_t)(q >> 24), xl[i][4 * j + 3], b1);
                     }
-                    acc[r] = fmaf(h2f(sc), (b0 + b1) - 128.f * xsum[i], acc[r]);
+                    acc[r] = fmaf(h2f(sc), b0 + b1, acc[r]);
                 }
             }
         } else {
