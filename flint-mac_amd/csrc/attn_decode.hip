@@ -54,7 +54,7 @@ constexpr int DEC_THREADS = DEC_WAVES * 64;
 // 32 lanes that write 16 bytes each spread evenly over the banks
 constexpr int ACC_ROW = HEAD_DIM + 4;
 
-// VS = V slices: the 128 output dims of a head split over VS workgroups (VS = 1, 2 or 4). Each
+// VS = V slices: the 128 output dims of a head split over VS workgroups (VS = 1, 2, 4 or 8). Each
 // workgroup computes every score (all of K) and the P*V product for its 128/VS dims.
 template <int VS>
 struct KvTile {
@@ -216,7 +216,17 @@ __global__ __launch_bounds__(DEC_THREADS) void attn_decode_kernel(const DecodePa
     // split). The hardware deals workgroups to the XCDs in id order, so equal-sized units
     // spread every XCD's share of the stream evenly (a grid with idle slots skews it, and one
     // XCD moves ~1.2 TB/s at most).
-    const int wid = blockIdx.x;
+    // With V slices (one split per sequence, so wg_base[s] = 4 VS s) the launch ids are packed by
+    // XCD instead: 8 VS consecutive ids serve two sequences, the VS slices of kv head h of the
+    // first on XCD h and those of the second on XCD h + 4, so the K that all of them read comes
+    // from HBM once per kv head and from that XCD's L2 for the other slices. The id is mapped
+    // back to the flat order above.
+    int wid = blockIdx.x;
+    if constexpr (VS > 1) {
+        const int j = wid % (8 * VS), s = 2 * (wid / (8 * VS)) + ((j >> 2) & 1);
+        if (s >= n_seq) return;  // the second sequence of the last block when n_seq is odd
+        wid = 4 * VS * s + (j & 3) + 4 * (j >> 3);  // kv head j & 3, V slice j >> 3
+    }
     const int seq = __builtin_popcountll(__builtin_amdgcn_ballot_w64(lane < n_seq && wid >= t_base)) - 1;
     const int n_split = __builtin_amdgcn_readlane(t_ns, seq), pos = __builtin_amdgcn_readlane(t_pos, seq);
     const int tps = __builtin_amdgcn_readlane(t_tps, seq);
@@ -542,8 +552,14 @@ hipError_t decode_scratch(float **ptr) {
 }
 
 hipError_t launch_decode(const DecodeParams &P, int dtype, hipStream_t stream) {
-    dim3 grid(P.wg_base[P.n_seq]), block(DEC_THREADS);
-    if (dtype == DT_F16 && P.v_slices == 4)
+    // V slices: ids packed by XCD, 8 VS per pair of sequences (the kernel maps them back)
+    const int n_wg = P.v_slices > 1 ? 8 * P.v_slices * ((P.n_seq + 1) / 2) : P.wg_base[P.n_seq];
+    dim3 grid(n_wg), block(DEC_THREADS);
+    if (dtype == DT_F16 && P.v_slices == 8)
+        hipLaunchKernelGGL((attn_decode_kernel<DT_F16, 8>), grid, block, 0, stream, P);
+    else if (dtype == DT_BF16 && P.v_slices == 8)
+        hipLaunchKernelGGL((attn_decode_kernel<DT_BF16, 8>), grid, block, 0, stream, P);
+    else if (dtype == DT_F16 && P.v_slices == 4)
         hipLaunchKernelGGL((attn_decode_kernel<DT_F16, 4>), grid, block, 0, stream, P);
     else if (dtype == DT_BF16 && P.v_slices == 4)
         hipLaunchKernelGGL((attn_decode_kernel<DT_BF16, 4>), grid, block, 0, stream, P);

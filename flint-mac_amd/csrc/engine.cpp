@@ -191,11 +191,18 @@ void decode_impl(const flint_attn_layer *L, int n_seq, int64_t seq_stride, const
     int max_split = 1;
     for (int s = 0; s < n_seq; s++) max_split = std::max(max_split, P.n_split[s]);
     // One split per sequence (short key ranges, SWA layers): one CU streams each kv head's
-    // keys (~63 GB/s at most per CU), so 4 (or 2) workgroups per kv head, each reading all of
-    // K and a quarter (half) of V, shorten the stream without a merge; the K they all read
-    // comes from L2/MALL. Measured on SWA layers (513 keys): 8.1 us per call with one
-    // workgroup per kv head, 6.3 with 2, 5.7 with 4; 16 sequences: 9.8, 9.6, 9.1 us.
-    P.v_slices = max_split > 1 ? 1 : n_seq * N_HEAD_KV * 4 <= 256 ? 4 : n_seq * N_HEAD_KV * 2 <= 256 ? 2 : 1;
+    // keys (~36 GB/s per CU from HBM, ~63 GB/s from the caches), so 8 (or 4, 2) workgroups per
+    // kv head, each reading all of K and its slice of V, shorten the stream without a merge. The
+    // launch puts a kv head's slices on one XCD, so the K they all read comes from HBM once and
+    // from that XCD's L2 after. Measured on SWA layers (513 keys, rings in the caches): 8.1 us per
+    // call with one workgroup per kv head, 6.3 with 2, 5.7 with 4; 16 sequences: 9.8, 9.6, 9.1 us.
+    // Cold rings (as a decode step meets them): 7.09 us with 4 slices on two XCDs, 6.62 with 8 on
+    // two XCDs, 6.49 with 8 on one.
+    P.v_slices = max_split > 1                          ? 1
+                 : n_seq * N_HEAD_KV * 8 <= 256 ? 8
+                 : n_seq * N_HEAD_KV * 4 <= 256 ? 4
+                 : n_seq * N_HEAD_KV * 2 <= 256 ? 2
+                                                : 1;
     P.wg_base[0] = 0;
     int n_records = 0;  // partial records (in splits) of the launch: sequences of more than one split
     for (int s = 0; s < n_seq; s++) {

@@ -34,10 +34,11 @@ struct DecodeParams {
     int pos[MAX_SEQ];           // sequence s decodes the token at pos[s]
     int n_split[MAX_SEQ];       // key splits of sequence s
     int tps[MAX_SEQ];           // 32-key tiles per split of sequence s
-    int wg_base[MAX_SEQ + 1];   // first workgroup of sequence s (4 x v_slices per split); [n_seq] = grid size
+    int wg_base[MAX_SEQ + 1];   // first work unit of sequence s (4 x v_slices per split); [n_seq] = the
+                                // units of the launch (its grid size without V slices)
     int split0[MAX_SEQ];        // first partial record (in splits) of sequence s: the splits of the
                                 // sequences before it that have more than one (one split needs none)
-    int v_slices;               // 1, or 2 / 4 when every sequence has one split: a head's 128 output
+    int v_slices;               // 1, or 2 / 4 / 8 when every sequence has one split: a head's 128 output
                                 // dims in that many workgroups (each reads all of K and its part of V)
 };
 

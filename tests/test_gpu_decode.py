@@ -241,18 +241,21 @@ def test_decode_batch_64_sequences(cuda, store):
 
 
 @pytest.mark.parametrize("store", ["f16", "bf16"])
-@pytest.mark.parametrize("n_seq", [16, 24])
+@pytest.mark.parametrize("n_seq", [1, 3, 8, 16, 17, 24])
 def test_decode_batch_swa_v_slices(cuda, store, n_seq):
     """Batched SWA decode with V slices: every sequence has one split, so each kv head's
-    output dims are cut over 4 workgroups (16 sequences: 256 workgroups) or 2 (24
-    sequences: 4 would exceed 256). Positions before, at and past the ring wrap, and 0;
-    every sequence equals the oracle; the current token's K/V land in its ring slot, and
-    every other slot of the sequence's ring keeps what it held."""
+    output dims are cut over 8 workgroups (up to 8 sequences), 4 (up to 16: 256 workgroups)
+    or 2 (17 and 24 sequences: 4 would exceed 256). The launch ids are packed by XCD, two
+    sequences per block of ids, so the odd counts leave half of the last block idle.
+    Positions before, at and past the ring wrap, and 0; every sequence equals the oracle; the
+    current token's K/V land in its ring slot, and every other slot of the sequence's ring
+    keeps what it held."""
     _say(f"decode batch SWA v-slices n_seq={n_seq} store={store}")
     rng = np.random.default_rng(100 + n_seq)
     qn, kn, sk = layer_weights(rng)
     positions = [int(p) for p in rng.integers(1, 2600, n_seq)]
-    positions[0], positions[1], positions[2] = 0, 1023, 1024
+    fixed = [0, 1023, 1024] if n_seq >= 3 else [1501]
+    positions[:len(fixed)] = fixed
     kv = fa.KVLayer(is_swa=True, has_rope=True, n_slots=1024, kv_dtype=store, q_norm=qn, k_norm=kn, sinks=sk,
                     n_seq=n_seq)
     L = oracle_layer(kv, qn, kn, sk, store)
