@@ -22,7 +22,8 @@
 //    are fp32-accurate at no extra MFMA cost; P*V uses the same hi/lo trick on P.
 //  * A tile is 32 keys (16 x 16-byte loads per lane, 16 KiB per wave). Each
 //    wave keeps two tiles in flight, and a tile's registers are refilled as
-//    soon as it is consumed; the first is requested before the prologue.
+//    soon as it is consumed; the first is requested before the prologue, the
+//    second after its barrier.
 //  * Compact code on the critical path: each wave runs the straight-line
 //    parts of the kernel once, from a cold instruction cache, so the q / k
 //    normalisation is cooperative (one q head per wave, a NEOX pair per lane)
@@ -273,21 +274,22 @@ __global__ __launch_bounds__(DEC_THREADS) void attn_decode_kernel(const DecodePa
         vx = make_float2(vr[lane], vr[lane + 64]);
     }
     __builtin_amdgcn_sched_barrier(0);
-    // The first two tiles, before the prologue waits for its own loads, so tile latency
-    // overlaps the prologue. Issued unconditionally (a wave without such a tile reads 16
-    // bytes per load of tile t_begin, never consumed), since loads under a branch make the
-    // compiler's wait counting at the join conservative. (Under a full stream a wave's
-    // later load instructions stall at issue until the CU has room for them, so at long
-    // contexts the prologue ends only as the stream does; the tiles land no earlier when
-    // the prologue goes first, so nothing is gained by reordering.)
+    // The first tile, before the prologue waits for its own loads, so its latency overlaps
+    // the prologue; the second after the prologue's barrier. Once the CU's memory pipeline is
+    // full a wave's load instructions stall at issue, and a wave still issuing cannot reach
+    // the barrier: with both tiles issued here every wave waited for the slowest wave's 32
+    // loads to be accepted (q operands ready ~2.9 us after the start of a cold SWA call, ~2.2
+    // with one tile). Issuing no tile before the prologue readies q by ~1.2 us but leaves the
+    // first tile's latency exposed (slower, also at 32k). Issued unconditionally (a wave
+    // without such a tile reads 16 bytes per load of tile t_begin, never consumed), since
+    // loads under a branch make the compiler's wait counting at the join conservative.
     KvTile<VS> ta, tb;
     int t_a = t_begin + wave, t_b = t_a + W;
     load_tile(ta, kc, vc, t_a < t_end ? t_a : t_begin, lane, slot_mask, t_a < t_end, slice);
-    load_tile(tb, kc, vc, t_b < t_end ? t_b : t_begin, lane, slot_mask, t_b < t_end, slice);
     __builtin_amdgcn_sched_barrier(0);
-    // The current token's rows are handed to the prologue here, after the tile loads: left
+    // The current token's rows are handed to the prologue here, after the tile's loads: left
     // alone, the compiler rounds v to the cache dtype right after its load, in the branch
-    // above, and that wave then waits for the load before it issues its tiles.
+    // above, and that wave then waits for the load before it issues its tile.
     asm volatile("" : "+v"(kx.x), "+v"(kx.y), "+v"(kw.x), "+v"(kw.y), "+v"(vx.x), "+v"(vx.y));
 
     // ---- prologue: wave w normalises q head w (+ RoPE), the last split's last wave also
@@ -326,7 +328,8 @@ __global__ __launch_bounds__(DEC_THREADS) void attn_decode_kernel(const DecodePa
             }
         }
     }
-    lds_barrier();  // the q operands are in LDS; the tile loads stay in flight
+    lds_barrier();  // the q operands are in LDS; the first tile's loads stay in flight
+    load_tile(tb, kc, vc, t_b < t_end ? t_b : t_begin, lane, slot_mask, t_b < t_end, slice);
     vec8 qb[4];  // MFMA B operand: column n = head hloc, hi or lo half; k = dims 32c + 8g + e
 #pragma unroll
     for (int c = 0; c < 4; c++) qb[c] = *(const vec8 *)&sm_qh[hl][hloc][32 * c + 8 * g];
