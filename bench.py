@@ -39,7 +39,7 @@ MFMA_PEAK_TFLOPS = 2500.0   # MI355X dense bf16/f16 MFMA
 # HBM bytes per decode call (attn_decode_kernel + attn_combine_kernel) at 32k, from rocprofv3
 # --pmc FETCH_SIZE and WRITE_SIZE runs of `bench.py --only decode --no-cpu`, each scaled by the
 # counter's reading for the 64 MiB calibration copy (profiles/decode_32k_f16.md).
-DECODE_TRAFFIC_BYTES = 68876235
+DECODE_TRAFFIC_BYTES = 68866200
 # HBM bytes per prefill call (kv_prep_kernel + flash_prefill_kernel) at T = 4000, bf16 KV, from
 # rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs of `bench.py --only prefill_full|prefill_swa
 # --no-cpu`, scaled like the decode figure (profiles/prefill_4000_bf16.md); None = not measured.
