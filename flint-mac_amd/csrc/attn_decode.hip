@@ -40,6 +40,10 @@
 //    equal shares of the stream. Every kernel argument the block needs is read at wave
 //    start (the per-sequence tables one entry per lane), so the kernel-argument fetch
 //    costs one memory round trip.
+//  * Short key ranges (one split per sequence, SWA layers): a kv head's 128 output dims
+//    are cut over 8 (4, 2) V-slice workgroups, each reading all of K, and the launch ids
+//    are packed so that a kv head's slices share one XCD: its K comes from HBM once and
+//    from that XCD's L2 for the other slices.
 #include <mutex>
 
 #include "common.h"
