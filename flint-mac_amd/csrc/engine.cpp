@@ -402,6 +402,12 @@ void proj_gemm(const MatvecSeg *seg, int n_seg, int N, int K, const float *x, lo
     W.wh = pl ? pl->wh : (_Float16 *)(ws + o_wh);
     W.wl = pl ? pl->wl : (_Float16 *)(ws + o_wl);
     W.fexp = pl ? pl->fexp : (int *)(ws + o_f);
+    // every segment q8_0: the q8 form (the values in wh, the block scales in wl's memory, which
+    // holds N K / 32 floats with room to spare)
+    bool q8 = true;
+    for (int i = 0; i < n_seg; i++) q8 = q8 && seg[i].type == W_Q8_0;
+    W.q8 = q8;
+    W.wd = (float *)W.wl;
     GemmActParams X{};
     X.norm_w = norm_w;
     X.eps = eps;
@@ -410,6 +416,7 @@ void proj_gemm(const MatvecSeg *seg, int n_seg, int N, int K, const float *x, lo
     X.eexp = (int *)(ws + o_e);
     GemmParams G{};
     G.wh = W.wh, G.wl = W.wl, G.fexp = W.fexp, G.xh = X.xh, G.xl = X.xl, G.eexp = X.eexp;
+    G.q8 = W.q8, G.wd = W.wd;
     G.add = add;
     G.N = N;
     G.K = K;

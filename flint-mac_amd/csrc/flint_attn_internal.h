@@ -127,6 +127,11 @@ struct GemmWeightParams {  // wprep: rows [0, N) of the segments -> wh, wl [N][K
     int n_seg;
     _Float16 *wh, *wl;
     int *fexp;
+    // q8: every segment is q8_0; then wh holds the quantised values (exact in f16) and wd the
+    // blocks' scales, [N / 128 row tiles][K / 32 blocks][128 rows] floats (in wl's memory), and
+    // the GEMM takes the q8 form
+    int q8;
+    float *wd;
 };
 struct GemmActParams {     // xprep: rows [0, T_pad) -> xh, xl [T_pad][K], eexp [T_pad]
     const float *x;        // [T] rows of x_stride floats (16-byte aligned)
@@ -140,6 +145,8 @@ struct GemmActParams {     // xprep: rows [0, T_pad) -> xh, xl [T_pad][K], eexp 
 struct GemmParams {
     const _Float16 *wh, *wl, *xh, *xl;
     const int *fexp, *eexp;
+    int q8;                // the weights as q8_0 values and block scales (GemmWeightParams::q8)
+    const float *wd;
     float *y;              // [T] rows of y_stride floats (16-byte aligned, stride a multiple of 4)
     long long y_stride;
     int add, N, K, T;

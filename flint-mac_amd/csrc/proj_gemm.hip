@@ -122,6 +122,40 @@ __global__ __launch_bounds__(512) void wprep_kernel(const GemmWeightParams P) {
     }
 }
 
+
+// ---------------------------------------------------------------------------
+// The q8_0 form. A q8_0 weight is d q, with q an integer of magnitude at most 127 (exact in f16)
+// and d its 32-element block's scale, and a 32-k chunk of the GEMM is one block. So a chunk's
+// products are sum_k (xh + xl) q on the matrix cores, two products per pair instead of gemm3's
+// three and no weight lo plane, and the scale joins in fp32: acc += d T, one d per weight row and
+// chunk. The x planes are gemm3's.
+//
+// wprep_q8: thread (row n, block b) writes the block's 32 values as f16 into the plane's chunk
+// order (plane_unit) and d into wd[n / 128][b][n % 128].
+template <int K>
+__global__ __launch_bounds__(256) void wprep_q8_kernel(const GemmWeightParams P) {
+    constexpr int NB = K / 32;
+    const int idx = blockIdx.x * 256 + threadIdx.x, n = idx / NB, b = idx % NB;  // block fastest
+    const int in2 = P.n_seg > 2 && n >= P.seg[2].row0, in1 = !in2 && P.n_seg > 1 && n >= P.seg[1].row0;
+    const MatvecSeg S = in2 ? P.seg[2] : in1 ? P.seg[1] : P.seg[0];
+    // a block: f16 d, then 32 int8 values; 2-byte aligned (34-byte blocks)
+    const uint16_t *blk = (const uint16_t *)(S.w + (size_t)(n - S.row0) * S.row_bytes + 34 * b);
+    uint16_t w[17];
+#pragma unroll
+    for (int i = 0; i < 17; i++) w[i] = blk[i];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        f16x8 v;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const int k = 8 * j + e;  // byte k of the values: half k >> 1 of words 1 ..
+            v[e] = (_Float16)(int8_t)(w[1 + (k >> 1)] >> (8 * (k & 1)));
+        }
+        *(f16x8 *)(P.wh + plane_unit(n, 4 * b + j, K)) = v;
+    }
+    P.wd[((size_t)(n >> 7) * NB + b) * GEMM_TILE + (n & 127)] = (float)__builtin_bit_cast(_Float16, w[0]);
+}
+
 // ---------------------------------------------------------------------------
 // xprep: one 512-thread workgroup per 8 activation rows t0 .. t0 + 7 (rows T .. T_pad - 1 are
 // written as zeros). Lane (row rho = lane & 7, group lane gl = lane >> 3) of wave w holds the
@@ -343,10 +377,144 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemm3_kernel(const GemmParams P
     }
 }
 
+
+// gemm_q8: gemm3's tiles, deal, LDS order and pipelining with the tokens as operand A and the
+// weights' values as operand B, so that an MFMA output lane holds one weight row (16 tokens of
+// it) and takes one d per chunk. A chunk's 128 scales ride along in LDS with its planes.
+__global__ __launch_bounds__(GM_THREADS, 2) void gemmq8_kernel(const GemmParams P) {
+    // [buffer][plane (x hi, x lo, weight values)]: 8 KiB each, and the chunk's scales
+    __shared__ __align__(16) uint8_t lds[2][3][GM_PLANE_CHUNK];
+    __shared__ __align__(16) float dl[2][GM_TILE];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wn = wave & 1, wt = wave >> 1;
+    const int NT = P.N / GM_TILE, id = blockIdx.x;
+    int nt, tt;
+    if (NT % 8 == 0) {  // the XCD deal of gemm3
+        const int w = NT / 8, j = id >> 3;
+        nt = (id & 7) * w + j % w;
+        tt = j / w;
+    } else {
+        nt = id % NT;
+        tt = id / NT;
+    }
+    const int n0 = nt * GM_TILE, t0 = tt * GM_TILE;
+    const int K = P.K;
+    const _Float16 *src[3] = {P.xh + (size_t)t0 * K, P.xl + (size_t)t0 * K, P.wh + (size_t)n0 * K};
+    const float *srcd = P.wd + (size_t)nt * (K / GM_KC) * GM_TILE;  // [chunk][128 rows]
+    int goff[2], loff[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int u = tid + GM_THREADS * i;
+        goff[i] = 8 * u;
+        loff[i] = 16 * u;
+    }
+    u32x4 ga[3][2], gb[3][2];  // [plane][unit]
+    f32x4 da, db;              // scales 4 (tid & 31) .. +3 of the chunk (every thread loads them)
+    auto gload = [&](u32x4 (&g)[3][2], f32x4 &d, int kc) {
+#pragma unroll
+        for (int p = 0; p < 3; p++)
+#pragma unroll
+            for (int i = 0; i < 2; i++) g[p][i] = *(const u32x4 *)(src[p] + goff[i] + (size_t)kc * GM_TILE);
+        d = *(const f32x4 *)(srcd + (size_t)(kc / GM_KC) * GM_TILE + 4 * (tid & 31));
+    };
+    auto lstore = [&](const u32x4 (&g)[3][2], const f32x4 &d, int buf) {
+#pragma unroll
+        for (int p = 0; p < 3; p++)
+#pragma unroll
+            for (int i = 0; i < 2; i++) *(u32x4 *)(lds[buf][p] + loff[i]) = g[p][i];
+        if (tid < 32) *(f32x4 *)&dl[buf][4 * tid] = d;
+    };
+    f32x16 acc[2][2];  // [token block][weight block]
+#pragma unroll
+    for (int a = 0; a < 2; a++)
+#pragma unroll
+        for (int b = 0; b < 2; b++) acc[a][b] = f32x16{};
+    auto compute = [&](int buf) {
+        f16x8 wq[2][2];  // [k-step of 16][weight block 2wn + b]
+#pragma unroll
+        for (int s = 0; s < 2; s++)
+#pragma unroll
+            for (int b = 0; b < 2; b++)
+                wq[s][b] = *(const f16x8 *)(lds[buf][2] + ((2 * wn + b) * 2 + s) * 1024 + lane * 16);
+        float d[2];
+#pragma unroll
+        for (int b = 0; b < 2; b++) d[b] = dl[buf][64 * wn + 32 * b + (lane & 31)];
+#pragma unroll
+        for (int a = 0; a < 2; a++) {
+            f32x16 T[2];
+#pragma unroll
+            for (int s = 0; s < 2; s++) {
+                const int tb = ((2 * wt + a) * 2 + s) * 1024 + lane * 16;  // token block 2wt + a
+                const f16x8 xh = *(const f16x8 *)(lds[buf][0] + tb), xl = *(const f16x8 *)(lds[buf][1] + tb);
+#pragma unroll
+                for (int b = 0; b < 2; b++) {
+                    T[b] = mfma32_f16(xh, wq[s][b], s == 0 ? f32x16{} : T[b]);
+                    T[b] = mfma32_f16(xl, wq[s][b], T[b]);
+                }
+            }
+#pragma unroll
+            for (int b = 0; b < 2; b++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) acc[a][b][e] = fmaf(d[b], T[b][e], acc[a][b][e]);
+        }
+    };
+    const int n_chunks = K / GM_KC;
+    gload(ga, da, 0);
+    gload(gb, db, GM_KC);
+    lstore(ga, da, 0);
+    gload(ga, da, 2 * GM_KC);
+    lds_barrier();
+    const int last = (n_chunks - 1) * GM_KC;
+    for (int c = 0; c < n_chunks; c += 2) {
+        lstore(gb, db, 1);
+        gload(gb, db, min((c + 3) * GM_KC, last));
+        compute(0);
+        lds_barrier();
+        lstore(ga, da, 0);
+        gload(ga, da, min((c + 4) * GM_KC, last));
+        compute(1);
+        lds_barrier();
+    }
+    // epilogue: block (a, b) element e is token t0 + 64 wt + 32 a + 8 (e >> 2) + 4 (lane >> 5) + (e & 3)
+    // and weight row n0 + 64 wn + 32 b + (lane & 31): a store instruction writes 32 consecutive
+    // floats of each of two token rows
+#pragma unroll
+    for (int a = 0; a < 2; a++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+            const int t = t0 + 64 * wt + 32 * a + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+            if (t >= P.T) continue;
+            const int et = P.eexp[t];
+            float *yt = P.y + (size_t)t * P.y_stride + n0 + 64 * wn + (lane & 31);
+#pragma unroll
+            for (int b = 0; b < 2; b++) {
+                float v = __builtin_amdgcn_ldexpf(acc[a][b][e], et);
+                if (P.add) v += yt[32 * b];
+                yt[32 * b] = v;
+            }
+        }
+}
+
 hipError_t launch_proj_gemm(const GemmWeightParams &W, const GemmActParams &X, const GemmParams &G, bool prep_weights,
                             hipStream_t stream) {
     // the planes' chunk order and the GEMM's tiles need whole 128-row tiles of both operands
     if (G.N % GM_TILE != 0 || X.T_pad % GM_TILE != 0 || (G.K != 2048 && G.K != 4096)) return hipErrorInvalidValue;
+    if (G.q8) {
+        if (prep_weights) {
+            if (G.K == 2048)
+                hipLaunchKernelGGL(wprep_q8_kernel<2048>, dim3(G.N * (2048 / 32) / 256), dim3(256), 0, stream, W);
+            else
+                hipLaunchKernelGGL(wprep_q8_kernel<4096>, dim3(G.N * (4096 / 32) / 256), dim3(256), 0, stream, W);
+        }
+        if (X.T_pad > 0) {
+            if (G.K == 2048)
+                hipLaunchKernelGGL(xprep_kernel<2048>, dim3(X.T_pad / 8), dim3(512), 0, stream, X);
+            else
+                hipLaunchKernelGGL(xprep_kernel<4096>, dim3(X.T_pad / 8), dim3(512), 0, stream, X);
+            hipLaunchKernelGGL(gemmq8_kernel, dim3(G.N / GM_TILE * (X.T_pad / GM_TILE)), dim3(GM_THREADS), 0, stream, G);
+        }
+        return hipGetLastError();
+    }
     if (G.K == 2048) {
         if (prep_weights) hipLaunchKernelGGL(wprep_kernel<2048>, dim3(G.N / 8), dim3(512), 0, stream, W);
         if (X.T_pad > 0) hipLaunchKernelGGL(xprep_kernel<2048>, dim3(X.T_pad / 8), dim3(512), 0, stream, X);
