@@ -402,12 +402,11 @@ void proj_gemm(const MatvecSeg *seg, int n_seg, int N, int K, const float *x, lo
     W.wh = pl ? pl->wh : (_Float16 *)(ws + o_wh);
     W.wl = pl ? pl->wl : (_Float16 *)(ws + o_wl);
     W.fexp = pl ? pl->fexp : (int *)(ws + o_f);
-    // every segment q8_0: the q8 form (the values in wh, the block scales in wl's memory, which
-    // holds N K / 32 floats with room to spare)
-    bool q8 = true;
-    for (int i = 0; i < n_seg; i++) q8 = q8 && seg[i].type == W_Q8_0;
-    W.q8 = q8;
+    // every segment q8_0: the q8 form (the values in wh, the block scales in wl's memory: N K / 32
+    // floats, in the workspace with room to spare, in kept planes laid out for it)
+    W.q8 = gemm_q8(seg, n_seg);
     W.wd = (float *)W.wl;
+    if (pl && !W.q8 && !pl->fexp) throw Error("projection GEMM: weight planes laid out for q8_0 weights");
     GemmActParams X{};
     X.norm_w = norm_w;
     X.eps = eps;
@@ -516,17 +515,32 @@ void o_proj_impl(const flint_weight *wo, const float *att, int n_tok, float *x, 
 
 }  // namespace
 
-size_t planes_bytes(int N, int K) {
-    const size_t w = ((size_t)N * K * sizeof(_Float16) + 255) / 256 * 256;
-    return 2 * w + ((size_t)N * sizeof(int) + 255) / 256 * 256;
+bool gemm_q8(const MatvecSeg *seg, int n_seg) {
+    bool q8 = n_seg > 0;
+    for (int i = 0; i < n_seg; i++) q8 = q8 && seg[i].type == W_Q8_0;
+    return q8;
 }
 
-WeightPlanes planes_at(void *mem, int N, int K) {
-    const size_t w = ((size_t)N * K * sizeof(_Float16) + 255) / 256 * 256;
+bool qkv_gemm_q8(const flint_weight *wq, const flint_weight *wk, const flint_weight *wv) {
+    return wq->type == W_Q8_0 && wk->type == W_Q8_0 && wv->type == W_Q8_0;
+}
+
+bool o_gemm_q8(const flint_weight *wo) { return wo->type == W_Q8_0; }
+
+static size_t align256(size_t b) { return (b + 255) / 256 * 256; }
+
+size_t planes_bytes(int N, int K, bool q8) {
+    const size_t w = align256((size_t)N * K * sizeof(_Float16));
+    if (q8) return w + align256((size_t)N * (K / 32) * sizeof(float));
+    return 2 * w + align256((size_t)N * sizeof(int));
+}
+
+WeightPlanes planes_at(void *mem, int N, int K, bool q8) {
+    const size_t w = align256((size_t)N * K * sizeof(_Float16));
     WeightPlanes pl;
     pl.wh = (_Float16 *)mem;
     pl.wl = (_Float16 *)((char *)mem + w);
-    pl.fexp = (int *)((char *)mem + 2 * w);
+    pl.fexp = q8 ? nullptr : (int *)((char *)mem + 2 * w);
     return pl;
 }
 

@@ -160,15 +160,20 @@ hipError_t launch_proj_gemm(const GemmWeightParams &W, const GemmActParams &X, c
 int matvec_row_multiple(int k);  // n_rows of a matvec launch must be a multiple of this
 
 // A projection's weight planes kept by a caller that runs many batches through the same weights
-// (the model's layer-major prefill): one device block of planes_bytes(N, K) holding wh, wl
+// (the model's layer-major prefill): one device block of planes_bytes(N, K, q8) holding wh, wl
 // [N][K] and fexp [N], built once with build_*_planes; the *_rows projections given them skip
-// their per-call weight prep (the planes are the same bits that prep would write).
+// their per-call weight prep (the planes are the same bits that prep would write). q8 (every
+// weight of the projection in q8_0, gemm_q8): wh holds the values and wl's place the block
+// scales, N K / 32 floats, with no fexp.
 struct WeightPlanes {
     _Float16 *wh = nullptr, *wl = nullptr;
     int *fexp = nullptr;
 };
-size_t planes_bytes(int N, int K);
-WeightPlanes planes_at(void *mem, int N, int K);
+bool gemm_q8(const MatvecSeg *seg, int n_seg);  // the GEMM's q8_0 form: every segment in q8_0
+bool qkv_gemm_q8(const flint_weight *wq, const flint_weight *wk, const flint_weight *wv);
+bool o_gemm_q8(const flint_weight *wo);
+size_t planes_bytes(int N, int K, bool q8);
+WeightPlanes planes_at(void *mem, int N, int K, bool q8);
 void build_qkv_planes(const flint_weight *wq, const flint_weight *wk, const flint_weight *wv, const WeightPlanes &pl,
                       hipStream_t stream);
 void build_o_planes(const flint_weight *wo, const WeightPlanes &pl, hipStream_t stream);

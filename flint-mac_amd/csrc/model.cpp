@@ -158,8 +158,9 @@ struct flint_attn_model {
     float *qkv = nullptr, *att = nullptr;
     int cap = 0;
     int32_t n_ctx = 0, pos = 0;  // the session: context length and tokens processed
-    // The prefill GEMMs' f16 hi/lo planes of every layer's q|k|v and o weights (75.5 MB a layer),
-    // one allocation made at the first prefill block that takes the GEMM; a layer's planes are built
+    // The prefill GEMMs' f16 hi/lo planes of every layer's q|k|v and o weights (75.5 MB a layer;
+    // 40.1 MB in q8_0, whose GEMM keeps the values and the block scales), one allocation made at
+    // the first prefill block that takes the GEMM, layer il's at planes_off[il]; a layer's planes are built
     // on the stream of its first such block and read by every later one. planes_on: the caller's
     // switch (flint_attn_model_set_weight_planes). A failed allocation is tried once per prefill
     // call (planes_failed_call: the call it failed in), and the projections rebuild the planes in
@@ -168,6 +169,7 @@ struct flint_attn_model {
     bool planes_on = true;
     uint64_t prefill_call = 0, planes_failed_call = 0;
     std::vector<uint8_t> planes_built;
+    std::vector<size_t> planes_off;
     // Engine::last_gpu_ms and its profiler (enable_profiling / last_profile, engine.h:54-56, 63):
     // marks are HIP events recorded on the call's stream, mark 0 where a step or prefill starts,
     // then one where it ends or, with profiling on, one after each stage (the embedding, then per
@@ -187,8 +189,11 @@ struct flint_attn_model {
         if (att) (void)hipFree(att);
         if (planes) (void)hipFree(planes);
     }
-    static size_t layer_planes_bytes() {
-        return planes_bytes(FLINT_QKV_DIM, FLINT_N_EMBD) + planes_bytes(FLINT_N_EMBD, FLINT_Q_DIM);
+    static size_t qkv_planes_bytes(const Layer &L) {
+        return planes_bytes(FLINT_QKV_DIM, FLINT_N_EMBD, qkv_gemm_q8(&L.q, &L.k, &L.v));
+    }
+    static size_t layer_planes_bytes(const Layer &L) {
+        return qkv_planes_bytes(L) + planes_bytes(FLINT_N_EMBD, FLINT_Q_DIM, o_gemm_q8(&L.o));
     }
     // the layer's q|k|v and o planes, built on `stream` if this is the first use; false when
     // there is no memory for them
@@ -196,7 +201,9 @@ struct flint_attn_model {
         if (!planes_on) return false;
         if (!planes) {
             if (planes_failed_call == prefill_call) return false;  // already failed in this call
-            if (hipMalloc(&planes, layers.size() * layer_planes_bytes()) != hipSuccess) {
+            planes_off.assign(layers.size() + 1, 0);
+            for (size_t i = 0; i < layers.size(); i++) planes_off[i + 1] = planes_off[i] + layer_planes_bytes(layers[i]);
+            if (hipMalloc(&planes, planes_off.back()) != hipSuccess) {
                 (void)hipGetLastError();  // clear the allocation error; the projections work without planes
                 planes = nullptr;
                 planes_failed_call = prefill_call;
@@ -205,12 +212,11 @@ struct flint_attn_model {
             planes_failed_call = 0;
             planes_built.assign(layers.size(), 0);
         }
-        char *base = (char *)planes + (size_t)il * layer_planes_bytes();
-        const WeightPlanes pq = planes_at(base, FLINT_QKV_DIM, FLINT_N_EMBD);
-        const WeightPlanes po =
-            planes_at(base + planes_bytes(FLINT_QKV_DIM, FLINT_N_EMBD), FLINT_N_EMBD, FLINT_Q_DIM);
+        const Layer &L = layers[il];
+        char *base = (char *)planes + planes_off[il];
+        const WeightPlanes pq = planes_at(base, FLINT_QKV_DIM, FLINT_N_EMBD, qkv_gemm_q8(&L.q, &L.k, &L.v));
+        const WeightPlanes po = planes_at(base + qkv_planes_bytes(L), FLINT_N_EMBD, FLINT_Q_DIM, o_gemm_q8(&L.o));
         if (!planes_built[il]) {
-            const Layer &L = layers[il];
             build_qkv_planes(&L.q, &L.k, &L.v, pq, stream);
             build_o_planes(&L.o, po, stream);
             planes_built[il] = 1;

@@ -90,7 +90,8 @@ int32_t flint_attn_model_block_prefill(flint_attn_model *m, int32_t il, float *X
 /*
  * The prefill projections' kept weight planes (no counterpart in the reference): from the first
  * prefill block of 16 or more tokens, a model keeps every layer's q|k|v and o weights as f16
- * hi/lo planes in one device allocation (75.5 MB a layer, 3.7 GB for Flint's 49), so later
+ * hi/lo planes in one device allocation (75.5 MB a layer; 40.1 MB for q8_0 weights, kept as
+ * their values and block scales: 2.0 GB for Flint's 49 layers in q8_0), so later
  * prefill blocks skip their per-call weight prep. on = 0 frees them (after a device
  * synchronize) and prefill rebuilds the planes in its workspace on every call; on = 1 (the
  * default) allows them again. When the allocation fails, prefill goes on without them and
