@@ -360,19 +360,29 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemm3_kernel(const GemmParams P
         if (t >= P.T) continue;
         const int et = P.eexp[t];
         float *yt = P.y + (size_t)t * P.y_stride;
+        // the exponents and the residual (add) first: a load after a store to y that may alias it
+        // waits for that store
+        int4 f[2][4];
+        f32x4 yin[2][4];
 #pragma unroll
         for (int a = 0; a < 2; a++)
 #pragma unroll
             for (int q = 0; q < 4; q++) {
                 const int n = n0 + 64 * wn + 32 * a + 8 * q + 4 * (lane >> 5);
-                const int4 f = *(const int4 *)(P.fexp + n);
-                f32x4 v = {__builtin_amdgcn_ldexpf(acc[a][b][4 * q], et + f.x),
-                           __builtin_amdgcn_ldexpf(acc[a][b][4 * q + 1], et + f.y),
-                           __builtin_amdgcn_ldexpf(acc[a][b][4 * q + 2], et + f.z),
-                           __builtin_amdgcn_ldexpf(acc[a][b][4 * q + 3], et + f.w)};
-                f32x4 *dst = (f32x4 *)(yt + n);
-                if (P.add) v += *dst;
-                *dst = v;
+                f[a][q] = *(const int4 *)(P.fexp + n);
+                if (P.add) yin[a][q] = *(const f32x4 *)(yt + n);
+            }
+#pragma unroll
+        for (int a = 0; a < 2; a++)
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const int n = n0 + 64 * wn + 32 * a + 8 * q + 4 * (lane >> 5);
+                f32x4 v = {__builtin_amdgcn_ldexpf(acc[a][b][4 * q], et + f[a][q].x),
+                           __builtin_amdgcn_ldexpf(acc[a][b][4 * q + 1], et + f[a][q].y),
+                           __builtin_amdgcn_ldexpf(acc[a][b][4 * q + 2], et + f[a][q].z),
+                           __builtin_amdgcn_ldexpf(acc[a][b][4 * q + 3], et + f[a][q].w)};
+                if (P.add) v += yin[a][q];
+                *(f32x4 *)(yt + n) = v;
             }
     }
 }
@@ -509,22 +519,36 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemmq8_kernel(const GemmParams 
     wait_vmcnt<0>();  // the re-read past the last chunk lands before the workgroup's LDS goes
     // epilogue: block (a, b) element e is token t0 + 64 wt + 32 a + 8 (e >> 2) + 4 (lane >> 5) + (e & 3)
     // and weight row n0 + 64 wn + 32 b + (lane & 31): a store instruction writes 32 consecutive
-    // floats of each of two token rows
+    // floats of each of two token rows. Token block a by token block a, its row exponents and
+    // its residual (add) are all read before its first store (rows past T re-read row T - 1): a
+    // load after a store that may alias it waits for the store, so loads between the stores cost
+    // a round trip each (36 us per o launch at T = 4000).
+    auto row = [&](int a, int e) { return min(t0 + 64 * wt + 32 * a + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3), P.T - 1); };
+    float *const y0 = P.y + n0 + 64 * wn + (lane & 31);
 #pragma unroll
-    for (int a = 0; a < 2; a++)
+    for (int a = 0; a < 2; a++) {
+        int ex[16];
+        float yin[16][2];
+#pragma unroll
+        for (int e = 0; e < 16; e++) ex[e] = P.eexp[row(a, e)];
+        if (P.add) {
+#pragma unroll
+            for (int e = 0; e < 16; e++)
+#pragma unroll
+                for (int b = 0; b < 2; b++) yin[e][b] = y0[(size_t)row(a, e) * P.y_stride + 32 * b];
+        }
 #pragma unroll
         for (int e = 0; e < 16; e++) {
             const int t = t0 + 64 * wt + 32 * a + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
             if (t >= P.T) continue;
-            const int et = P.eexp[t];
-            float *yt = P.y + (size_t)t * P.y_stride + n0 + 64 * wn + (lane & 31);
 #pragma unroll
             for (int b = 0; b < 2; b++) {
-                float v = __builtin_amdgcn_ldexpf(acc[a][b][e], et);
-                if (P.add) v += yt[32 * b];
-                yt[32 * b] = v;
+                float v = __builtin_amdgcn_ldexpf(acc[a][b][e], ex[e]);
+                if (P.add) v += yin[e][b];
+                y0[(size_t)t * P.y_stride + 32 * b] = v;
             }
         }
+    }
 }
 
 hipError_t launch_proj_gemm(const GemmWeightParams &W, const GemmActParams &X, const GemmParams &G, bool prep_weights,
