@@ -143,6 +143,64 @@ __device__ inline void deq32(int type, const uint8_t *row, int sb, float (&w)[32
     }
 }
 
+// The integer form of sub-block sb (w_int_sub), for the batched projections: its 32 values v
+// and the scales s of elements 0-15 (s[0]) and 16-31 (s[1]), computed in ggml's float order,
+// so that s * v is deq32's weight. Only for types with w_int_sub(type) > 0.
+__device__ inline void deq32_int(int type, const uint8_t *row, int sb, _Float16 (&v)[32], float (&s)[2]) {
+#pragma clang fp contract(off)
+    switch (type) {
+        case W_Q8_0: {  // y = q * d
+            const uint16_t *p = (const uint16_t *)(row + 34 * sb);
+            s[0] = s[1] = h2f(p[0]);
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const uint32_t u = p[1 + i];
+                v[2 * i] = (_Float16)(int8_t)(u & 0xff);
+                v[2 * i + 1] = (_Float16)(int8_t)(u >> 8);
+            }
+            break;
+        }
+        case W_Q6_K: {  // y = (d * sc) * (q6 - 32)
+            const uint8_t *blk = row + 210 * (sb >> 3);
+            const int j = sb & 7, n = j >> 2, g = j & 3;
+            const uint16_t *ql = (const uint16_t *)(blk + 64 * n + 32 * (g & 1));
+            const uint16_t *qh = (const uint16_t *)(blk + 128 + 32 * n);
+            const uint32_t scw = *(const uint16_t *)(blk + 192 + 8 * n + 2 * g);
+            const float d = h2f(*(const uint16_t *)(blk + 208));
+            s[0] = d * (float)(int8_t)(scw & 0xff), s[1] = d * (float)(int8_t)(scw >> 8);
+            const int lsh = 4 * (g >> 1), hsh = 2 * g;
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const uint32_t lo = ql[i], hi = qh[i];
+#pragma unroll
+                for (int b = 0; b < 2; b++)
+                    v[2 * i + b] = (_Float16)((int)((((lo >> (8 * b)) >> lsh) & 15) | ((((hi >> (8 * b)) >> hsh) & 3) << 4)) - 32);
+            }
+            break;
+        }
+        case W_IQ4_XS: {  // y = (d * (ls - 32)) * table[nibble]
+            const uint8_t *blk = row + 136 * (sb >> 3);
+            const int ib = sb & 7;
+            const uint2 hdr = *(const uint2 *)blk;
+            const uint32_t ls = ((hdr.y >> (8 * (ib >> 1) + 4 * (ib & 1))) & 15) | (((hdr.x >> (16 + 2 * ib)) & 3) << 4);
+            s[0] = s[1] = h2f(hdr.x & 0xffff) * (float)((int)ls - 32);
+            const uint2 q0 = *(const uint2 *)(blk + 8 + 16 * ib), q1 = *(const uint2 *)(blk + 16 + 16 * ib);
+            const uint32_t qs[4] = {q0.x, q0.y, q1.x, q1.y};
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const uint32_t u = byte_of(qs, i);
+                v[i] = (_Float16)iq4_value(u & 15);
+                v[i + 16] = (_Float16)iq4_value(u >> 4);
+            }
+            break;
+        }
+        default:
+            s[0] = s[1] = 0.f;
+#pragma unroll
+            for (int i = 0; i < 32; i++) v[i] = 0;
+    }
+}
+
 __device__ inline bool w_is_float(int t) { return t == W_F32 || t == W_F16 || t == W_BF16; }
 
 }  // namespace flint

@@ -402,11 +402,11 @@ void proj_gemm(const MatvecSeg *seg, int n_seg, int N, int K, const float *x, lo
     W.wh = pl ? pl->wh : (_Float16 *)(ws + o_wh);
     W.wl = pl ? pl->wl : (_Float16 *)(ws + o_wl);
     W.fexp = pl ? pl->fexp : (int *)(ws + o_f);
-    // every segment q8_0: the q8 form (the values in wh, the block scales in wl's memory: N K / 32
-    // floats, in the workspace with room to spare, in kept planes laid out for it)
-    W.q8 = gemm_q8(seg, n_seg);
+    // every segment in the integer form: the values in wh, the scales in wl's memory (N K / isub
+    // floats: in the workspace with room to spare, in kept planes laid out for it)
+    W.isub = gemm_int_sub(seg, n_seg);
     W.wd = (float *)W.wl;
-    if (pl && !W.q8 && !pl->fexp) throw Error("projection GEMM: weight planes laid out for q8_0 weights");
+    if (pl && !W.isub && !pl->fexp) throw Error("projection GEMM: weight planes laid out for the integer form");
     GemmActParams X{};
     X.norm_w = norm_w;
     X.eps = eps;
@@ -415,7 +415,7 @@ void proj_gemm(const MatvecSeg *seg, int n_seg, int N, int K, const float *x, lo
     X.eexp = (int *)(ws + o_e);
     GemmParams G{};
     G.wh = W.wh, G.wl = W.wl, G.fexp = W.fexp, G.xh = X.xh, G.xl = X.xl, G.eexp = X.eexp;
-    G.q8 = W.q8, G.wd = W.wd;
+    G.isub = W.isub, G.wd = W.wd;
     G.add = add;
     G.N = N;
     G.K = K;
@@ -515,32 +515,40 @@ void o_proj_impl(const flint_weight *wo, const float *att, int n_tok, float *x, 
 
 }  // namespace
 
-bool gemm_q8(const MatvecSeg *seg, int n_seg) {
-    bool q8 = n_seg > 0;
-    for (int i = 0; i < n_seg; i++) q8 = q8 && seg[i].type == W_Q8_0;
-    return q8;
+// 0 when a segment is not of the integer form; else the smallest of their scale spans
+static int int_sub_of(const int *types, int n) {
+    int sub = n > 0 ? 32 : 0;
+    for (int i = 0; i < n; i++) sub = std::min(sub, w_int_sub(types[i]));
+    return sub;
 }
 
-bool qkv_gemm_q8(const flint_weight *wq, const flint_weight *wk, const flint_weight *wv) {
-    return wq->type == W_Q8_0 && wk->type == W_Q8_0 && wv->type == W_Q8_0;
+int gemm_int_sub(const MatvecSeg *seg, int n_seg) {
+    int t[3];
+    for (int i = 0; i < n_seg; i++) t[i] = seg[i].type;
+    return int_sub_of(t, n_seg);
 }
 
-bool o_gemm_q8(const flint_weight *wo) { return wo->type == W_Q8_0; }
+int qkv_gemm_sub(const flint_weight *wq, const flint_weight *wk, const flint_weight *wv) {
+    const int t[3] = {wq->type, wk->type, wv->type};
+    return int_sub_of(t, 3);
+}
+
+int o_gemm_sub(const flint_weight *wo) { return int_sub_of(&wo->type, 1); }
 
 static size_t align256(size_t b) { return (b + 255) / 256 * 256; }
 
-size_t planes_bytes(int N, int K, bool q8) {
+size_t planes_bytes(int N, int K, int isub) {
     const size_t w = align256((size_t)N * K * sizeof(_Float16));
-    if (q8) return w + align256((size_t)N * (K / 32) * sizeof(float));
+    if (isub) return w + align256((size_t)N * (K / isub) * sizeof(float));
     return 2 * w + align256((size_t)N * sizeof(int));
 }
 
-WeightPlanes planes_at(void *mem, int N, int K, bool q8) {
+WeightPlanes planes_at(void *mem, int N, int K, int isub) {
     const size_t w = align256((size_t)N * K * sizeof(_Float16));
     WeightPlanes pl;
     pl.wh = (_Float16 *)mem;
     pl.wl = (_Float16 *)((char *)mem + w);
-    pl.fexp = q8 ? nullptr : (int *)((char *)mem + 2 * w);
+    pl.fexp = isub ? nullptr : (int *)((char *)mem + 2 * w);
     return pl;
 }
 

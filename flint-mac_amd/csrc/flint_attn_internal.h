@@ -92,6 +92,10 @@ hipError_t launch_prefill(const PrefillParams &P, int dtype, hipStream_t stream)
 
 // Weight formats of the attention projections (ggml type ids, /root/reference/src/gguf.h:14-19)
 constexpr int W_F32 = 0, W_F16 = 1, W_Q8_0 = 8, W_Q5_K = 13, W_Q6_K = 14, W_IQ4_XS = 23, W_BF16 = 30;
+// The batched projections' integer form: q8_0, iq4_xs and q6_K weights are v * s with v an
+// integer of magnitude at most 127 (exact in f16) and s the scale of 32 (q8_0, iq4_xs) or 16
+// (q6_K) consecutive elements; 0: not of that form.
+__host__ __device__ constexpr int w_int_sub(int t) { return t == W_Q8_0 || t == W_IQ4_XS ? 32 : t == W_Q6_K ? 16 : 0; }
 
 struct MatvecSeg {         // rows [row0, row0 + rows) of one launch come from one tensor
     const uint8_t *w;      // its first row (16-byte aligned)
@@ -127,10 +131,11 @@ struct GemmWeightParams {  // wprep: rows [0, N) of the segments -> wh, wl [N][K
     int n_seg;
     _Float16 *wh, *wl;
     int *fexp;
-    // q8: every segment is q8_0; then wh holds the quantised values (exact in f16) and wd the
-    // blocks' scales, [N / 128 row tiles][K / 32 blocks][128 rows] floats (in wl's memory), and
-    // the GEMM takes the q8 form
-    int q8;
+    // isub: every segment in the integer form (w_int_sub), 32 if all scales cover 32 elements,
+    // else 16; then wh holds the values and wd the scales, [N / 128 row tiles][K / 32 blocks]
+    // [32 / isub][128 rows] floats (in wl's memory), and the GEMM takes the integer form.
+    // 0: the hi/lo planes.
+    int isub;
     float *wd;
 };
 struct GemmActParams {     // xprep: rows [0, T_pad) -> xh, xl [T_pad][K], eexp [T_pad]
@@ -145,7 +150,7 @@ struct GemmActParams {     // xprep: rows [0, T_pad) -> xh, xl [T_pad][K], eexp 
 struct GemmParams {
     const _Float16 *wh, *wl, *xh, *xl;
     const int *fexp, *eexp;
-    int q8;                // the weights as q8_0 values and block scales (GemmWeightParams::q8)
+    int isub;              // the weights as integer values and scales (GemmWeightParams::isub)
     const float *wd;
     float *y;              // [T] rows of y_stride floats (16-byte aligned, stride a multiple of 4)
     long long y_stride;
@@ -160,20 +165,20 @@ hipError_t launch_proj_gemm(const GemmWeightParams &W, const GemmActParams &X, c
 int matvec_row_multiple(int k);  // n_rows of a matvec launch must be a multiple of this
 
 // A projection's weight planes kept by a caller that runs many batches through the same weights
-// (the model's layer-major prefill): one device block of planes_bytes(N, K, q8) holding wh, wl
+// (the model's layer-major prefill): one device block of planes_bytes(N, K, isub) holding wh, wl
 // [N][K] and fexp [N], built once with build_*_planes; the *_rows projections given them skip
-// their per-call weight prep (the planes are the same bits that prep would write). q8 (every
-// weight of the projection in q8_0, gemm_q8): wh holds the values and wl's place the block
-// scales, N K / 32 floats, with no fexp.
+// their per-call weight prep (the planes are the same bits that prep would write). isub > 0 (the
+// projection's integer form, gemm_int_sub): wh holds the values and wl's place the scales,
+// N K / isub floats, with no fexp.
 struct WeightPlanes {
     _Float16 *wh = nullptr, *wl = nullptr;
     int *fexp = nullptr;
 };
-bool gemm_q8(const MatvecSeg *seg, int n_seg);  // the GEMM's q8_0 form: every segment in q8_0
-bool qkv_gemm_q8(const flint_weight *wq, const flint_weight *wk, const flint_weight *wv);
-bool o_gemm_q8(const flint_weight *wo);
-size_t planes_bytes(int N, int K, bool q8);
-WeightPlanes planes_at(void *mem, int N, int K, bool q8);
+int gemm_int_sub(const MatvecSeg *seg, int n_seg);  // the GEMM's integer form: 32, 16 or 0
+int qkv_gemm_sub(const flint_weight *wq, const flint_weight *wk, const flint_weight *wv);
+int o_gemm_sub(const flint_weight *wo);
+size_t planes_bytes(int N, int K, int isub);
+WeightPlanes planes_at(void *mem, int N, int K, int isub);
 void build_qkv_planes(const flint_weight *wq, const flint_weight *wk, const flint_weight *wv, const WeightPlanes &pl,
                       hipStream_t stream);
 void build_o_planes(const flint_weight *wo, const WeightPlanes &pl, hipStream_t stream);

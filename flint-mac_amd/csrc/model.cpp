@@ -159,7 +159,7 @@ struct flint_attn_model {
     int cap = 0;
     int32_t n_ctx = 0, pos = 0;  // the session: context length and tokens processed
     // The prefill GEMMs' f16 hi/lo planes of every layer's q|k|v and o weights (75.5 MB a layer;
-    // 40.1 MB in q8_0, whose GEMM keeps the values and the block scales), one allocation made at
+    // 40.1 MB in q8_0, whose GEMM keeps the integer values and the block scales), one allocation made at
     // the first prefill block that takes the GEMM, layer il's at planes_off[il]; a layer's planes are built
     // on the stream of its first such block and read by every later one. planes_on: the caller's
     // switch (flint_attn_model_set_weight_planes). A failed allocation is tried once per prefill
@@ -190,10 +190,10 @@ struct flint_attn_model {
         if (planes) (void)hipFree(planes);
     }
     static size_t qkv_planes_bytes(const Layer &L) {
-        return planes_bytes(FLINT_QKV_DIM, FLINT_N_EMBD, qkv_gemm_q8(&L.q, &L.k, &L.v));
+        return planes_bytes(FLINT_QKV_DIM, FLINT_N_EMBD, qkv_gemm_sub(&L.q, &L.k, &L.v));
     }
     static size_t layer_planes_bytes(const Layer &L) {
-        return qkv_planes_bytes(L) + planes_bytes(FLINT_N_EMBD, FLINT_Q_DIM, o_gemm_q8(&L.o));
+        return qkv_planes_bytes(L) + planes_bytes(FLINT_N_EMBD, FLINT_Q_DIM, o_gemm_sub(&L.o));
     }
     // the layer's q|k|v and o planes, built on `stream` if this is the first use; false when
     // there is no memory for them
@@ -214,8 +214,8 @@ struct flint_attn_model {
         }
         const Layer &L = layers[il];
         char *base = (char *)planes + planes_off[il];
-        const WeightPlanes pq = planes_at(base, FLINT_QKV_DIM, FLINT_N_EMBD, qkv_gemm_q8(&L.q, &L.k, &L.v));
-        const WeightPlanes po = planes_at(base + qkv_planes_bytes(L), FLINT_N_EMBD, FLINT_Q_DIM, o_gemm_q8(&L.o));
+        const WeightPlanes pq = planes_at(base, FLINT_QKV_DIM, FLINT_N_EMBD, qkv_gemm_sub(&L.q, &L.k, &L.v));
+        const WeightPlanes po = planes_at(base + qkv_planes_bytes(L), FLINT_N_EMBD, FLINT_Q_DIM, o_gemm_sub(&L.o));
         if (!planes_built[il]) {
             build_qkv_planes(&L.q, &L.k, &L.v, pq, stream);
             build_o_planes(&L.o, po, stream);

@@ -124,36 +124,34 @@ __global__ __launch_bounds__(512) void wprep_kernel(const GemmWeightParams P) {
 
 
 // ---------------------------------------------------------------------------
-// The q8_0 form. A q8_0 weight is d q, with q an integer of magnitude at most 127 (exact in f16)
-// and d its 32-element block's scale, and a 32-k chunk of the GEMM is one block. So a chunk's
-// products are sum_k (xh + xl) q on the matrix cores, two products per pair instead of gemm3's
-// three and no weight lo plane, and the scale joins in fp32: acc += d T, one d per weight row and
-// chunk. The x planes are gemm3's.
+// The integer form. A q8_0, iq4_xs or q6_K weight is s v, with v an integer of magnitude at most
+// 127 (exact in f16) and s the scale of its 32 (q8_0, iq4_xs) or 16 (q6_K) elements, and a 32-k
+// chunk of the GEMM is one 32-element sub-block. So a chunk's products are sum_k (xh + xl) v on
+// the matrix cores, two products per pair instead of gemm3's three and no weight lo plane, and
+// the scale joins in fp32: acc += s T, one s per weight row and chunk (SUB = 32) or k-step of 16
+// (SUB = 16). The x planes are gemm3's.
 //
-// wprep_q8: thread (row n, block b) writes the block's 32 values as f16 into the plane's chunk
-// order (plane_unit) and d into wd[n / 128][b][n % 128].
-template <int K>
-__global__ __launch_bounds__(256) void wprep_q8_kernel(const GemmWeightParams P) {
-    constexpr int NB = K / 32;
-    const int idx = blockIdx.x * 256 + threadIdx.x, n = idx / NB, b = idx % NB;  // block fastest
+// wprep_int: thread (row n, sub-block b) writes the sub-block's 32 values as f16 into the plane's
+// chunk order (plane_unit) and its scales into wd[n / 128][b][32 / SUB][n % 128].
+template <int K, int SUB>
+__global__ __launch_bounds__(256) void wprep_int_kernel(const GemmWeightParams P) {
+    constexpr int NB = K / 32, NS = 32 / SUB;
+    const int idx = blockIdx.x * 256 + threadIdx.x, n = idx / NB, b = idx % NB;  // sub-block fastest
     const int in2 = P.n_seg > 2 && n >= P.seg[2].row0, in1 = !in2 && P.n_seg > 1 && n >= P.seg[1].row0;
     const MatvecSeg S = in2 ? P.seg[2] : in1 ? P.seg[1] : P.seg[0];
-    // a block: f16 d, then 32 int8 values; 2-byte aligned (34-byte blocks)
-    const uint16_t *blk = (const uint16_t *)(S.w + (size_t)(n - S.row0) * S.row_bytes + 34 * b);
-    uint16_t w[17];
-#pragma unroll
-    for (int i = 0; i < 17; i++) w[i] = blk[i];
+    _Float16 v[32];
+    float sc[2];
+    deq32_int(S.type, S.w + (size_t)(n - S.row0) * S.row_bytes, b, v, sc);
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-        f16x8 v;
+        f16x8 u;
 #pragma unroll
-        for (int e = 0; e < 8; e++) {
-            const int k = 8 * j + e;  // byte k of the values: half k >> 1 of words 1 ..
-            v[e] = (_Float16)(int8_t)(w[1 + (k >> 1)] >> (8 * (k & 1)));
-        }
-        *(f16x8 *)(P.wh + plane_unit(n, 4 * b + j, K)) = v;
+        for (int e = 0; e < 8; e++) u[e] = v[8 * j + e];
+        *(f16x8 *)(P.wh + plane_unit(n, 4 * b + j, K)) = u;
     }
-    P.wd[((size_t)(n >> 7) * NB + b) * GEMM_TILE + (n & 127)] = (float)__builtin_bit_cast(_Float16, w[0]);
+    float *const d = P.wd + (((size_t)(n >> 7) * NB + b) * NS) * GEMM_TILE + (n & 127);
+    d[0] = sc[0];  // SUB = 32: the two halves' scales are one
+    if constexpr (NS == 2) d[GEMM_TILE] = sc[1];
 }
 
 // ---------------------------------------------------------------------------
@@ -388,18 +386,23 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemm3_kernel(const GemmParams P
 }
 
 
-// gemm_q8: gemm3's tiles, deal and LDS order with the tokens as operand A and the weights'
+// gemm_int: gemm3's tiles, deal and LDS order with the tokens as operand A and the weights'
 // values as operand B, so that an MFMA output lane holds one weight row (16 tokens of it) and
-// takes one d per chunk. The chunks go straight from memory into LDS (global_load_lds_dwordx4:
-// each wave-wide load writes 1 KiB, lane l's 16 bytes at l * 16 from the wave's LDS address),
-// three stages deep: while chunk c is computed, chunks c + 1 and c + 2 are in flight, and no
-// register holds them. A chunk's 128 scales ride along (lanes 0-7 of each wave load 128 bytes).
-// Each step makes one chunk's products T = sum (xh + xl) q, four independent chains of four MFMAs,
-// and scales the chunk before's (acc += d T) in between, so that those FMAs run beside MFMAs that
-// do not feed them (two register sets for T take turns). Against one chunk's MFMAs and FMAs in
-// the same step: 4000 tokens through 49 Flint blocks 23.2 against 24.0 ms.
-constexpr int GQ_STAGE = 3 * GM_PLANE_CHUNK + GM_TILE * 4;  // x hi, x lo, weight values, scales
-constexpr int GQ_LOADS = 7;                                 // direct loads per wave per chunk
+// takes one scale per chunk (SUB = 32) or k-step (SUB = 16). The chunks go straight from memory
+// into LDS (global_load_lds_dwordx4: each wave-wide load writes 1 KiB, lane l's 16 bytes at
+// l * 16 from the wave's LDS address), three stages deep: while chunk c is computed, chunks c + 1
+// and c + 2 are in flight, and no register holds them. A chunk's 128 (SUB = 32) or 256 scales
+// ride along (lanes 0-7 or 0-15 of each wave load 128 or 256 bytes).
+// Each step makes the products T = sum (xh + xl) v of one chunk (SUB = 32: four independent
+// chains of four MFMAs) or k-step (SUB = 16: chains of two), and scales the step before's
+// (acc += s T) in between, so that those FMAs run beside MFMAs that do not feed them (two
+// register sets for T take turns). Against one chunk's MFMAs and FMAs in the same step, q8_0:
+// 4000 tokens through 49 Flint blocks 23.2 against 24.0 ms.
+template <int SUB>
+constexpr int gq_scales() { return (32 / SUB) * GM_TILE; }  // a chunk's scales, per row tile
+template <int SUB>
+constexpr int gq_stage() { return 3 * GM_PLANE_CHUNK + gq_scales<SUB>() * 4; }  // x hi, x lo, values, scales
+constexpr int GQ_LOADS = 7;                                                       // direct loads per wave per chunk
 
 typedef __attribute__((address_space(3))) void lds_void;
 
@@ -409,8 +412,10 @@ __device__ inline void wait_vmcnt() {  // s_waitcnt vmcnt(N), other counters unt
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-__global__ __launch_bounds__(GM_THREADS, 2) void gemmq8_kernel(const GemmParams P) {
-    __shared__ __align__(16) uint8_t lds[3][GQ_STAGE];
+template <int SUB>
+__global__ __launch_bounds__(GM_THREADS, 2) void gemm_int_kernel(const GemmParams P) {
+    constexpr int SCB = gq_scales<SUB>(), SCL = SCB / 16;  // scales per chunk; lanes that load them
+    __shared__ __align__(16) uint8_t lds[3][gq_stage<SUB>()];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wn = wave & 1, wt = wave >> 1;
@@ -429,7 +434,7 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemmq8_kernel(const GemmParams 
     // this lane's units tid and tid + 256 of each plane's chunk; its 16 bytes of the scales
     const _Float16 *src[3] = {P.xh + (size_t)t0 * K + 8 * tid, P.xl + (size_t)t0 * K + 8 * tid,
                               P.wh + (size_t)n0 * K + 8 * tid};
-    const float *srcd = P.wd + (size_t)nt * (K / GM_KC) * GM_TILE + 4 * (8 * wave + (lane & 7));
+    const float *srcd = P.wd + (size_t)nt * (K / GM_KC) * SCB + SCB / 4 * wave + 4 * (lane & (SCL - 1));
     const int n_chunks = K / GM_KC;
     auto issue = [&](int c, int st) {  // chunk c into stage st
         uint8_t *const base = lds[st];
@@ -440,9 +445,9 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemmq8_kernel(const GemmParams 
                 __builtin_amdgcn_global_load_lds(src[p] + (size_t)c * GM_TILE * GM_KC + 2048 * i,
                                                  (lds_void *)(base + p * GM_PLANE_CHUNK + (256 * i + 64 * wave) * 16),
                                                  16, 0, 0);
-        if (lane < 8)
-            __builtin_amdgcn_global_load_lds(srcd + (size_t)c * GM_TILE,
-                                             (lds_void *)(base + 3 * GM_PLANE_CHUNK + 128 * wave), 16, 0, 0);
+        if (lane < SCL)
+            __builtin_amdgcn_global_load_lds(srcd + (size_t)c * SCB,
+                                             (lds_void *)(base + 3 * GM_PLANE_CHUNK + SCB * wave), 16, 0, 0);
     };
     f32x16 acc[2][2];  // [token block][weight block]
 #pragma unroll
@@ -456,10 +461,13 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemmq8_kernel(const GemmParams 
 #pragma unroll
         for (int b = 0; b < 2; b++) TB[a][b] = f32x16{};
     dB[0] = dB[1] = 0.f;
-    auto step = [&](int st, f32x16 (&T)[2][2], float (&dn)[2], const f32x16 (&Tp)[2][2], const float (&dp)[2]) {
+    // one step: the products of k-steps s0 .. s1 - 1 of the chunk in stage st into T, the step
+    // before's products Tp scaled into acc, this step's scales into dn
+    auto step = [&](int st, int s0, int s1, f32x16 (&T)[2][2], float (&dn)[2], const f32x16 (&Tp)[2][2],
+                    const float (&dp)[2]) {
         const uint8_t *const base = lds[st];
 #pragma unroll
-        for (int s = 0; s < 2; s++) {
+        for (int s = s0; s < s1; s++) {
             f16x8 xh[2], xl[2], wq[2];
 #pragma unroll
             for (int j = 0; j < 2; j++) {
@@ -472,12 +480,12 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemmq8_kernel(const GemmParams 
 #pragma unroll
             for (int a = 0; a < 2; a++)
 #pragma unroll
-                for (int b = 0; b < 2; b++) T[a][b] = mfma32_f16(xh[a], wq[b], s == 0 ? f32x16{} : T[a][b]);
+                for (int b = 0; b < 2; b++) T[a][b] = mfma32_f16(xh[a], wq[b], s == s0 ? f32x16{} : T[a][b]);
 #pragma unroll
             for (int a = 0; a < 2; a++)
 #pragma unroll
                 for (int b = 0; b < 2; b++) T[a][b] = mfma32_f16(xl[a], wq[b], T[a][b]);
-            if (s == 0) {
+            if (s == s0) {
 #pragma unroll
                 for (int b = 0; b < 2; b++)
 #pragma unroll
@@ -486,8 +494,9 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemmq8_kernel(const GemmParams 
                         for (int e = 0; e < 16; e++) acc[a][b][e] = fmaf(dp[b], Tp[a][b][e], acc[a][b][e]);
             }
         }
+        const float *const sc = (const float *)(base + 3 * GM_PLANE_CHUNK) + (SUB == 16 ? GM_TILE * s0 : 0);
 #pragma unroll
-        for (int b = 0; b < 2; b++) dn[b] = *(const float *)(base + 3 * GM_PLANE_CHUNK + 4 * (64 * wn + 32 * b + (lane & 31)));
+        for (int b = 0; b < 2; b++) dn[b] = sc[64 * wn + 32 * b + (lane & 31)];
     };
     // Chunk c lives in stage c % 3. Every wave issues the same GQ_LOADS loads per chunk (past the
     // last chunk it re-reads the last one into a stage no one reads again), so "chunk c has
@@ -506,9 +515,17 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemmq8_kernel(const GemmParams 
     };
     issue(0, 0);
     issue(1, 1);
-    for (int c = 0; c < n_chunks; c += 2) {  // K is a multiple of 64: the chunk count is even
-        step(sync(c), TA, dA, TB, dB);
-        step(sync(c + 1), TB, dB, TA, dA);
+    if constexpr (SUB == 32) {
+        for (int c = 0; c < n_chunks; c += 2) {  // K is a multiple of 64: the chunk count is even
+            step(sync(c), 0, 2, TA, dA, TB, dB);
+            step(sync(c + 1), 0, 2, TB, dB, TA, dA);
+        }
+    } else {
+        for (int c = 0; c < n_chunks; c++) {
+            const int st = sync(c);
+            step(st, 0, 1, TA, dA, TB, dB);
+            step(st, 1, 2, TB, dB, TA, dA);
+        }
     }
 #pragma unroll
     for (int b = 0; b < 2; b++)
@@ -555,19 +572,20 @@ hipError_t launch_proj_gemm(const GemmWeightParams &W, const GemmActParams &X, c
                             hipStream_t stream) {
     // the planes' chunk order and the GEMM's tiles need whole 128-row tiles of both operands
     if (G.N % GM_TILE != 0 || X.T_pad % GM_TILE != 0 || (G.K != 2048 && G.K != 4096)) return hipErrorInvalidValue;
-    if (G.q8) {
+    if (G.isub == 32 || G.isub == 16) {
+        const bool s32 = G.isub == 32;
         if (prep_weights) {
-            if (G.K == 2048)
-                hipLaunchKernelGGL(wprep_q8_kernel<2048>, dim3(G.N * (2048 / 32) / 256), dim3(256), 0, stream, W);
-            else
-                hipLaunchKernelGGL(wprep_q8_kernel<4096>, dim3(G.N * (4096 / 32) / 256), dim3(256), 0, stream, W);
+            void (*wk)(GemmWeightParams) = G.K == 2048 ? (s32 ? wprep_int_kernel<2048, 32> : wprep_int_kernel<2048, 16>)
+                                                       : (s32 ? wprep_int_kernel<4096, 32> : wprep_int_kernel<4096, 16>);
+            hipLaunchKernelGGL(wk, dim3(G.N * (G.K / 32) / 256), dim3(256), 0, stream, W);
         }
         if (X.T_pad > 0) {
             if (G.K == 2048)
                 hipLaunchKernelGGL(xprep_kernel<2048>, dim3(X.T_pad / 8), dim3(512), 0, stream, X);
             else
                 hipLaunchKernelGGL(xprep_kernel<4096>, dim3(X.T_pad / 8), dim3(512), 0, stream, X);
-            hipLaunchKernelGGL(gemmq8_kernel, dim3(G.N / GM_TILE * (X.T_pad / GM_TILE)), dim3(GM_THREADS), 0, stream, G);
+            void (*gk)(GemmParams) = s32 ? gemm_int_kernel<32> : gemm_int_kernel<16>;
+            hipLaunchKernelGGL(gk, dim3(G.N / GM_TILE * (X.T_pad / GM_TILE)), dim3(GM_THREADS), 0, stream, G);
         }
         return hipGetLastError();
     }
