@@ -143,11 +143,13 @@ __device__ inline void deq32(int type, const uint8_t *row, int sb, float (&w)[32
     }
 }
 
-// The integer form of sub-block sb (w_int_sub), for the batched projections: its 32 values v
-// and the scales s of elements 0-15 (s[0]) and 16-31 (s[1]), computed in ggml's float order,
-// so that s * v is deq32's weight. Only for types with w_int_sub(type) > 0.
-__device__ inline void deq32_int(int type, const uint8_t *row, int sb, _Float16 (&v)[32], float (&s)[2]) {
+// The integer form of sub-block sb (w_int_sub), for the batched projections: its 32 values v,
+// the scales s of elements 0-15 (s[0]) and 16-31 (s[1]) and the min m (q5_K; else 0), computed
+// in ggml's float order, so that s * v - m is deq32's weight (s * v when m = 0). Only for types
+// with w_int_sub(type) > 0.
+__device__ inline void deq32_int(int type, const uint8_t *row, int sb, _Float16 (&v)[32], float (&s)[2], float &m) {
 #pragma clang fp contract(off)
+    m = 0.f;
     switch (type) {
         case W_Q8_0: {  // y = q * d
             const uint16_t *p = (const uint16_t *)(row + 34 * sb);
@@ -192,6 +194,26 @@ __device__ inline void deq32_int(int type, const uint8_t *row, int sb, _Float16 
                 v[i] = (_Float16)iq4_value(u & 15);
                 v[i + 16] = (_Float16)iq4_value(u >> 4);
             }
+            break;
+        }
+        case W_Q5_K: {  // y = (d * sc) * (q4 + 16 h) - dmin * m
+            const uint8_t *blk = row + 176 * (sb >> 3);
+            const int j = sb & 7;
+            const uint32_t dm = *(const uint32_t *)blk;
+            const uint32_t sw[3] = {((const uint32_t *)(blk + 4))[0], ((const uint32_t *)(blk + 4))[1],
+                                    ((const uint32_t *)(blk + 4))[2]};
+            const uint32_t sc = j < 4 ? byte_of(sw, j) & 63 : (byte_of(sw, j + 4) & 15) | ((byte_of(sw, j - 4) >> 6) << 4);
+            const uint32_t mn = j < 4 ? byte_of(sw, j + 4) & 63 : (byte_of(sw, j + 4) >> 4) | ((byte_of(sw, j) >> 6) << 4);
+            s[0] = s[1] = h2f(dm & 0xffff) * (float)sc;
+            m = h2f(dm >> 16) * (float)mn;
+            uint32_t qh[8], ql[8];
+            *(u32x4 *)&qh[0] = ((const u32x4 *)(blk + 16))[0];
+            *(u32x4 *)&qh[4] = ((const u32x4 *)(blk + 16))[1];
+            *(u32x4 *)&ql[0] = ((const u32x4 *)(blk + 48 + 32 * (j >> 1)))[0];
+            *(u32x4 *)&ql[4] = ((const u32x4 *)(blk + 48 + 32 * (j >> 1)))[1];
+            const int ls = 4 * (j & 1);
+#pragma unroll
+            for (int i = 0; i < 32; i++) v[i] = (_Float16)(((byte_of(ql, i) >> ls) & 15) + (((byte_of(qh, i) >> j) & 1) << 4));
             break;
         }
         default:

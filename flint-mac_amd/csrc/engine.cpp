@@ -394,7 +394,9 @@ void proj_gemm(const MatvecSeg *seg, int n_seg, int N, int K, const float *x, lo
         return o;
     };
     const size_t o_wh = take(wbytes), o_wl = take(wbytes), o_f = take(pl ? 0 : (size_t)N * sizeof(int));
+    const IntForm form = gemm_int_form(seg, n_seg);
     const size_t o_xh = take(xbytes), o_xl = take(xbytes), o_e = take((size_t)T_pad * sizeof(int));
+    const size_t o_xs = take(form.min ? (size_t)T_pad * (K / 32) * sizeof(float) : 0);
     char *ws = off ? (char *)scratch().gemm.get(off) : nullptr;
     GemmWeightParams W{};
     for (int i = 0; i < n_seg; i++) W.seg[i] = seg[i];
@@ -402,10 +404,12 @@ void proj_gemm(const MatvecSeg *seg, int n_seg, int N, int K, const float *x, lo
     W.wh = pl ? pl->wh : (_Float16 *)(ws + o_wh);
     W.wl = pl ? pl->wl : (_Float16 *)(ws + o_wl);
     W.fexp = pl ? pl->fexp : (int *)(ws + o_f);
-    // every segment in the integer form: the values in wh, the scales in wl's memory (N K / isub
-    // floats: in the workspace with room to spare, in kept planes laid out for it)
-    W.isub = gemm_int_sub(seg, n_seg);
+    // every segment in the integer form: the values in wh, the scales, then the mins, in wl's
+    // memory (N K (1 / sub + 1 / 32) floats: in the workspace with room to spare, in kept planes
+    // laid out for it)
+    W.isub = form.sub, W.imin = form.min;
     W.wd = (float *)W.wl;
+    W.wm = form.sub ? W.wd + (size_t)N * (K / form.sub) : nullptr;
     if (pl && !W.isub && !pl->fexp) throw Error("projection GEMM: weight planes laid out for the integer form");
     GemmActParams X{};
     X.norm_w = norm_w;
@@ -413,9 +417,10 @@ void proj_gemm(const MatvecSeg *seg, int n_seg, int N, int K, const float *x, lo
     X.xh = (_Float16 *)(ws + o_xh);
     X.xl = (_Float16 *)(ws + o_xl);
     X.eexp = (int *)(ws + o_e);
+    X.xs = form.min ? (float *)(ws + o_xs) : nullptr;
     GemmParams G{};
     G.wh = W.wh, G.wl = W.wl, G.fexp = W.fexp, G.xh = X.xh, G.xl = X.xl, G.eexp = X.eexp;
-    G.isub = W.isub, G.wd = W.wd;
+    G.isub = W.isub, G.imin = W.imin, G.wd = W.wd, G.wm = W.wm, G.xs = X.xs;
     G.add = add;
     G.N = N;
     G.K = K;
@@ -515,40 +520,43 @@ void o_proj_impl(const flint_weight *wo, const float *att, int n_tok, float *x, 
 
 }  // namespace
 
-// 0 when a segment is not of the integer form; else the smallest of their scale spans
-static int int_sub_of(const int *types, int n) {
-    int sub = n > 0 ? 32 : 0;
-    for (int i = 0; i < n; i++) sub = std::min(sub, w_int_sub(types[i]));
-    return sub;
+// none when a segment is not of the integer form; else the smallest of their scale spans, and
+// whether any has mins
+static IntForm int_form_of(const int *types, int n) {
+    IntForm f;
+    f.sub = n > 0 ? 32 : 0;
+    for (int i = 0; i < n; i++) f.sub = std::min(f.sub, w_int_sub(types[i])), f.min = f.min || w_int_min(types[i]);
+    if (!f.sub) f.min = false;
+    return f;
 }
 
-int gemm_int_sub(const MatvecSeg *seg, int n_seg) {
+IntForm gemm_int_form(const MatvecSeg *seg, int n_seg) {
     int t[3];
     for (int i = 0; i < n_seg; i++) t[i] = seg[i].type;
-    return int_sub_of(t, n_seg);
+    return int_form_of(t, n_seg);
 }
 
-int qkv_gemm_sub(const flint_weight *wq, const flint_weight *wk, const flint_weight *wv) {
+IntForm qkv_gemm_form(const flint_weight *wq, const flint_weight *wk, const flint_weight *wv) {
     const int t[3] = {wq->type, wk->type, wv->type};
-    return int_sub_of(t, 3);
+    return int_form_of(t, 3);
 }
 
-int o_gemm_sub(const flint_weight *wo) { return int_sub_of(&wo->type, 1); }
+IntForm o_gemm_form(const flint_weight *wo) { return int_form_of(&wo->type, 1); }
 
 static size_t align256(size_t b) { return (b + 255) / 256 * 256; }
 
-size_t planes_bytes(int N, int K, int isub) {
+size_t planes_bytes(int N, int K, IntForm f) {
     const size_t w = align256((size_t)N * K * sizeof(_Float16));
-    if (isub) return w + align256((size_t)N * (K / isub) * sizeof(float));
+    if (f.sub) return w + align256((size_t)N * (K / f.sub + (f.min ? K / 32 : 0)) * sizeof(float));
     return 2 * w + align256((size_t)N * sizeof(int));
 }
 
-WeightPlanes planes_at(void *mem, int N, int K, int isub) {
+WeightPlanes planes_at(void *mem, int N, int K, IntForm f) {
     const size_t w = align256((size_t)N * K * sizeof(_Float16));
     WeightPlanes pl;
     pl.wh = (_Float16 *)mem;
     pl.wl = (_Float16 *)((char *)mem + w);
-    pl.fexp = isub ? nullptr : (int *)((char *)mem + 2 * w);
+    pl.fexp = f.sub ? nullptr : (int *)((char *)mem + 2 * w);
     return pl;
 }
 

@@ -92,10 +92,13 @@ hipError_t launch_prefill(const PrefillParams &P, int dtype, hipStream_t stream)
 
 // Weight formats of the attention projections (ggml type ids, /root/reference/src/gguf.h:14-19)
 constexpr int W_F32 = 0, W_F16 = 1, W_Q8_0 = 8, W_Q5_K = 13, W_Q6_K = 14, W_IQ4_XS = 23, W_BF16 = 30;
-// The batched projections' integer form: q8_0, iq4_xs and q6_K weights are v * s with v an
-// integer of magnitude at most 127 (exact in f16) and s the scale of 32 (q8_0, iq4_xs) or 16
-// (q6_K) consecutive elements; 0: not of that form.
-__host__ __device__ constexpr int w_int_sub(int t) { return t == W_Q8_0 || t == W_IQ4_XS ? 32 : t == W_Q6_K ? 16 : 0; }
+// The batched projections' integer form: q8_0, iq4_xs, q6_K and q5_K weights are v * s (- m for
+// q5_K) with v an integer of magnitude at most 127 (exact in f16), s the scale of 32 (q8_0,
+// iq4_xs, q5_K) or 16 (q6_K) consecutive elements and m the min of 32 (q5_K); 0: not of that form.
+__host__ __device__ constexpr int w_int_sub(int t) {
+    return t == W_Q8_0 || t == W_IQ4_XS || t == W_Q5_K ? 32 : t == W_Q6_K ? 16 : 0;
+}
+__host__ __device__ constexpr bool w_int_min(int t) { return t == W_Q5_K; }
 
 struct MatvecSeg {         // rows [row0, row0 + rows) of one launch come from one tensor
     const uint8_t *w;      // its first row (16-byte aligned)
@@ -134,9 +137,10 @@ struct GemmWeightParams {  // wprep: rows [0, N) of the segments -> wh, wl [N][K
     // isub: every segment in the integer form (w_int_sub), 32 if all scales cover 32 elements,
     // else 16; then wh holds the values and wd the scales, [N / 128 row tiles][K / 32 blocks]
     // [32 / isub][128 rows] floats (in wl's memory), and the GEMM takes the integer form.
-    // 0: the hi/lo planes.
-    int isub;
-    float *wd;
+    // 0: the hi/lo planes. imin: a segment has mins (q5_K); then wm holds them (0 for the other
+    // segments), [N / 128][K / 32][128] floats after wd.
+    int isub, imin;
+    float *wd, *wm;
 };
 struct GemmActParams {     // xprep: rows [0, T_pad) -> xh, xl [T_pad][K], eexp [T_pad]
     const float *x;        // [T] rows of x_stride floats (16-byte aligned)
@@ -146,12 +150,14 @@ struct GemmActParams {     // xprep: rows [0, T_pad) -> xh, xl [T_pad][K], eexp 
     int T, T_pad;          // T_pad: T rounded up to the GEMM tile (rows past T are zeros)
     _Float16 *xh, *xl;
     int *eexp;
+    float *xs;             // or null; else the sums of (xh + xl) over each 32-element block,
+                           // [T_pad / 128][K / 32][128] (the integer form's mins need them)
 };
 struct GemmParams {
     const _Float16 *wh, *wl, *xh, *xl;
     const int *fexp, *eexp;
-    int isub;              // the weights as integer values and scales (GemmWeightParams::isub)
-    const float *wd;
+    int isub, imin;        // the weights as integer values, scales and mins (GemmWeightParams)
+    const float *wd, *wm, *xs;
     float *y;              // [T] rows of y_stride floats (16-byte aligned, stride a multiple of 4)
     long long y_stride;
     int add, N, K, T;
@@ -167,18 +173,22 @@ int matvec_row_multiple(int k);  // n_rows of a matvec launch must be a multiple
 // A projection's weight planes kept by a caller that runs many batches through the same weights
 // (the model's layer-major prefill): one device block of planes_bytes(N, K, isub) holding wh, wl
 // [N][K] and fexp [N], built once with build_*_planes; the *_rows projections given them skip
-// their per-call weight prep (the planes are the same bits that prep would write). isub > 0 (the
-// projection's integer form, gemm_int_sub): wh holds the values and wl's place the scales,
-// N K / isub floats, with no fexp.
+// their per-call weight prep (the planes are the same bits that prep would write). In the
+// integer form (gemm_int_form) wh holds the values and wl's place the scales (N K / sub floats),
+// then the mins (N K / 32 floats, if any), with no fexp.
 struct WeightPlanes {
     _Float16 *wh = nullptr, *wl = nullptr;
     int *fexp = nullptr;
 };
-int gemm_int_sub(const MatvecSeg *seg, int n_seg);  // the GEMM's integer form: 32, 16 or 0
-int qkv_gemm_sub(const flint_weight *wq, const flint_weight *wk, const flint_weight *wv);
-int o_gemm_sub(const flint_weight *wo);
-size_t planes_bytes(int N, int K, int isub);
-WeightPlanes planes_at(void *mem, int N, int K, int isub);
+struct IntForm {  // a projection's integer form: sub 32, 16 or 0 (none); min: a segment has mins
+    int sub = 0;
+    bool min = false;
+};
+IntForm gemm_int_form(const MatvecSeg *seg, int n_seg);
+IntForm qkv_gemm_form(const flint_weight *wq, const flint_weight *wk, const flint_weight *wv);
+IntForm o_gemm_form(const flint_weight *wo);
+size_t planes_bytes(int N, int K, IntForm f);
+WeightPlanes planes_at(void *mem, int N, int K, IntForm f);
 void build_qkv_planes(const flint_weight *wq, const flint_weight *wk, const flint_weight *wv, const WeightPlanes &pl,
                       hipStream_t stream);
 void build_o_planes(const flint_weight *wo, const WeightPlanes &pl, hipStream_t stream);

@@ -190,10 +190,10 @@ struct flint_attn_model {
         if (planes) (void)hipFree(planes);
     }
     static size_t qkv_planes_bytes(const Layer &L) {
-        return planes_bytes(FLINT_QKV_DIM, FLINT_N_EMBD, qkv_gemm_sub(&L.q, &L.k, &L.v));
+        return planes_bytes(FLINT_QKV_DIM, FLINT_N_EMBD, qkv_gemm_form(&L.q, &L.k, &L.v));
     }
     static size_t layer_planes_bytes(const Layer &L) {
-        return qkv_planes_bytes(L) + planes_bytes(FLINT_N_EMBD, FLINT_Q_DIM, o_gemm_sub(&L.o));
+        return qkv_planes_bytes(L) + planes_bytes(FLINT_N_EMBD, FLINT_Q_DIM, o_gemm_form(&L.o));
     }
     // the layer's q|k|v and o planes, built on `stream` if this is the first use; false when
     // there is no memory for them
@@ -214,8 +214,8 @@ struct flint_attn_model {
         }
         const Layer &L = layers[il];
         char *base = (char *)planes + planes_off[il];
-        const WeightPlanes pq = planes_at(base, FLINT_QKV_DIM, FLINT_N_EMBD, qkv_gemm_sub(&L.q, &L.k, &L.v));
-        const WeightPlanes po = planes_at(base + qkv_planes_bytes(L), FLINT_N_EMBD, FLINT_Q_DIM, o_gemm_sub(&L.o));
+        const WeightPlanes pq = planes_at(base, FLINT_QKV_DIM, FLINT_N_EMBD, qkv_gemm_form(&L.q, &L.k, &L.v));
+        const WeightPlanes po = planes_at(base + qkv_planes_bytes(L), FLINT_N_EMBD, FLINT_Q_DIM, o_gemm_form(&L.o));
         if (!planes_built[il]) {
             build_qkv_planes(&L.q, &L.k, &L.v, pq, stream);
             build_o_planes(&L.o, po, stream);

@@ -124,15 +124,17 @@ __global__ __launch_bounds__(512) void wprep_kernel(const GemmWeightParams P) {
 
 
 // ---------------------------------------------------------------------------
-// The integer form. A q8_0, iq4_xs or q6_K weight is s v, with v an integer of magnitude at most
-// 127 (exact in f16) and s the scale of its 32 (q8_0, iq4_xs) or 16 (q6_K) elements, and a 32-k
-// chunk of the GEMM is one 32-element sub-block. So a chunk's products are sum_k (xh + xl) v on
-// the matrix cores, two products per pair instead of gemm3's three and no weight lo plane, and
-// the scale joins in fp32: acc += s T, one s per weight row and chunk (SUB = 32) or k-step of 16
-// (SUB = 16). The x planes are gemm3's.
+// The integer form. A q8_0, iq4_xs, q5_K or q6_K weight is s v (- m for q5_K), with v an integer
+// of magnitude at most 127 (exact in f16), s the scale of its 32 (q8_0, iq4_xs, q5_K) or 16 (q6_K)
+// elements and m the min of its 32, and a 32-k chunk of the GEMM is one 32-element sub-block. So
+// a chunk's products are sum_k (xh + xl) v on the matrix cores, two products per pair instead of
+// gemm3's three and no weight lo plane, and the scale joins in fp32: acc += s T, one s per weight
+// row and chunk (SUB = 32) or k-step of 16 (SUB = 16); the min as acc -= m S with S = sum_k
+// (xh + xl) over the block, which xprep writes per row and block. The x planes are gemm3's.
 //
 // wprep_int: thread (row n, sub-block b) writes the sub-block's 32 values as f16 into the plane's
-// chunk order (plane_unit) and its scales into wd[n / 128][b][32 / SUB][n % 128].
+// chunk order (plane_unit), its scales into wd[n / 128][b][32 / SUB][n % 128] and, with mins, its
+// min into wm[n / 128][b][n % 128].
 template <int K, int SUB>
 __global__ __launch_bounds__(256) void wprep_int_kernel(const GemmWeightParams P) {
     constexpr int NB = K / 32, NS = 32 / SUB;
@@ -140,8 +142,8 @@ __global__ __launch_bounds__(256) void wprep_int_kernel(const GemmWeightParams P
     const int in2 = P.n_seg > 2 && n >= P.seg[2].row0, in1 = !in2 && P.n_seg > 1 && n >= P.seg[1].row0;
     const MatvecSeg S = in2 ? P.seg[2] : in1 ? P.seg[1] : P.seg[0];
     _Float16 v[32];
-    float sc[2];
-    deq32_int(S.type, S.w + (size_t)(n - S.row0) * S.row_bytes, b, v, sc);
+    float sc[2], mn;
+    deq32_int(S.type, S.w + (size_t)(n - S.row0) * S.row_bytes, b, v, sc, mn);
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         f16x8 u;
@@ -152,6 +154,7 @@ __global__ __launch_bounds__(256) void wprep_int_kernel(const GemmWeightParams P
     float *const d = P.wd + (((size_t)(n >> 7) * NB + b) * NS) * GEMM_TILE + (n & 127);
     d[0] = sc[0];  // SUB = 32: the two halves' scales are one
     if constexpr (NS == 2) d[GEMM_TILE] = sc[1];
+    if (P.imin) P.wm[((size_t)(n >> 7) * NB + b) * GEMM_TILE + (n & 127)] = mn;
 }
 
 // ---------------------------------------------------------------------------
@@ -228,6 +231,15 @@ __global__ __launch_bounds__(512) void xprep_kernel(const GemmActParams P) {
         const size_t o = plane_unit(t, gl + 8 * (wave + 8 * j), K);
         *(f16x8 *)(P.xh + o) = h8;
         *(f16x8 *)(P.xl + o) = l8;
+        if (P.xs) {  // the block sums: a 32-element block's 4 groups are lanes gl ^ 1, ^ 2, ^ 3
+            float gs = 0.f;
+#pragma unroll
+            for (int i = 0; i < 8; i++) gs += (float)h8[i] + (float)l8[i];
+            gs += __shfl_xor(gs, 8, 64);
+            gs += __shfl_xor(gs, 16, 64);
+            const int b = (gl + 8 * (wave + 8 * j)) >> 2;
+            if ((gl & 3) == 0) P.xs[((size_t)(t >> 7) * (K / 32) + b) * GEMM_TILE + (t & 127)] = gs;
+        }
     }
     if (tid < 8) P.eexp[t] = e;  // lanes 0..7 of wave 0: rows rho = tid
 }
@@ -402,7 +414,7 @@ template <int SUB>
 constexpr int gq_scales() { return (32 / SUB) * GM_TILE; }  // a chunk's scales, per row tile
 template <int SUB>
 constexpr int gq_stage() { return 3 * GM_PLANE_CHUNK + gq_scales<SUB>() * 4; }  // x hi, x lo, values, scales
-constexpr int GQ_LOADS = 7;                                                       // direct loads per wave per chunk
+// with mins, the block sums of the chunk's 128 tokens and the mins of its 128 rows follow
 
 typedef __attribute__((address_space(3))) void lds_void;
 
@@ -412,10 +424,11 @@ __device__ inline void wait_vmcnt() {  // s_waitcnt vmcnt(N), other counters unt
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-template <int SUB>
+template <int SUB, bool MIN>
 __global__ __launch_bounds__(GM_THREADS, 2) void gemm_int_kernel(const GemmParams P) {
     constexpr int SCB = gq_scales<SUB>(), SCL = SCB / 16;  // scales per chunk; lanes that load them
-    __shared__ __align__(16) uint8_t lds[3][gq_stage<SUB>()];
+    constexpr int STAGE = gq_stage<SUB>(), LOADS = MIN ? 9 : 7;  // direct loads per wave per chunk
+    __shared__ __align__(16) uint8_t lds[3][STAGE + (MIN ? 2 * GM_TILE * 4 : 0)];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wn = wave & 1, wt = wave >> 1;
@@ -435,6 +448,9 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemm_int_kernel(const GemmParam
     const _Float16 *src[3] = {P.xh + (size_t)t0 * K + 8 * tid, P.xl + (size_t)t0 * K + 8 * tid,
                               P.wh + (size_t)n0 * K + 8 * tid};
     const float *srcd = P.wd + (size_t)nt * (K / GM_KC) * SCB + SCB / 4 * wave + 4 * (lane & (SCL - 1));
+    const size_t mo = 32 * wave + 4 * (lane & 7);  // this lane's 16 bytes of the block sums and mins
+    const float *srcs = MIN ? P.xs + (size_t)tt * (K / GM_KC) * GM_TILE + mo : nullptr;
+    const float *srcm = MIN ? P.wm + (size_t)nt * (K / GM_KC) * GM_TILE + mo : nullptr;
     const int n_chunks = K / GM_KC;
     auto issue = [&](int c, int st) {  // chunk c into stage st
         uint8_t *const base = lds[st];
@@ -448,6 +464,13 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemm_int_kernel(const GemmParam
         if (lane < SCL)
             __builtin_amdgcn_global_load_lds(srcd + (size_t)c * SCB,
                                              (lds_void *)(base + 3 * GM_PLANE_CHUNK + SCB * wave), 16, 0, 0);
+        if constexpr (MIN) {
+            if (lane < 8) {
+                __builtin_amdgcn_global_load_lds(srcs + (size_t)c * GM_TILE, (lds_void *)(base + STAGE + 128 * wave), 16, 0, 0);
+                __builtin_amdgcn_global_load_lds(srcm + (size_t)c * GM_TILE,
+                                                 (lds_void *)(base + STAGE + 4 * GM_TILE + 128 * wave), 16, 0, 0);
+            }
+        }
     };
     f32x16 acc[2][2];  // [token block][weight block]
 #pragma unroll
@@ -494,6 +517,21 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemm_int_kernel(const GemmParam
                         for (int e = 0; e < 16; e++) acc[a][b][e] = fmaf(dp[b], Tp[a][b][e], acc[a][b][e]);
             }
         }
+        if (MIN && s0 == 0) {  // the chunk's mins: acc -= m S, S of element e's token
+            const float *const sl = (const float *)(base + STAGE), *const ml = sl + GM_TILE;
+#pragma unroll
+            for (int a = 0; a < 2; a++)
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const f32x4 S4 = *(const f32x4 *)(sl + 64 * wt + 32 * a + 8 * q + 4 * (lane >> 5));
+#pragma unroll
+                    for (int b = 0; b < 2; b++) {
+                        const float m = ml[64 * wn + 32 * b + (lane & 31)];
+#pragma unroll
+                        for (int i = 0; i < 4; i++) acc[a][b][4 * q + i] = fmaf(-m, S4[i], acc[a][b][4 * q + i]);
+                    }
+                }
+        }
         const float *const sc = (const float *)(base + 3 * GM_PLANE_CHUNK) + (SUB == 16 ? GM_TILE * s0 : 0);
 #pragma unroll
         for (int b = 0; b < 2; b++) dn[b] = sc[64 * wn + 32 * b + (lane & 31)];
@@ -506,7 +544,7 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemm_int_kernel(const GemmParam
     // in flight (vmcnt(0)); the empty asm keeps the compiler from moving LDS reads across the
     // barrier, and the chunk before's reads have all returned (their registers fed its MFMAs).
     auto sync = [&](int c) {
-        wait_vmcnt<GQ_LOADS>();
+        wait_vmcnt<LOADS>();
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
         const int st = c % 3;
@@ -584,7 +622,8 @@ hipError_t launch_proj_gemm(const GemmWeightParams &W, const GemmActParams &X, c
                 hipLaunchKernelGGL(xprep_kernel<2048>, dim3(X.T_pad / 8), dim3(512), 0, stream, X);
             else
                 hipLaunchKernelGGL(xprep_kernel<4096>, dim3(X.T_pad / 8), dim3(512), 0, stream, X);
-            void (*gk)(GemmParams) = s32 ? gemm_int_kernel<32> : gemm_int_kernel<16>;
+            void (*gk)(GemmParams) = G.imin ? (s32 ? gemm_int_kernel<32, true> : gemm_int_kernel<16, true>)
+                                            : (s32 ? gemm_int_kernel<32, false> : gemm_int_kernel<16, false>);
             hipLaunchKernelGGL(gk, dim3(G.N / GM_TILE * (X.T_pad / GM_TILE)), dim3(GM_THREADS), 0, stream, G);
         }
         return hipGetLastError();
