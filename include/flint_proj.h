@@ -93,9 +93,9 @@ int32_t flint_attn_o_proj(const flint_weight *wo, const float *att, float *x, vo
  * the matrix cores: weight and activation rows split into f16 hi/lo pairs (22 bits, each row
  * scaled by a power of two), products summed in fp32 (q8_0, iq4_xs, q5_K and q6_K weights keep
  * their integer values, exact in f16, and take their block scales and mins in fp32); every
- * output is within fp32 reassociation
- * of the single-token result (both within the oracle's bound). It uses a device workspace of
- * 4 (rows + 128-token-padded n_tok) x K bytes, allocated on first use and reused.
+ * output is within fp32 reassociation of the single-token result (both within the oracle's
+ * bound). It uses a device workspace of 4 (rows + 128-token-padded n_tok) x K bytes (and
+ * n_tok K / 8 more with q5_K weights), allocated on first use and reused.
  * Replace the prefill's k_rmsnorm_rows + three mm (q, k, v), and mm(o) + k_add_rows, at
  * /root/reference/src/engine.mm:1083-1086 and 1105-1111.
  */
