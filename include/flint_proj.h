@@ -94,8 +94,9 @@ int32_t flint_attn_o_proj(const flint_weight *wo, const float *att, float *x, vo
  * scaled by a power of two), products summed in fp32 (q8_0, iq4_xs, q5_K and q6_K weights keep
  * their integer values, exact in f16, and take their block scales and mins in fp32); every
  * output is within fp32 reassociation of the single-token result (both within the oracle's
- * bound). It uses a device workspace of 4 (rows + 128-token-padded n_tok) x K bytes (and
- * n_tok K / 8 more with q5_K weights), allocated on first use and reused.
+ * bound). Batches run in passes of at most 8192 tokens, so the device workspace has a ceiling:
+ * 4 (rows + p) x K bytes, p = the pass's tokens padded to 128 (and p K / 8 more with q5_K
+ * weights), allocated on first use and reused.
  * Replace the prefill's k_rmsnorm_rows + three mm (q, k, v), and mm(o) + k_add_rows, at
  * /root/reference/src/engine.mm:1083-1086 and 1105-1111.
  */
