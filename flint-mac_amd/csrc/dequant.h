@@ -216,6 +216,12 @@ __device__ inline void deq32_int(int type, const uint8_t *row, int sb, _Float16 
             for (int i = 0; i < 32; i++) v[i] = (_Float16)(((byte_of(ql, i) >> ls) & 15) + (((byte_of(qh, i) >> j) & 1) << 4));
             break;
         }
+        case W_F16: {  // y = the half itself
+            s[0] = s[1] = 1.f;
+#pragma unroll
+            for (int k = 0; k < 4; k++) *(u32x4 *)&v[8 * k] = ((const u32x4 *)(row + 64 * sb))[k];
+            break;
+        }
         default:
             s[0] = s[1] = 0.f;
 #pragma unroll
