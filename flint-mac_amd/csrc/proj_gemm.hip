@@ -404,7 +404,8 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemm3_kernel(const GemmParams P
 // into LDS (global_load_lds_dwordx4: each wave-wide load writes 1 KiB, lane l's 16 bytes at
 // l * 16 from the wave's LDS address), three stages deep: while chunk c is computed, chunks c + 1
 // and c + 2 are in flight, and no register holds them. A chunk's 128 (SUB = 32) or 256 scales
-// ride along (lanes 0-7 or 0-15 of each wave load 128 or 256 bytes).
+// ride along (lanes 0-7 or 0-15 of each wave load 128 or 256 bytes), and with mins (MIN) the
+// chunk's block sums of its 128 tokens and mins of its 128 rows (lanes 0-7 again, two loads).
 // Each step makes the products T = sum (xh + xl) v of one chunk (SUB = 32: four independent
 // chains of four MFMAs) or k-step (SUB = 16: chains of two), and scales the step before's
 // (acc += s T) in between, so that those FMAs run beside MFMAs that do not feed them (two
@@ -414,7 +415,6 @@ template <int SUB>
 constexpr int gq_scales() { return (32 / SUB) * GM_TILE; }  // a chunk's scales, per row tile
 template <int SUB>
 constexpr int gq_stage() { return 3 * GM_PLANE_CHUNK + gq_scales<SUB>() * 4; }  // x hi, x lo, values, scales
-// with mins, the block sums of the chunk's 128 tokens and the mins of its 128 rows follow
 
 typedef __attribute__((address_space(3))) void lds_void;
 
@@ -536,9 +536,9 @@ __global__ __launch_bounds__(GM_THREADS, 2) void gemm_int_kernel(const GemmParam
 #pragma unroll
         for (int b = 0; b < 2; b++) dn[b] = sc[64 * wn + 32 * b + (lane & 31)];
     };
-    // Chunk c lives in stage c % 3. Every wave issues the same GQ_LOADS loads per chunk (past the
+    // Chunk c lives in stage c % 3. Every wave issues the same LOADS loads per chunk (past the
     // last chunk it re-reads the last one into a stage no one reads again), so "chunk c has
-    // landed" is vmcnt(GQ_LOADS) with chunk c + 1 still in flight; the barrier then makes every
+    // landed" is vmcnt(LOADS) with chunk c + 1 still in flight; the barrier then makes every
     // wave's part of it visible, and it also ends every wave's reads of stage (c - 1) % 3, which
     // chunk c + 2 overwrites after it. No fence: a workgroup-scope fence would wait for every load
     // in flight (vmcnt(0)); the empty asm keeps the compiler from moving LDS reads across the
