@@ -108,11 +108,25 @@ __global__ __launch_bounds__(256) void prefix_kernel(const PrefillParams P) {
     const int row0 = 32 * (P.n_direct + (int)blockIdx.x), pos0 = P.kbase + row0;  // the tile's first position
     const int crow = row0 - 32 * P.n_direct;  // its row in the copy, which starts at tile n_direct
     if (pos0 + 32 > P.p0) {  // the tile holding p0: raw values of positions [pos0, p0)
+        // every load before the first store: a load after a store that may alias it (both
+        // 16-bit) waits for the store, one round trip per element
+        constexpr int PER = 32 * HEAD_DIM / 256;  // elements per thread, at most
         uint16_t *raw = (uint16_t *)P.sk;
-        for (int i = tid; i < (P.p0 - pos0) * HEAD_DIM; i += 256) {
-            const int r = i >> 7, d = i & 127, slot = (pos0 + r) & P.cache_mask;
-            raw[pk_index(kvh, crow + r, d, P.k_rows)] = P.cache_k[kt_index(kvh, slot, d, P.n_slots)];
-            raw[pv_index(kvh, crow + r, d, P.k_rows)] = P.cache_v[vt_index(kvh, slot, d, P.n_slots)];
+        const int n = (P.p0 - pos0) * HEAD_DIM;
+        uint16_t kx[PER], vx[PER];
+#pragma unroll
+        for (int j = 0; j < PER; j++) {
+            const int i = min(tid + 256 * j, n - 1), r = i >> 7, d = i & 127, slot = (pos0 + r) & P.cache_mask;
+            kx[j] = P.cache_k[kt_index(kvh, slot, d, P.n_slots)];
+            vx[j] = P.cache_v[vt_index(kvh, slot, d, P.n_slots)];
+        }
+#pragma unroll
+        for (int j = 0; j < PER; j++) {
+            const int i = tid + 256 * j, r = i >> 7, d = i & 127;
+            if (i < n) {
+                raw[pk_index(kvh, crow + r, d, P.k_rows)] = kx[j];
+                raw[pv_index(kvh, crow + r, d, P.k_rows)] = vx[j];
+            }
         }
         return;
     }
@@ -247,14 +261,20 @@ __global__ __launch_bounds__(KP_THREADS) void kv_prep_kernel(const PrefillParams
         // [pos0, p0) come from the copy, where prefix_kernel left the cache's raw values
         // (kbase <= pos0, 32-aligned)
         const uint16_t *raw = (const uint16_t *)P.sk;
+        // all rows' loads first (rows from lo on re-read the first row), so they share one round trip
+        uint16_t rk[KP_ROWS][2], rv[KP_ROWS][2];
 #pragma unroll
         for (int i = 0; i < KP_ROWS; i++) {
-            const int r = r0 + i, row = pos0 + r - P.kbase - 32 * P.n_direct;  // the copy starts at tile n_direct
+            const int r = pos0 + r0 + i < lo ? r0 + i : r0;
+            const int row = pos0 + r - P.kbase - 32 * P.n_direct;  // the copy starts at tile n_direct
+            rk[i][0] = raw[pk_index(kvh, row, lane, P.k_rows)], rk[i][1] = raw[pk_index(kvh, row, lane + 64, P.k_rows)];
+            rv[i][0] = raw[pv_index(kvh, row, lane, P.k_rows)], rv[i][1] = raw[pv_index(kvh, row, lane + 64, P.k_rows)];
+        }
+#pragma unroll
+        for (int i = 0; i < KP_ROWS; i++) {
+            const int r = r0 + i;
             if (pos0 + r < lo) {
-                const uint16_t k0 = raw[pk_index(kvh, row, lane, P.k_rows)];
-                const uint16_t k1 = raw[pk_index(kvh, row, lane + 64, P.k_rows)];
-                const uint16_t v0 = raw[pv_index(kvh, row, lane, P.k_rows)];
-                const uint16_t v1 = raw[pv_index(kvh, row, lane + 64, P.k_rows)];
+                const uint16_t k0 = rk[i][0], k1 = rk[i][1], v0 = rv[i][0], v1 = rv[i][1];
                 kl[r][lane] = k0, kl[r][lane + 64] = k1, vt[lane][r] = v0, vt[lane + 64][r] = v1;
                 if constexpr (DT == DT_BF16) {
                     mk = fmaxf(mk, fmaxf(fabsf(KT::to_float(k0)), fabsf(KT::to_float(k1))));
