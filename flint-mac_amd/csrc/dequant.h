@@ -222,6 +222,25 @@ __device__ inline void deq32_int(int type, const uint8_t *row, int sb, _Float16 
             for (int k = 0; k < 4; k++) *(u32x4 *)&v[8 * k] = ((const u32x4 *)(row + 64 * sb))[k];
             break;
         }
+        case W_BF16: {  // y = the bf16 value: 8 significant bits, exact in f16 once the block's
+                        // largest magnitude is scaled into [2^14, 2^15) (values below 2^-10 of
+                        // it, beneath f16's normal range, round to f16's subnormal steps)
+            uint32_t h[16];
+#pragma unroll
+            for (int k = 0; k < 4; k++) *(u32x4 *)&h[4 * k] = ((const u32x4 *)(row + 64 * sb))[k];
+            float w[32], mx = 0.f;
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                w[2 * i] = __uint_as_float(h[i] << 16);
+                w[2 * i + 1] = __uint_as_float(h[i] & 0xffff0000u);
+                mx = fmaxf(mx, fmaxf(fabsf(w[2 * i]), fabsf(w[2 * i + 1])));
+            }
+            const int e = mx > 0.f && __builtin_isfinite(mx) ? __builtin_amdgcn_frexp_expf(mx) - 15 : 0;
+            s[0] = s[1] = __builtin_amdgcn_ldexpf(1.f, e);
+#pragma unroll
+            for (int i = 0; i < 32; i++) v[i] = (_Float16)__builtin_amdgcn_ldexpf(w[i], -e);
+            break;
+        }
         default:
             s[0] = s[1] = 0.f;
 #pragma unroll

@@ -95,9 +95,10 @@ constexpr int W_F32 = 0, W_F16 = 1, W_Q8_0 = 8, W_Q5_K = 13, W_Q6_K = 14, W_IQ4_
 // The batched projections' integer form: q8_0, iq4_xs, q6_K and q5_K weights are v * s (- m for
 // q5_K) with v an integer of magnitude at most 127 (exact in f16), s the scale of 32 (q8_0,
 // iq4_xs, q5_K) or 16 (q6_K) consecutive elements and m the min of 32 (q5_K); f16 weights are
-// v * 1 with v the weight itself; 0: not of that form.
+// v * 1 with v the weight itself, bf16 weights v * 2^e with e putting their block of 32 in f16's
+// range; 0: not of that form.
 __host__ __device__ constexpr int w_int_sub(int t) {
-    return t == W_Q8_0 || t == W_IQ4_XS || t == W_Q5_K || t == W_F16 ? 32 : t == W_Q6_K ? 16 : 0;
+    return t == W_Q8_0 || t == W_IQ4_XS || t == W_Q5_K || t == W_F16 || t == W_BF16 ? 32 : t == W_Q6_K ? 16 : 0;
 }
 __host__ __device__ constexpr bool w_int_min(int t) { return t == W_Q5_K; }
 

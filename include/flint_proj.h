@@ -93,7 +93,7 @@ int32_t flint_attn_o_proj(const flint_weight *wo, const float *att, float *x, vo
  * the matrix cores: weight and activation rows split into f16 hi/lo pairs (22 bits, each row
  * scaled by a power of two), products summed in fp32 (q8_0, iq4_xs, q5_K and q6_K weights keep
  * their integer values, exact in f16, and take their block scales and mins in fp32; f16
- * weights are used as they are); every
+ * weights are used as they are, bf16 ones scaled by a power of two per block of 32); every
  * output is within fp32 reassociation of the single-token result (both within the oracle's
  * bound). Batches run in passes of at most 8192 tokens, so the device workspace has a ceiling:
  * 4 (rows + p) x K bytes, p = the pass's tokens padded to 128 (and p K / 8 more with q5_K

@@ -238,10 +238,10 @@ def _gemm_case(cuda, rng, types, wo_type, T, x_scale=None, att_scale=None):
 
 @pytest.mark.parametrize("types,wo_type", [(("q8_0",) * 3, "q8_0"), (("q5_K", "q6_K", "iq4_xs"), "q6_K"),
                                            (("bf16", "f16", "f32"), "iq4_xs"), (("q6_K",) * 3, "q5_K"),
-                                           (("iq4_xs",) * 3, "bf16"), (("f16",) * 3, "f16")])
+                                           (("iq4_xs",) * 3, "bf16"), (("f16",) * 3, "f16"), (("bf16",) * 3, "q5_K")])
 def test_projection_rows_gemm_matches_oracle(cuda, types, wo_type):
     """Batches from 16 tokens (the GEMM on f16 hi/lo planes, or on the weights' integer values
-    and block scales for q8_0 / iq4_xs / q5_K / q6_K / f16): every output within the fp32
+    and block scales for q8_0 / iq4_xs / q5_K / q6_K / f16 / bf16): every output within the fp32
     reassociation bound of the oracle's double-accumulated matvec, at 131 tokens (a partial
     128-token tile) in the engine's formats, the residual added in the o projection."""
     _gemm_case(cuda, np.random.default_rng(51 + len(wo_type)), types, wo_type, 131)
