@@ -81,6 +81,44 @@ def test_prefill_4000_config4(cuda, store, is_swa):
         assert k_close(kc[:, s, :], K[p].reshape(N_HEAD_KV, HEAD_DIM), store), f"K slot {s} pos {p}"
 
 
+@pytest.mark.parametrize("n,p0,store,big_v", [(2701, 0, "f16", False), (3000, 517, "bf16", False), (2200, 0, "bf16", True)],
+                         ids=["T2701_f16", "p0_517_T2483_bf16", "T2200_bf16_scaled"])
+def test_prefill_swa_two_rounds(cuda, n, p0, store, big_v):
+    """SWA prefills of more than 64 query blocks (two rounds of workgroups, each kv head's blocks
+    dealt to two XCDs in halves, half of the first round started late): odd block counts, a
+    last block of 13 rows, a call after a cached prefix at an unaligned position, and the
+    scaled path (V rows at 1e5, past f16). Every row against the oracle; the ring bit-exact
+    for V."""
+    _say(f"SWA two rounds: n={n} p0={p0} store={store} big_v={big_v}")
+    rng = np.random.default_rng(5)
+    qn, kn, sk = layer_weights(rng)
+    qkv = rng.standard_normal((n, QKV_DIM)).astype(np.float32)
+    if big_v:
+        qkv[3::7, 4608:] *= 1e5
+    kv = fa.KVLayer(is_swa=True, has_rope=True, n_slots=1024, kv_dtype=store, rope_theta=1e4, q_norm=qn, k_norm=kn,
+                    sinks=sk)
+    L = oracle_layer(kv, qn, kn, sk, store)
+    dq = torch.from_numpy(qkv).to(cuda)
+    att = torch.zeros((n, Q_DIM), device=cuda)
+    if p0:
+        kv.prefill(dq[:p0], att[:p0], 0)
+    kv.prefill(dq[p0:], att[p0:], p0)
+    torch.cuda.synchronize()
+    got = att.cpu().numpy().astype(np.float64)
+    assert np.all(np.isfinite(got))
+    K = np.zeros((n, KV_DIM), np.float32)
+    V = np.zeros((n, KV_DIM), np.float32)
+    want = fo.prefill(L, qkv, 0, K, V, n_threads=16).astype(np.float64)
+    scale = np.maximum(1.0, np.abs(want).max(axis=1, keepdims=True)) if big_v else 1.0
+    for r0 in range(0, n, 500):
+        r1 = min(n, r0 + 500)
+        sc = scale[r0:r1] if big_v else 1.0
+        assert_close(got[r0:r1] / sc, want[r0:r1] / sc, f"rows {r0}..{r1 - 1}")
+    vc = kv.v_slots()[0].float().cpu().numpy()
+    for p in range(n - 1024, n):
+        assert np.array_equal(vc[:, kv.slot(p), :], V[p].reshape(N_HEAD_KV, HEAD_DIM)), f"V slot of pos {p}"
+
+
 @pytest.mark.parametrize("il,is_swa", [(0, False), (2, True)], ids=["layer0_full_nope", "layer2_swa_rope"])
 def test_debug_attn_reference_test_attn_probes(cuda, il, is_swa):
     """The reference's `flint test-attn` (/root/reference/src/main.mm:241-314): 1300 tokens in
