@@ -119,6 +119,34 @@ def test_prefill_swa_two_rounds(cuda, n, p0, store, big_v):
         assert np.array_equal(vc[:, kv.slot(p), :], V[p].reshape(N_HEAD_KV, HEAD_DIM)), f"V slot of pos {p}"
 
 
+@pytest.mark.parametrize("n,is_swa,store", [(16384, False, "f16"), (12000, True, "bf16")], ids=["full_16384_f16", "swa_12000_bf16"])
+def test_prefill_long_prompt_probes(cuda, n, is_swa, store):
+    """One call over a long prompt (512 and 375 query blocks: several rounds of workgroups, the
+    longest-first deal of a causal layer over 2048 workgroups): probe rows at block edges, round
+    boundaries and random positions against the oracle, and the cache's V rows of sampled
+    positions bit-exact."""
+    _say(f"long prompt probes n={n} swa={is_swa} store={store}")
+    rng = np.random.default_rng(17)
+    qn, kn, sk = layer_weights(rng)
+    qkv = rng.standard_normal((n, QKV_DIM)).astype(np.float32)
+    kv = fa.KVLayer(is_swa=is_swa, has_rope=True, n_slots=1024 if is_swa else n, kv_dtype=store, rope_theta=1e6,
+                    q_norm=qn, k_norm=kn, sinks=sk)
+    L = oracle_layer(kv, qn, kn, sk, store)
+    att = torch.zeros((n, Q_DIM), device=cuda)
+    kv.prefill(torch.from_numpy(qkv).to(cuda), att, 0)
+    torch.cuda.synchronize()
+    got = att.cpu().numpy()
+    assert np.all(np.isfinite(got))
+    K, V = _oracle_history(L, qkv)
+    probes = _probes(n, extra=[4095, 4096, 8191, 8192, 8224, 12287, 12288, n // 2, n - 33, n - 32, n - 31])
+    want = _oracle_at(L, qkv, K, V, probes)
+    for p in probes:
+        assert_close(got[p], want[p], f"pos {p}")
+    vc = kv.v_slots()[0].float().cpu().numpy()
+    for p in (range(n - 1024, n, 7) if is_swa else range(0, n, 97)):
+        assert np.array_equal(vc[:, kv.slot(p), :], V[p].reshape(N_HEAD_KV, HEAD_DIM)), f"V slot of pos {p}"
+
+
 @pytest.mark.parametrize("il,is_swa", [(0, False), (2, True)], ids=["layer0_full_nope", "layer2_swa_rope"])
 def test_debug_attn_reference_test_attn_probes(cuda, il, is_swa):
     """The reference's `flint test-attn` (/root/reference/src/main.mm:241-314): 1300 tokens in
