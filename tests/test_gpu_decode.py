@@ -117,6 +117,32 @@ def test_decode_split_k_32k_config3(cuda, store):
     assert np.array_equal(vc, fo.round_store(qkv[4608:], store).reshape(N_HEAD_KV, HEAD_DIM))
 
 
+@pytest.mark.parametrize("store", ["f16", "bf16"])
+def test_decode_very_long_context(cuda, store):
+    """One sequence at 196611 cached positions (a ragged last tile; splits of ~130 tiles from the
+    auto plan), and the same call with 9 and 65 splits, against the oracle; the current token's
+    K/V land in slot pos."""
+    n = 196611
+    _say(f"decode very long context n={n} store={store}")
+    rng = np.random.default_rng(23)
+    qn, kn, sk = layer_weights(rng)
+    kv = fa.KVLayer(is_swa=False, has_rope=True, n_slots=n + 29, kv_dtype=store, rope_theta=1e6, q_norm=qn, k_norm=kn,
+                    sinks=sk)
+    L = oracle_layer(kv, qn, kn, sk, store)
+    K, V = _history(rng, n + 1, store)
+    _fill_cache(kv, K[:n], V[:n], np.arange(n))
+    qkv = rng.standard_normal(QKV_DIM).astype(np.float32)
+    dq = torch.from_numpy(qkv).to(cuda)
+    want = fo.decode_step(L, qkv, n, K, V, n_threads=8)
+    for kps in (0, 24576, 3072):  # auto, 9, 65 splits
+        att = torch.zeros(Q_DIM, device=cuda)
+        kv.decode(dq, att, n, keys_per_split=kps)
+        torch.cuda.synchronize()
+        assert_close(att.cpu().numpy(), want, f"keys_per_split={kps}")
+    vc = kv.v_slots()[0, :, n, :].float().cpu().numpy()
+    assert np.array_equal(vc, fo.round_store(qkv[4608:], store).reshape(N_HEAD_KV, HEAD_DIM))
+
+
 def test_decode_edge_positions_and_sinks(cuda):
     """pos 0 (current token only), 1, 31/32/33 around a tile edge, extreme sinks."""
     _say("decode edge positions and sinks")
