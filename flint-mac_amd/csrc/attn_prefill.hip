@@ -685,12 +685,29 @@ __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const Pref
     //      A pair reads tiles t + 1 .. t + 3 (stored before the previous barrier) and
     //      writes tiles t + 4, t + 5 into the two ring slots whose tiles were last read in
     //      the previous pair, so five slots never conflict. ----
+    // Without DIRECT, the loop's tiles go straight from memory into their ring slots
+    // (global_load_lds_dwordx4: wave w's load i writes units 512 i + 64 w + lane, lane l's 16 bytes
+    // at the LDS address in m0 plus 16 l), so no register holds them and no LDS store moves them.
+    // Inline asm: for an LDS load it tracks, the compiler makes every later barrier wait for all
+    // loads; these are waited for explicitly before the barrier that publishes their slots.
+    constexpr bool DMA = !DIRECT;
+    const uint32_t dma_voff = 16 * tid;  // the lane's bytes from a tile's start (unit tid)
+    const uint32_t dma_lds = (uint32_t)(uintptr_t)(lds_void *)&ring[0][0][0] + 1024 * __builtin_amdgcn_readfirstlane(wave);
+    auto dma_tile = [&](int t, int sl) {  // tile t into ring slot sl (wave-uniform)
+        const _Float16 *const src = skv + (size_t)t * (PF_TILE_UNITS * 8);
+#pragma unroll
+        for (int i = 0; i < PF_UNITS_PER_THREAD; i++)
+            asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(
+                             dma_lds + (uint32_t)(sl * PF_TILE_UNITS * 16 + PF_THREADS * 16 * i)),
+                         "v"(dma_voff), "s"(src + PF_THREADS * 8 * i)
+                         : "m0");
+    };
     pf_lstore(R0, ring[0], tid);
     if (t_lo + 1 <= t_hi) pf_lstore(R1, ring[1], tid);
     if (t_lo + 2 <= t_hi) pf_lstore(R2, ring[2], tid);
     if (t_lo + 3 <= t_hi) pf_lstore(R3, ring[3], tid);
     PfTile R;
-    if (t_lo + 4 <= t_hi) gload(R, t_lo + 4);
+    if (!DMA && t_lo + 4 <= t_hi) gload(R, t_lo + 4);
     __syncthreads();
 
     f16x8 kf[8], vf[8];
@@ -723,11 +740,15 @@ __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const Pref
             l += e0 + e1;
             asm volatile("" : "+v"(l));  // keeps the row sum in this slot
             sn = mfma32_f16(kf[g], qf[g], g == 0 ? negm : sn);
-            if (g < PF_UNITS_PER_THREAD && st4) {
+            if (!DMA && g < PF_UNITS_PER_THREAD && st4) {
                 const int u = tid + PF_THREADS * g;
                 ring[sl4][u >> 6][u & 63] = __builtin_bit_cast(f16x8, R.u[g]);
             }
-            if (g == PF_UNITS_PER_THREAD && ld5) gload(R, t + 5);
+            if (!DMA && g == PF_UNITS_PER_THREAD && ld5) gload(R, t + 5);
+            // DMA, first step of a pair: tiles t + 4 and t + 5 into the slots of tiles t - 1 and t,
+            // which no wave reads after the barrier before this pair
+            if (DMA && g == 0 && !bar && st4) dma_tile(t + 4, sl4);
+            if (DMA && g == 1 && !bar && ld5) dma_tile(t + 5, sl0);
             __builtin_amdgcn_sched_barrier(0);
         }
         const f16x8 pf[2] = {__builtin_bit_cast(f16x8, u32x4{pw[0], pw[1], pw[2], pw[3]}),
@@ -748,7 +769,10 @@ __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const Pref
         // interleave.
         if (edge(kp1)) pf_mask(sn, kp1, hh, key_lo, key_hi);
         if (over) pf_rescale(sn, m, l, negm, acc);
-        if (bar) __syncthreads();
+        if (bar) {
+            if (DMA) wait_vmcnt<0>();  // this wave's part of the pair's two tiles is in its slots
+            __syncthreads();
+        }
         sl0 = sl1;
     };
     // two steps per iteration, so the score buffers alternate without copies

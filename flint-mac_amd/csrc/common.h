@@ -97,6 +97,15 @@ __device__ inline void pin_sgpr(T x) {
     asm volatile("" ::"s"(x));
 }
 
+// LDS pointer type of the global_load_lds builtin (loads straight from memory into LDS)
+typedef __attribute__((address_space(3))) void lds_void;
+
+template <int N>
+__device__ inline void wait_vmcnt() {  // s_waitcnt vmcnt(N), other counters untouched
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
 __device__ inline void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
     __builtin_amdgcn_s_barrier();

@@ -416,14 +416,6 @@ constexpr int gq_scales() { return (32 / SUB) * GM_TILE; }  // a chunk's scales,
 template <int SUB>
 constexpr int gq_stage() { return 3 * GM_PLANE_CHUNK + gq_scales<SUB>() * 4; }  // x hi, x lo, values, scales
 
-typedef __attribute__((address_space(3))) void lds_void;
-
-template <int N>
-__device__ inline void wait_vmcnt() {  // s_waitcnt vmcnt(N), other counters untouched
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
 template <int SUB, bool MIN>
 __global__ __launch_bounds__(GM_THREADS, 2) void gemm_int_kernel(const GemmParams P) {
     constexpr int SCB = gq_scales<SUB>(), SCL = SCB / 16;  // scales per chunk; lanes that load them
