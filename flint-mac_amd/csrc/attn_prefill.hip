@@ -547,11 +547,35 @@ __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const Pref
 #pragma unroll
         for (int k = 0; k < 4; k++) x[g][k] = *(const float4 *)(qp + 32 * k);
     }
+    // Without DIRECT, the tiles go straight from memory into their ring slots
+    // (global_load_lds_dwordx4: wave w's load i writes units 512 i + 64 w + lane, lane l's 16 bytes
+    // at the LDS address in m0 plus 16 l), so no register holds them and no LDS store moves them.
+    // Inline asm: for an LDS load it tracks, the compiler makes every later barrier wait for all
+    // loads; these are waited for explicitly before the barrier that publishes their slots.
+    constexpr bool DMA = !DIRECT;
+    const uint32_t dma_voff = 16 * tid;  // the lane's bytes from a tile's start (unit tid)
+    const uint32_t dma_lds = (uint32_t)(uintptr_t)(lds_void *)&ring[0][0][0] + 1024 * __builtin_amdgcn_readfirstlane(wave);
+    auto dma_tile = [&](int t, int sl) {  // tile t into ring slot sl (wave-uniform)
+        const _Float16 *const src = skv + (size_t)t * (PF_TILE_UNITS * 8);
+#pragma unroll
+        for (int i = 0; i < PF_UNITS_PER_THREAD; i++)
+            asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(
+                             dma_lds + (uint32_t)(sl * PF_TILE_UNITS * 16 + PF_THREADS * 16 * i)),
+                         "v"(dma_voff), "s"(src + PF_THREADS * 8 * i)
+                         : "m0");
+    };
     PfTile R0, R1, R2, R3;
-    gload(R0, t_lo);
-    if (t_lo + 1 <= t_hi) gload(R1, t_lo + 1);
-    if (t_lo + 2 <= t_hi) gload(R2, t_lo + 2);
-    if (t_lo + 3 <= t_hi) gload(R3, t_lo + 3);
+    if constexpr (DMA) {  // the first four tiles into slots 0..3 (waited for before the loop)
+        dma_tile(t_lo, 0);
+        if (t_lo + 1 <= t_hi) dma_tile(t_lo + 1, 1);
+        if (t_lo + 2 <= t_hi) dma_tile(t_lo + 2, 2);
+        if (t_lo + 3 <= t_hi) dma_tile(t_lo + 3, 3);
+    } else {
+        gload(R0, t_lo);
+        if (t_lo + 1 <= t_hi) gload(R1, t_lo + 1);
+        if (t_lo + 2 <= t_hi) gload(R2, t_lo + 2);
+        if (t_lo + 3 <= t_hi) gload(R3, t_lo + 3);
+    }
 
     // After the RMSNorm |q| <= sqrt(128) |gain|, and the scale log2(e)/sqrt(128) follows: q
     // gains that could take q past f16's range, or keep it below 2^-6, make q be stored scaled
@@ -628,6 +652,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const Pref
         //      (no margin), and acc accumulates p V' 2^(eV_t - E) with E the largest V exponent
         //      so far (acc is rescaled when it grows). ----
         const int *te = P.texp + (size_t)kvh * (P.k_rows >> 5);
+        if (DMA) wait_vmcnt<0>();  // the first four tiles have landed in the ring (unused here)
         for (int t = t_lo; t <= t_hi; t++) {
             __syncthreads();  // every wave is done with the previous tile's LDS
             {
@@ -685,27 +710,14 @@ __global__ __launch_bounds__(PF_THREADS, 1) void flash_prefill_kernel(const Pref
     //      A pair reads tiles t + 1 .. t + 3 (stored before the previous barrier) and
     //      writes tiles t + 4, t + 5 into the two ring slots whose tiles were last read in
     //      the previous pair, so five slots never conflict. ----
-    // Without DIRECT, the loop's tiles go straight from memory into their ring slots
-    // (global_load_lds_dwordx4: wave w's load i writes units 512 i + 64 w + lane, lane l's 16 bytes
-    // at the LDS address in m0 plus 16 l), so no register holds them and no LDS store moves them.
-    // Inline asm: for an LDS load it tracks, the compiler makes every later barrier wait for all
-    // loads; these are waited for explicitly before the barrier that publishes their slots.
-    constexpr bool DMA = !DIRECT;
-    const uint32_t dma_voff = 16 * tid;  // the lane's bytes from a tile's start (unit tid)
-    const uint32_t dma_lds = (uint32_t)(uintptr_t)(lds_void *)&ring[0][0][0] + 1024 * __builtin_amdgcn_readfirstlane(wave);
-    auto dma_tile = [&](int t, int sl) {  // tile t into ring slot sl (wave-uniform)
-        const _Float16 *const src = skv + (size_t)t * (PF_TILE_UNITS * 8);
-#pragma unroll
-        for (int i = 0; i < PF_UNITS_PER_THREAD; i++)
-            asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(
-                             dma_lds + (uint32_t)(sl * PF_TILE_UNITS * 16 + PF_THREADS * 16 * i)),
-                         "v"(dma_voff), "s"(src + PF_THREADS * 8 * i)
-                         : "m0");
-    };
-    pf_lstore(R0, ring[0], tid);
-    if (t_lo + 1 <= t_hi) pf_lstore(R1, ring[1], tid);
-    if (t_lo + 2 <= t_hi) pf_lstore(R2, ring[2], tid);
-    if (t_lo + 3 <= t_hi) pf_lstore(R3, ring[3], tid);
+    if constexpr (DMA) {
+        wait_vmcnt<0>();  // this wave's part of the first four tiles is in slots 0..3
+    } else {
+        pf_lstore(R0, ring[0], tid);
+        if (t_lo + 1 <= t_hi) pf_lstore(R1, ring[1], tid);
+        if (t_lo + 2 <= t_hi) pf_lstore(R2, ring[2], tid);
+        if (t_lo + 3 <= t_hi) pf_lstore(R3, ring[3], tid);
+    }
     PfTile R;
     if (!DMA && t_lo + 4 <= t_hi) gload(R, t_lo + 4);
     __syncthreads();
