@@ -43,7 +43,7 @@ DECODE_TRAFFIC_BYTES = 68866200
 # HBM bytes per prefill call (kv_prep_kernel + flash_prefill_kernel) at T = 4000, bf16 KV, from
 # rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs of `bench.py --only prefill_full|prefill_swa
 # --no-cpu`, scaled like the decode figure (profiles/prefill_4000_bf16.md); None = not measured.
-PREFILL_TRAFFIC_BYTES = {"full": 184852270, "swa": 169538012}
+PREFILL_TRAFFIC_BYTES = {"full": 184807293, "swa": 169446994}
 # Flint's 49 layers: full attention (no RoPE) at layers 0, 48 and i % 4 == 1, SWA + RoPE elsewhere
 # (/root/reference/src/metal/flint_config.h:37-38): 14 full, 35 SWA
 FLINT_FULL_LAYERS = [i == 0 or i == 48 or i % 4 == 1 for i in range(49)]
